@@ -1,0 +1,196 @@
+// Table build, tile decode, 128-point transforms, router top-k, row grouping.
+#pragma once
+
+#include "codec.hpp"
+
+namespace esc {
+
+// ---------------------------------------------------------------- table
+__global__ __launch_bounds__(256) void k_lut_init() {
+  uint32_t s = blockIdx.x * 256u + threadIdx.x;
+  g_lut[s] = decode_hash_bits(s);
+}
+
+// ---------------------------------------------------------------- decode
+// code [TK][TN][8K] -> w [IC][OC] f16 (escha_mlx/msl.py:183-202, ref.py:126-134).
+// One 256-thread block per tile, one thread per trellis step.
+template <int K, bool LUT>
+__global__ __launch_bounds__(256) void k_decode_tiles(const uint32_t* __restrict__ code, int TN,
+                                                      int OC, uint16_t* __restrict__ w) {
+  const int tile = blockIdx.x;
+  const int kt = tile / TN, nt = tile - kt * TN;
+  const int t = threadIdx.x;
+  const uint32_t* wp = code + (size_t)tile * (8 * K);
+  uint32_t s = step_state<K>([&](int i) { return wp[i]; }, t);
+  uint16_t v = LUT ? g_lut[s] : decode_hash_bits(s);
+  w[(size_t)(16 * kt + step_row(t)) * OC + 16 * nt + step_col(t)] = v;
+}
+
+// ---------------------------------------------------------------- H128
+// One wave owns one 128-block of one row; lane l holds elements 2l and 2l+1.
+// Stage s pairs i with i ^ (1 << s), bit 0 first, (a + b, a - b) in float32
+// (escha_mlx/ref.py:204-218, msl.py:905-913).  Built with -ffp-contract=off.
+__device__ __forceinline__ void h128_wave(float& v0, float& v1) {
+  const int lane = threadIdx.x & 63;
+  {
+    float a = v0, b = v1;
+    v0 = a + b;
+    v1 = a - b;
+  }
+#pragma unroll
+  for (int s = 1; s < 7; ++s) {
+    const int m = 1 << (s - 1);
+    float o0 = __shfl_xor(v0, m);
+    float o1 = __shfl_xor(v1, m);
+    if (lane & m) {
+      v0 = o0 - v0;
+      v1 = o1 - v1;
+    } else {
+      v0 = v0 + o0;
+      v1 = v1 + o1;
+    }
+  }
+}
+
+// xh = f16(H128(f32(rows) * rin) * RS); rin is [E][IC] gathered by row_expert,
+// or [IC] when row_expert is null (escha_mlx/msl.py:875-916, 1029-1047).
+// grid (IC/128, m), block 64.
+__global__ __launch_bounds__(64) void k_input_transform(const uint16_t* __restrict__ rows,
+                                                        const float* __restrict__ rin,
+                                                        const int* __restrict__ row_expert,
+                                                        int IC, float rs,
+                                                        uint16_t* __restrict__ out) {
+  const int blk = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+  const size_t off = (size_t)row * IC + blk * 128 + 2 * lane;
+  const float* r = rin + (row_expert ? (size_t)row_expert[row] * IC : 0) + blk * 128 + 2 * lane;
+  float v0 = (float)__builtin_bit_cast(half_t, rows[off]) * r[0];
+  float v1 = (float)__builtin_bit_cast(half_t, rows[off + 1]) * r[1];
+  h128_wave(v0, v1);
+  out[off] = __builtin_bit_cast(uint16_t, (half_t)(v0 * rs));
+  out[off + 1] = __builtin_bit_cast(uint16_t, (half_t)(v1 * rs));
+}
+
+// y = f16((H128(mid) * RS) * rout) [+ bias, added in f32 after the f16 round]
+// (escha_mlx/msl.py:919-949, 1050-1067; bias per dense.py:358-361).
+__global__ __launch_bounds__(64) void k_output_transform(const float* __restrict__ mid,
+                                                         const float* __restrict__ rout,
+                                                         const int* __restrict__ row_expert,
+                                                         const uint16_t* __restrict__ bias,
+                                                         int OC, float rs,
+                                                         uint16_t* __restrict__ out) {
+  const int blk = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+  const size_t off = (size_t)row * OC + blk * 128 + 2 * lane;
+  const int c = blk * 128 + 2 * lane;
+  const float* r = rout + (row_expert ? (size_t)row_expert[row] * OC : 0) + c;
+  float v0 = mid[off], v1 = mid[off + 1];
+  h128_wave(v0, v1);
+  half_t y0 = (half_t)((v0 * rs) * r[0]);
+  half_t y1 = (half_t)((v1 * rs) * r[1]);
+  if (bias) {
+    y0 = (half_t)((float)y0 + (float)__builtin_bit_cast(half_t, bias[c]));
+    y1 = (half_t)((float)y1 + (float)__builtin_bit_cast(half_t, bias[c + 1]));
+  }
+  out[off] = __builtin_bit_cast(uint16_t, y0);
+  out[off + 1] = __builtin_bit_cast(uint16_t, y1);
+}
+
+// ---------------------------------------------------------------- router
+// logits [T][E] f32 -> ids [T][k] (descending, ties -> lower id), scores [T][k]
+// = softmax over the k selected logits (escha_mlx/ref.py:326-331).
+// One wave per token; E <= 1024 held as 16 values per lane.
+__global__ __launch_bounds__(64) void k_route_topk(const float* __restrict__ logits, int E,
+                                                   int top_k, int* __restrict__ ids,
+                                                   float* __restrict__ scores) {
+  const int tok = blockIdx.x, lane = threadIdx.x;
+  const float* lg = logits + (size_t)tok * E;
+  constexpr int kPer = 16;
+  float v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    int e = lane + 64 * i;
+    v[i] = e < E ? lg[e] : -__builtin_inff();
+  }
+  float top0 = 0.f, sel[32];
+  int selid[32];
+  for (int k = 0; k < top_k; ++k) {
+    // lane-local best (value desc, id asc)
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      int e = lane + 64 * i;
+      if (e < E && (v[i] > bv || (v[i] == bv && e < bi))) {
+        bv = v[i];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      float ov = __shfl_xor(bv, m);
+      int oi = __shfl_xor(bi, m);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    sel[k] = bv;
+    selid[k] = bi;
+    if (k == 0) top0 = bv;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      if (lane + 64 * i == bi) v[i] = -__builtin_inff();
+  }
+  if (lane == 0) {
+    float den = 0.f;
+    float ex[32];
+    for (int k = 0; k < top_k; ++k) {
+      ex[k] = expf(sel[k] - top0);
+      den += ex[k];
+    }
+    for (int k = 0; k < top_k; ++k) {
+      ids[(size_t)tok * top_k + k] = selid[k];
+      scores[(size_t)tok * top_k + k] = ex[k] / den;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- groups
+// Device build_groups (escha_mlx/moe.py:30-78): rows sorted stably by expert,
+// each expert padded to a multiple of R, padding slots = m (zero sink row),
+// groups past the end = expert -1.  Integer only, one block, deterministic.
+// Shared memory holds per-expert counts; E <= 4096.
+__global__ __launch_bounds__(1024) void k_build_groups(const int* __restrict__ row_expert, int m,
+                                                       int E, int R, int n_groups,
+                                                       int* __restrict__ rows_idx,
+                                                       int* __restrict__ group_expert) {
+  __shared__ int s_cnt[4096];
+  __shared__ int s_start[4096];
+  const int tid = threadIdx.x, nt = blockDim.x;
+  for (int e = tid; e < E; e += nt) s_cnt[e] = 0;
+  for (int i = tid; i < n_groups * R; i += nt) rows_idx[i] = m;
+  for (int g = tid; g < n_groups; g += nt) group_expert[g] = -1;
+  __syncthreads();
+  for (int r = tid; r < m; r += nt) atomicAdd(&s_cnt[row_expert[r]], 1);
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int e = 0; e < E; ++e) {
+      s_start[e] = acc;
+      acc += (s_cnt[e] + R - 1) / R * R;
+    }
+  }
+  __syncthreads();
+  // group_expert: every padded group of expert e
+  for (int e = tid; e < E; e += nt) {
+    int ng = (s_cnt[e] + R - 1) / R;
+    for (int g = 0; g < ng; ++g) group_expert[s_start[e] / R + g] = e;
+  }
+  // stable placement: rank of row r among earlier rows with the same expert
+  for (int r = tid; r < m; r += nt) {
+    int e = row_expert[r], rank = 0;
+    for (int q = 0; q < r; ++q) rank += (row_expert[q] == e);
+    rows_idx[s_start[e] + rank] = r;
+  }
+}
+
+}  // namespace esc

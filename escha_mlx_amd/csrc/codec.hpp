@@ -1,0 +1,83 @@
+// escha trellis codec for gfx950: format constants, state windows, lane map,
+// hash / table decode.  Shared by every kernel of libescha_hip.
+//
+// Format (escha_mlx/ref.py:10-11, 37-48, 58-134):
+//   * a projection with IC inputs / OC outputs is code[IC/16][OC/16][8K] uint32
+//     (the int16 export viewed little-endian; MoE stacks prepend E);
+//   * tile (kt, nt) holds W[16kt:16kt+16, 16nt:16nt+16] of W [IC, OC], y = x @ W;
+//   * a tile's 8K words form one circular bitstream of 256K bits, word 0 bit 31
+//     first; trellis step t's 16-bit state is the window of bits
+//     [K(t+1)-16, K(t+1)) mod 256K read MSB-first;
+//   * step t = 8L + j sits at row 2(L&3) + (j&1) + 8((j>>1)&1),
+//     col 2((L>>3) + 4[j>=4]) + ((L>>2)&1) of the tile (ref.py:96-111);
+//   * decode(s): r = ((s * 0xCBAC1FED) & 0x8FFF8FFF) ^ 0x3B603B60,
+//     value = f16(lo16 r) + f16(hi16 r), round-to-nearest-even.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace esc {
+
+constexpr uint32_t kHashMul = 0xCBAC1FEDu;
+constexpr uint32_t kHashMask = 0x8FFF8FFFu;
+constexpr uint32_t kHashXor = 0x3B603B60u;
+// 1/sqrt(128) as the float32 the format pins (escha_mlx/ref.py:30).
+constexpr float kRS = 0.088388347648f;
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- lane map
+// Row / column of trellis step t inside its 16x16 tile.
+__host__ __device__ constexpr int step_row(int t) {
+  return 2 * ((t >> 3) & 3) + ((t & 7) & 1) + 8 * (((t & 7) >> 1) & 1);
+}
+__host__ __device__ constexpr int step_col(int t) {
+  return 2 * (((t >> 3) >> 3) + 4 * ((t & 7) >= 4)) + (((t >> 3) >> 2) & 1);
+}
+
+// ---------------------------------------------------------------- decode
+// The 32-bit hash word whose two f16 halves sum to the decoded weight.
+__device__ __forceinline__ uint32_t hash_word(uint32_t s) {
+  uint32_t x = s * kHashMul;
+  return (x & kHashMask) ^ kHashXor;
+}
+
+__device__ __forceinline__ half_t halves_sum(uint32_t r) {
+  half_t lo = __builtin_bit_cast(half_t, (uint16_t)(r & 0xFFFFu));
+  half_t hi = __builtin_bit_cast(half_t, (uint16_t)(r >> 16));
+  return lo + hi;  // f16 add, RNE (default rounding mode)
+}
+
+__device__ __forceinline__ half_t decode_hash(uint32_t s) {
+  return halves_sum(hash_word(s));
+}
+
+__device__ __forceinline__ uint16_t decode_hash_bits(uint32_t s) {
+  return __builtin_bit_cast(uint16_t, decode_hash(s));
+}
+
+// 16-bit state whose window starts `start` bits into the 64-bit MSB-first
+// funnel {hi, lo}; any 0 <= start <= 48 keeps the window inside the pair.
+__device__ __forceinline__ uint32_t window16(uint32_t hi, uint32_t lo, int start) {
+  uint64_t m = ((uint64_t)hi << 32) | lo;
+  return (uint32_t)(m >> (48 - start)) & 0xFFFFu;
+}
+
+// State of trellis step t of a tile whose words are reachable through `w(i)`.
+template <int K, typename WordFn>
+__device__ __forceinline__ uint32_t step_state(WordFn w, int t) {
+  constexpr int kBits = 256 * K;
+  constexpr int kWords = 8 * K;
+  int start = (K * (t + 1) - 16 + kBits) % kBits;
+  int a = start >> 5;
+  return window16(w(a), w((a + 1) % kWords), start & 31);
+}
+
+// Table decode: 65,536 f16 values, built on the device by the hash itself
+// (bit-identical by construction) and staged through LDS by the kernels that
+// use it.  One copy per device, filled once by esc_init().
+__device__ uint16_t g_lut[65536];
+
+}  // namespace esc

@@ -1,0 +1,402 @@
+// libescha_hip: the C ABI declared in include/escha_hip.h.
+// One translation unit so the device decode table is a single symbol.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/escha_hip.h"
+#include "moe.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define ESC_REQUIRE(cond, ...) \
+  do {                         \
+    if (!(cond)) return fail(ESC_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+int hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(ESC_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return ESC_OK;
+}
+
+int launched(const char* what) { return hip_check(hipGetLastError(), what); }
+
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+constexpr int kMaxDevices = 64;
+std::mutex g_init_mu;
+bool g_lut_ready[kMaxDevices];
+
+int ensure_lut() {
+  int dev = 0;
+  if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return fail(ESC_EINVAL, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  if (g_lut_ready[dev]) return ESC_OK;
+  hipLaunchKernelGGL(esc::k_lut_init, dim3(256), dim3(256), 0, 0);
+  if (int rc = launched("k_lut_init")) return rc;
+  if (int rc = hip_check(hipDeviceSynchronize(), "esc_init sync")) return rc;
+  g_lut_ready[dev] = true;
+  return ESC_OK;
+}
+
+int check_proj(int K, int IC, int OC) {
+  ESC_REQUIRE(K == 2 || K == 3, "escha code implies K=%d; this runtime implements K in [2, 3]", K);
+  ESC_REQUIRE(IC > 0 && OC > 0 && IC % 128 == 0 && OC % 128 == 0,
+              "escha linear dimensions must be positive multiples of 128, got %dx%d", IC, OC);
+  return ESC_OK;
+}
+
+// ---- dispatch helpers over compile-time parameters
+template <template <int, bool> class F, typename... A>
+int by_k_lut(int K, int lut, A... a) {
+  if (K == 2) return lut ? F<2, true>::run(a...) : F<2, false>::run(a...);
+  return lut ? F<3, true>::run(a...) : F<3, false>::run(a...);
+}
+
+template <int K, bool LUT>
+struct DecodeF {
+  static int run(const uint32_t* code, int IC, int OC, uint16_t* w, hipStream_t s) {
+    const int TK = IC / 16, TN = OC / 16;
+    hipLaunchKernelGGL((esc::k_decode_tiles<K, LUT>), dim3(TK * TN), dim3(256), 0, s, code, TN,
+                       OC, w);
+    return launched("k_decode_tiles");
+  }
+};
+
+template <int K, bool LUT, int MODE>
+struct ExactF {
+  template <int R>
+  static int go(const uint16_t* xh, const uint32_t* code, const int* a, const int* b, int M,
+                int n_groups, int TK, int TN, float* mid, hipStream_t s) {
+    hipLaunchKernelGGL((esc::k_gemm_exact<K, LUT, R, MODE>), dim3(TN / 8, n_groups), dim3(512),
+                       0, s, xh, code, a, b, M, TK, TN, mid);
+    return launched("k_gemm_exact");
+  }
+  static int run(int R, const uint16_t* xh, const uint32_t* code, const int* a, const int* b,
+                 int M, int n_groups, int TK, int TN, float* mid, hipStream_t s) {
+    switch (R) {
+      case 1: return go<1>(xh, code, a, b, M, n_groups, TK, TN, mid, s);
+      case 2: return go<2>(xh, code, a, b, M, n_groups, TK, TN, mid, s);
+      case 3: return go<3>(xh, code, a, b, M, n_groups, TK, TN, mid, s);
+      case 4: return go<4>(xh, code, a, b, M, n_groups, TK, TN, mid, s);
+      case 8: return go<8>(xh, code, a, b, M, n_groups, TK, TN, mid, s);
+      case 12: return go<12>(xh, code, a, b, M, n_groups, TK, TN, mid, s);
+      case 16: return go<16>(xh, code, a, b, M, n_groups, TK, TN, mid, s);
+    }
+    return fail(ESC_EINVAL, "rows per group R=%d not in {1,2,3,4,8,12,16}", R);
+  }
+};
+
+template <int MODE>
+int exact_dispatch(int K, int lut, int R, const uint16_t* xh, const uint32_t* code,
+                   const int* a, const int* b, int M, int n_groups, int TK, int TN, float* mid,
+                   hipStream_t s) {
+  if (K == 2)
+    return lut ? ExactF<2, true, MODE>::run(R, xh, code, a, b, M, n_groups, TK, TN, mid, s)
+               : ExactF<2, false, MODE>::run(R, xh, code, a, b, M, n_groups, TK, TN, mid, s);
+  return lut ? ExactF<3, true, MODE>::run(R, xh, code, a, b, M, n_groups, TK, TN, mid, s)
+             : ExactF<3, false, MODE>::run(R, xh, code, a, b, M, n_groups, TK, TN, mid, s);
+}
+
+template <int K, bool LUT>
+struct ExactOutF {
+  template <int R>
+  static int go(const uint16_t* xh, const uint32_t* code, const float* rout, int M, int TK,
+                int TN, float rs, uint16_t* out, hipStream_t s) {
+    hipLaunchKernelGGL((esc::k_gemm_exact_out<K, LUT, R>), dim3(TN / 8, (M + R - 1) / R),
+                       dim3(512), 0, s, xh, code, rout, M, TK, TN, rs, out);
+    return launched("k_gemm_exact_out");
+  }
+  static int run(int R, const uint16_t* xh, const uint32_t* code, const float* rout, int M,
+                 int TK, int TN, float rs, uint16_t* out, hipStream_t s) {
+    switch (R) {
+      case 1: return go<1>(xh, code, rout, M, TK, TN, rs, out, s);
+      case 2: return go<2>(xh, code, rout, M, TK, TN, rs, out, s);
+      case 4: return go<4>(xh, code, rout, M, TK, TN, rs, out, s);
+      case 8: return go<8>(xh, code, rout, M, TK, TN, rs, out, s);
+    }
+    return fail(ESC_EINVAL, "rows per group R=%d not in {1,2,4,8}", R);
+  }
+};
+
+// ---- split-K GEMV geometry: KS kt per block (multiple of 4, divides TK)
+int fast_splits(int K, int M, int TK, int TN) {
+  const int tpw = K == 2 ? 16 : 8;
+  const int per_split = ((TN + tpw - 1) / tpw) * M;  // blocks per kt split
+  int S = 1;
+  // aim for >= 1024 blocks of 4 waves while keeping >= 4 kt per block
+  while (per_split * S < 1024 && TK % (S * 2 * 4) == 0 && TK / (S * 2) >= 4) S *= 2;
+  return S;
+}
+
+template <int K, bool LUT>
+struct FastF {
+  static int run(const uint16_t* xh, const uint32_t* code, const int* row_expert, int M, int TK,
+                 int TN, int S, float* part, hipStream_t s) {
+    const int tpw = K == 2 ? 16 : 8;
+    hipLaunchKernelGGL((esc::k_gemv_fast<K, LUT>), dim3((TN + tpw - 1) / tpw, M, S), dim3(256), 0, s, xh,
+                       code, row_expert, M, TK, TN, TK / S, part);
+    return launched("k_gemv_fast");
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
+int esc_version(void) { return 100; }
+
+const char* esc_last_error(void) { return g_err.c_str(); }
+
+int esc_init(void) { return ensure_lut(); }
+
+int esc_decode_tiles(const uint32_t* code, int K, int IC, int OC, int use_lut, uint16_t* w,
+                     void* stream) {
+  if (int rc = check_proj(K, IC, OC)) return rc;
+  ESC_REQUIRE(code && w, "null pointer");
+  if (use_lut)
+    if (int rc = ensure_lut()) return rc;
+  return by_k_lut<DecodeF>(K, use_lut, code, IC, OC, w, S(stream));
+}
+
+int esc_input_transform(const uint16_t* rows, const float* rin, const int32_t* row_expert, int m,
+                        int IC, float rs, uint16_t* out, void* stream) {
+  ESC_REQUIRE(rows && rin && out, "null pointer");
+  ESC_REQUIRE(IC > 0 && IC % 128 == 0, "Hadamard dimension must be divisible by 128, got %d", IC);
+  ESC_REQUIRE(m >= 0, "negative row count");
+  if (m == 0) return ESC_OK;
+  hipLaunchKernelGGL(esc::k_input_transform, dim3(IC / 128, m), dim3(64), 0, S(stream), rows,
+                     rin, row_expert, IC, rs, out);
+  return launched("k_input_transform");
+}
+
+int esc_output_transform(const float* mid, const float* rout, const int32_t* row_expert,
+                         const uint16_t* bias, int m, int OC, float rs, uint16_t* out,
+                         void* stream) {
+  ESC_REQUIRE(mid && rout && out, "null pointer");
+  ESC_REQUIRE(OC > 0 && OC % 128 == 0, "Hadamard dimension must be divisible by 128, got %d", OC);
+  ESC_REQUIRE(m >= 0, "negative row count");
+  if (m == 0) return ESC_OK;
+  hipLaunchKernelGGL(esc::k_output_transform, dim3(OC / 128, m), dim3(64), 0, S(stream), mid,
+                     rout, row_expert, bias, OC, rs, out);
+  return launched("k_output_transform");
+}
+
+int esc_gemv(const uint16_t* xh, const uint32_t* code, const int32_t* row_expert, int M, int K,
+             int IC, int OC, int use_lut, float* mid, void* stream) {
+  if (int rc = check_proj(K, IC, OC)) return rc;
+  ESC_REQUIRE(xh && code && mid, "null pointer");
+  ESC_REQUIRE(M >= 0, "negative row count");
+  if (M == 0) return ESC_OK;
+  if (use_lut)
+    if (int rc = ensure_lut()) return rc;
+  return exact_dispatch<esc::kPerRow>(K, use_lut, 1, xh, code, row_expert, nullptr, M, M,
+                                      IC / 16, OC / 16, mid, S(stream));
+}
+
+size_t esc_gemv_fast_workspace(int M, int K, int IC, int OC) {
+  if (check_proj(K, IC, OC) || M <= 0) return 0;
+  return (size_t)fast_splits(K, M, IC / 16, OC / 16) * M * OC * sizeof(float);
+}
+
+int esc_gemv_fast_out(const uint16_t* xh, const uint32_t* code, const int32_t* row_expert,
+                      const float* rout, int M, int K, int IC, int OC, int use_lut, float rs,
+                      uint16_t* out, void* ws, size_t ws_bytes, void* stream) {
+  if (int rc = check_proj(K, IC, OC)) return rc;
+  ESC_REQUIRE(xh && code && rout && out, "null pointer");
+  ESC_REQUIRE(M >= 0, "negative row count");
+  if (M == 0) return ESC_OK;
+  const int TK = IC / 16, TN = OC / 16;
+  const int Sp = fast_splits(K, M, TK, TN);
+  const size_t need = (size_t)Sp * M * OC * sizeof(float);
+  if (!ws || ws_bytes < need)
+    return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, need);
+  if (use_lut)
+    if (int rc = ensure_lut()) return rc;
+  float* part = static_cast<float*>(ws);
+  if (int rc = by_k_lut<FastF>(K, use_lut, xh, code, row_expert, M, TK, TN, Sp, part, S(stream)))
+    return rc;
+  hipLaunchKernelGGL(esc::k_splitk_out, dim3(OC / 128, M), dim3(64), 0, S(stream), part, Sp, M,
+                     OC, rout, row_expert, rs, out);
+  return launched("k_splitk_out");
+}
+
+int esc_gemm_rows(const uint16_t* xh, const uint32_t* code, const int32_t* rows_idx,
+                  const int32_t* group_expert, int n_groups, int R, int n_rows, int K, int IC,
+                  int OC, int use_lut, float* mid, void* stream) {
+  if (int rc = check_proj(K, IC, OC)) return rc;
+  ESC_REQUIRE(xh && code && rows_idx && group_expert && mid, "null pointer");
+  ESC_REQUIRE(n_groups >= 0 && n_rows >= 0, "negative size");
+  if (n_groups == 0) return ESC_OK;
+  if (use_lut)
+    if (int rc = ensure_lut()) return rc;
+  return exact_dispatch<esc::kMoeGroups>(K, use_lut, R, xh, code, rows_idx, group_expert, n_rows,
+                                         n_groups, IC / 16, OC / 16, mid, S(stream));
+}
+
+int esc_dense_gemm_rows(const uint16_t* xh, const uint32_t* code, int M, int R, int K, int IC,
+                        int OC, int use_lut, float* mid, void* stream) {
+  if (int rc = check_proj(K, IC, OC)) return rc;
+  ESC_REQUIRE(xh && code && mid, "null pointer");
+  ESC_REQUIRE(M >= 0, "negative row count");
+  ESC_REQUIRE(R == 1 || R == 2 || R == 4 || R == 8 || R == 16, "dense R=%d not in {1,2,4,8,16}", R);
+  if (M == 0) return ESC_OK;
+  if (use_lut)
+    if (int rc = ensure_lut()) return rc;
+  return exact_dispatch<esc::kDenseRows>(K, use_lut, R, xh, code, nullptr, nullptr, M,
+                                         (M + R - 1) / R, IC / 16, OC / 16, mid, S(stream));
+}
+
+int esc_dense_gemm_rows_out(const uint16_t* xh, const uint32_t* code, const float* rout, int M,
+                            int R, int K, int IC, int OC, int use_lut, float rs, uint16_t* out,
+                            void* stream) {
+  if (int rc = check_proj(K, IC, OC)) return rc;
+  ESC_REQUIRE(xh && code && rout && out, "null pointer");
+  ESC_REQUIRE(M >= 0, "negative row count");
+  if (M == 0) return ESC_OK;
+  if (use_lut)
+    if (int rc = ensure_lut()) return rc;
+  const int TK = IC / 16, TN = OC / 16;
+  hipStream_t s = S(stream);
+  if (K == 2)
+    return use_lut ? ExactOutF<2, true>::run(R, xh, code, rout, M, TK, TN, rs, out, s)
+                   : ExactOutF<2, false>::run(R, xh, code, rout, M, TK, TN, rs, out, s);
+  return use_lut ? ExactOutF<3, true>::run(R, xh, code, rout, M, TK, TN, rs, out, s)
+                 : ExactOutF<3, false>::run(R, xh, code, rout, M, TK, TN, rs, out, s);
+}
+
+int esc_build_groups(const int32_t* row_expert, int m, int E, int R, int n_groups,
+                     int32_t* rows_idx, int32_t* group_expert, void* stream) {
+  ESC_REQUIRE(row_expert && rows_idx && group_expert, "null pointer");
+  ESC_REQUIRE(E > 0 && E <= 4096, "expert count %d not in [1, 4096]", E);
+  ESC_REQUIRE(R >= 1 && m >= 0, "bad R=%d / m=%d", R, m);
+  const long bound = ((long)m + (long)E * (R - 1) + R - 1) / R;
+  ESC_REQUIRE(n_groups >= bound, "n_groups %d below the bound %ld", n_groups, bound);
+  hipLaunchKernelGGL(esc::k_build_groups, dim3(1), dim3(1024), 0, S(stream), row_expert, m, E, R,
+                     n_groups, rows_idx, group_expert);
+  return launched("k_build_groups");
+}
+
+int esc_route_topk(const float* logits, int T, int E, int top_k, int32_t* ids, float* scores,
+                   void* stream) {
+  ESC_REQUIRE(logits && ids && scores, "null pointer");
+  ESC_REQUIRE(E > 0 && E <= 1024, "expert count %d not in [1, 1024]", E);
+  ESC_REQUIRE(top_k >= 1 && top_k <= 32 && top_k <= E, "top_k %d not in [1, min(32, E)]", top_k);
+  ESC_REQUIRE(T >= 0, "negative token count");
+  if (T == 0) return ESC_OK;
+  hipLaunchKernelGGL(esc::k_route_topk, dim3(T), dim3(64), 0, S(stream), logits, E, top_k, ids,
+                     scores);
+  return launched("k_route_topk");
+}
+
+int esc_swiglu(const uint16_t* gu, int m, int I, uint16_t* h, void* stream) {
+  ESC_REQUIRE(gu && h, "null pointer");
+  ESC_REQUIRE(m >= 0 && I > 0, "bad m=%d / I=%d", m, I);
+  if (m == 0) return ESC_OK;
+  hipLaunchKernelGGL(esc::k_swiglu, dim3((I + 255) / 256, m), dim3(256), 0, S(stream), gu, I, h);
+  return launched("k_swiglu");
+}
+
+int esc_moe_combine(const uint16_t* d16, const float* scores, int T, int top_k, int H,
+                    uint16_t* y, void* stream) {
+  ESC_REQUIRE(d16 && scores && y, "null pointer");
+  ESC_REQUIRE(T >= 0 && top_k >= 1 && H > 0, "bad T=%d / top_k=%d / H=%d", T, top_k, H);
+  if (T == 0) return ESC_OK;
+  hipLaunchKernelGGL(esc::k_combine, dim3((H + 255) / 256, T), dim3(256), 0, S(stream), d16,
+                     scores, top_k, H, y);
+  return launched("k_combine");
+}
+
+// ---- routed experts: input transform -> gate_up -> swiglu/transform -> down -> combine
+namespace {
+struct MoePlan {
+  int M, S1, S2;
+  size_t off_xh, off_p1, off_xh2, off_p2, total;
+};
+MoePlan moe_plan(int T, int top_k, int H, int I, int K_gu, int K_dn) {
+  MoePlan p;
+  p.M = T * top_k;
+  p.S1 = fast_splits(K_gu, p.M, H / 16, 2 * I / 16);
+  p.S2 = fast_splits(K_dn, p.M, I / 16, H / 16);
+  auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
+  p.off_xh = 0;
+  p.off_p1 = al(p.off_xh + (size_t)p.M * H * 2);
+  p.off_xh2 = al(p.off_p1 + (size_t)p.S1 * p.M * 2 * I * 4);
+  p.off_p2 = al(p.off_xh2 + (size_t)p.M * I * 2);
+  p.total = al(p.off_p2 + (size_t)p.S2 * p.M * H * 4);
+  return p;
+}
+}  // namespace
+
+size_t esc_moe_expert_path_workspace(int T, int top_k, int E, int H, int I) {
+  (void)E;
+  if (T <= 0 || top_k <= 0 || H <= 0 || I <= 0) return 0;
+  // the plan's sizes depend on K only through the split counts; take the max
+  size_t a = moe_plan(T, top_k, H, I, 2, 2).total, b = moe_plan(T, top_k, H, I, 3, 3).total;
+  size_t c = moe_plan(T, top_k, H, I, 2, 3).total, d = moe_plan(T, top_k, H, I, 3, 2).total;
+  return std::max(std::max(a, b), std::max(c, d));
+}
+
+int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, int T,
+                        int top_k, int E, int H, int I, const uint32_t* gu_code,
+                        const float* gu_rin, const float* gu_rout, int K_gu,
+                        const uint32_t* dn_code, const float* dn_rin, const float* dn_rout,
+                        int K_dn, int use_lut, uint16_t* y, void* ws, size_t ws_bytes,
+                        void* stream) {
+  ESC_REQUIRE(x && ids && scores && gu_code && gu_rin && gu_rout && dn_code && dn_rin && dn_rout &&
+                  y,
+              "null pointer");
+  ESC_REQUIRE(E > 0 && top_k >= 1 && top_k <= E, "bad E=%d / top_k=%d", E, top_k);
+  if (int rc = check_proj(K_gu, H, 2 * I)) return rc;
+  if (int rc = check_proj(K_dn, I, H)) return rc;
+  ESC_REQUIRE(T >= 0, "negative token count");
+  if (T == 0) return ESC_OK;
+  const MoePlan p = moe_plan(T, top_k, H, I, K_gu, K_dn);
+  if (!ws || ws_bytes < p.total)
+    return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, p.total);
+  if (use_lut)
+    if (int rc = ensure_lut()) return rc;
+  char* w = static_cast<char*>(ws);
+  uint16_t* xh = reinterpret_cast<uint16_t*>(w + p.off_xh);
+  float* p1 = reinterpret_cast<float*>(w + p.off_p1);
+  uint16_t* xh2 = reinterpret_cast<uint16_t*>(w + p.off_xh2);
+  float* p2 = reinterpret_cast<float*>(w + p.off_p2);
+  hipStream_t s = S(stream);
+  const float rs = esc::kRS;
+  hipLaunchKernelGGL(esc::k_moe_input, dim3(H / 128, p.M), dim3(64), 0, s, x, ids, top_k, gu_rin,
+                     H, rs, xh);
+  if (int rc = launched("k_moe_input")) return rc;
+  if (int rc = by_k_lut<FastF>(K_gu, use_lut, xh, gu_code, ids, p.M, H / 16, 2 * I / 16, p.S1,
+                               p1, s))
+    return rc;
+  hipLaunchKernelGGL(esc::k_moe_mid, dim3(I / 128, p.M), dim3(64), 0, s, p1, p.S1, p.M, I, ids,
+                     gu_rout, dn_rin, rs, xh2);
+  if (int rc = launched("k_moe_mid")) return rc;
+  if (int rc = by_k_lut<FastF>(K_dn, use_lut, xh2, dn_code, ids, p.M, I / 16, H / 16, p.S2, p2,
+                               s))
+    return rc;
+  hipLaunchKernelGGL(esc::k_moe_combine, dim3(H / 128, T), dim3(64), 0, s, p2, p.S2, p.M, H, ids,
+                     scores, top_k, dn_rout, rs, y);
+  return launched("k_moe_combine");
+}
+
+}  // extern "C"

@@ -1,0 +1,181 @@
+// Split-K coded GEMV for gfx950 (tolerance contract: the float32 sum is
+// reassociated, every decoded weight is still the bit-exact f16 of the format).
+//
+// Wave-step = one kt row of TPW consecutive tiles, which are contiguous in
+// memory (code [kt][nt][8K]), so one coalesced vector load per lane pulls a
+// wave's whole step: K=2 -> 16 B per lane (dwordx4, 4 lanes per 64 B tile,
+// 16 tiles = 1 KiB); K=3 -> 12 B per lane (dwordx3, 8 lanes per 96 B tile,
+// 8 tiles = 768 B).  Lane q of a tile owns the stream bits [q*32*WPL,
+// (q+1)*32*WPL) and therefore the trellis steps whose window ENDS there; the
+// 13-14 bits of history before its first word come from the previous lane of
+// the same tile (circularly) through one cross-lane move.  Every window offset,
+// tile row and output column is then a compile-time function of the step
+// index, so decode + multiply-add fully unroll with the window in VGPRs.
+//
+// Reduction: the 4 waves of a block split the block's kt range; their column
+// sums meet in LDS in a fixed order, and blocks along kt write float32
+// partials [S][M][OC] that the epilogue kernels sum in fixed order: the
+// result is deterministic run to run (no float atomics anywhere).
+#pragma once
+
+#include "exact.hpp"
+
+namespace esc {
+
+template <int K>
+struct Geo;
+template <>
+struct Geo<2> {
+  static constexpr int LPT = 4;   // lanes per tile
+  static constexpr int WPL = 4;   // words per lane
+  static constexpr int SPL = 64;  // trellis steps per lane
+  static constexpr int TPW = 16;  // tiles per wave-step
+  static constexpr int NCOL = 4;  // output columns per lane
+  __device__ static constexpr int col_slot(int u) { return 2 * ((u & 7) >= 4) + ((u >> 5) & 1); }
+  __device__ static int col(int q, int ci) { return 2 * q + (ci & 1) + 8 * (ci >> 1); }
+};
+template <>
+struct Geo<3> {
+  static constexpr int LPT = 8;
+  static constexpr int WPL = 3;
+  static constexpr int SPL = 32;
+  static constexpr int TPW = 8;
+  static constexpr int NCOL = 2;
+  __device__ static constexpr int col_slot(int u) { return (u & 7) >= 4; }
+  __device__ static int col(int q, int ci) { return q + 8 * ci; }
+};
+
+// Input-channel row (0..15) of the lane's step u (same for K=2 and K=3).
+__device__ constexpr int fast_row(int u) {
+  return 2 * ((u >> 3) & 3) + (u & 1) + 8 * ((u >> 1) & 1);
+}
+
+template <int K>
+struct LaneWords {
+  uint32_t w[Geo<K>::WPL];
+};
+
+template <int K>
+__device__ __forceinline__ LaneWords<K> load_lane_words(const uint32_t* p) {
+  LaneWords<K> r;
+  if constexpr (K == 2) {
+    uint4 v = *reinterpret_cast<const uint4*>(p);
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+    r.w[2] = v.z;
+    r.w[3] = v.w;
+  } else {
+    r.w[0] = p[0];
+    r.w[1] = p[1];
+    r.w[2] = p[2];
+  }
+  return r;
+}
+
+// Decode the lane's SPL steps of one tile and accumulate x * w into acc[NCOL].
+// xw: the 16 f16 inputs of this kt packed two per word (row r in half r&1 of
+// word r>>1).  wprev: the previous lane's last word.
+template <int K, bool LUT>
+__device__ __forceinline__ void fast_tile(const LaneWords<K>& lw, uint32_t wprev,
+                                          const uint32_t* xw, const uint16_t* lut, float* acc) {
+  using G = Geo<K>;
+#pragma unroll
+  for (int u = 0; u < G::SPL; ++u) {
+    const int rel = K * (u + 1) - 16;             // window start, bits from the lane's first bit
+    const int a = (rel + 32) / 32 - 1;            // word holding the first bit (-1: previous lane)
+    const int off = rel - 32 * a;
+    const uint32_t hi = a < 0 ? wprev : lw.w[a];
+    const uint32_t lo = (a + 1 < G::WPL) ? lw.w[a + 1] : 0u;
+    const uint32_t s = window16(hi, lo, off);
+    half_t wv;
+    if constexpr (LUT)
+      wv = __builtin_bit_cast(half_t, lut[s]);
+    else
+      wv = decode_hash(s);
+    const int r = fast_row(u);
+    const half_t xv = __builtin_bit_cast(half_t, (uint16_t)(xw[r >> 1] >> (16 * (r & 1))));
+    const int ci = G::col_slot(u);
+    acc[ci] = __builtin_fmaf((float)xv, (float)wv, acc[ci]);
+  }
+}
+
+// Partial GEMV: part[z][row][OC] = sum over the block's kt range.
+// grid (TN/TPW, M, S), block 256; KS = TK/S kt per block, KS % 4 == 0.
+// row_expert null -> dense (single stream).
+template <int K, bool LUT>
+__global__ __launch_bounds__(256) void k_gemv_fast(const uint16_t* __restrict__ xh,
+                                                   const uint32_t* __restrict__ code,
+                                                   const int* __restrict__ row_expert, int M,
+                                                   int TK, int TN, int KS,
+                                                   float* __restrict__ part) {
+  using G = Geo<K>;
+  __shared__ uint16_t s_lut[LUT ? 65536 : 1];
+  __shared__ float s_red[4][64][G::NCOL];
+  stage_lut<LUT>(s_lut);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int ntg = blockIdx.x, row = blockIdx.y, z = blockIdx.z;
+  const int IC = TK * 16, OC = TN * 16;
+  const int e = row_expert ? row_expert[row] : 0;
+  const uint32_t* base = code + (size_t)e * TK * TN * (8 * K);
+  const int q = lane % G::LPT, tile = lane / G::LPT;
+  const int src = tile * G::LPT + (q + G::LPT - 1) % G::LPT;
+  // a partial last tile group (TN not a multiple of TPW): those lanes neither
+  // load nor store
+  const bool valid = ntg * G::TPW + tile < TN;
+  const int KW = KS / 4;
+  const int kt0 = z * KS + wave * KW;
+  const uint32_t* xrow = reinterpret_cast<const uint32_t*>(xh + (size_t)row * IC);
+  float acc[G::NCOL];
+#pragma unroll
+  for (int i = 0; i < G::NCOL; ++i) acc[i] = 0.f;
+  const size_t lane_off = (size_t)ntg * G::TPW * (8 * K) + (size_t)lane * G::WPL;
+  LaneWords<K> zero{};
+  LaneWords<K> cur = valid ? load_lane_words<K>(base + (size_t)kt0 * TN * (8 * K) + lane_off) : zero;
+  for (int k = 0; k < KW; ++k) {
+    const int kt = kt0 + k;
+    LaneWords<K> nxt = cur;
+    if (valid && k + 1 < KW)
+      nxt = load_lane_words<K>(base + (size_t)(kt + 1) * TN * (8 * K) + lane_off);
+    uint32_t xw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xw[i] = xrow[8 * kt + i];
+    const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
+    fast_tile<K, LUT>(cur, wprev, xw, s_lut, acc);
+    cur = nxt;
+  }
+#pragma unroll
+  for (int i = 0; i < G::NCOL; ++i) s_red[wave][lane][i] = acc[i];
+  __syncthreads();
+  if (wave == 0 && valid) {
+    float* pr = part + ((size_t)z * M + row) * OC + (size_t)(ntg * G::TPW + tile) * 16;
+#pragma unroll
+    for (int i = 0; i < G::NCOL; ++i) {
+      float v = s_red[0][lane][i];
+      v = v + s_red[1][lane][i];
+      v = v + s_red[2][lane][i];
+      v = v + s_red[3][lane][i];
+      pr[G::col(q, i)] = v;
+    }
+  }
+}
+
+// out[row] = f16((H128(sum_z part[z][row]) * RS) * rout[e]); grid (OC/128, M), block 64.
+__global__ __launch_bounds__(64) void k_splitk_out(const float* __restrict__ part, int S, int M,
+                                                   int OC, const float* __restrict__ rout,
+                                                   const int* __restrict__ row_expert, float rs,
+                                                   uint16_t* __restrict__ out) {
+  const int blk = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+  const int c = blk * 128 + 2 * lane;
+  float v0 = 0.f, v1 = 0.f;
+  for (int z = 0; z < S; ++z) {
+    const float* p = part + ((size_t)z * M + row) * OC + c;
+    v0 = v0 + p[0];
+    v1 = v1 + p[1];
+  }
+  h128_wave(v0, v1);
+  const float* r = rout + (row_expert ? (size_t)row_expert[row] * OC : 0) + c;
+  out[(size_t)row * OC + c] = __builtin_bit_cast(uint16_t, (half_t)((v0 * rs) * r[0]));
+  out[(size_t)row * OC + c + 1] = __builtin_bit_cast(uint16_t, (half_t)((v1 * rs) * r[1]));
+}
+
+}  // namespace esc

@@ -1,0 +1,193 @@
+"""Dense coded linear: the escha_mlx.dense call surface on the HIP engine.
+
+``EschaWeight`` / ``EschaLinear`` / ``build`` / ``pack_code`` /
+``coded_bytes`` keep the reference's constructor inputs, validation and
+forward contract (escha_mlx/dense.py:145-483):
+
+    xh  = f16( H128(x * rin) * RS )
+    mid = xh @ decode(code)                       (f32)
+    y   = f16( H128(mid) * RS * rout ) [+ bias]
+
+with rin/rout the folded vectors (rin*s_in, rout*s_out in float32,
+escha_mlx/ref.py:242-277).  Kernel choice by row count follows
+EschaLinear._gemv (dense.py:300-335): M=1 -> GEMV, R = dense_block_r(M)
+rows share one decode, R <= 8 with the output transform fused.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import envs, ops
+
+RS = ops.RS
+SUPPORTED_K = frozenset({2, 3})
+_CONFIG_LEN = 6
+_PRODUCTION_CODEBOOK = 1
+DENSE_R_MAX = 16
+
+
+def _check_scale(name: str, vec, expect: int) -> None:
+    if vec is None:
+        return
+    shape = tuple(np.shape(vec))
+    if shape != (expect,):
+        raise ValueError(f"{name} must have shape ({expect},), got {shape}")
+
+
+def pack_code(code_i16: np.ndarray, device="cuda") -> torch.Tensor:
+    """int16 [TK, TN, 16K] -> int32 words [TK, TN, 8K] on the device (dense.py:145-155)."""
+    return ops.to_device_code(code_i16, device)
+
+
+def fold_scales(rin, rout, s_in=None, s_out=None):
+    """float32 products rin*s_in, rout*s_out (escha_mlx/ref.py:242-277)."""
+    ri = np.asarray(rin).astype(np.float32)
+    ro = np.asarray(rout).astype(np.float32)
+    if s_in is not None:
+        ri = ri * np.asarray(s_in).astype(np.float32)
+    if s_out is not None:
+        ro = ro * np.asarray(s_out).astype(np.float32)
+    return ri, ro
+
+
+def apply_bias() -> bool:
+    """ESCHA_MLX_BIAS=1 applies the exported correction (default off, dense.py:107-132)."""
+    v = __import__("os").environ.get("ESCHA_MLX_BIAS", "0")
+    if v not in ("0", "1", ""):
+        raise ValueError(f"ESCHA_MLX_BIAS must be 0 or 1, got {v!r}")
+    return v == "1"
+
+
+def dense_block_r(m: int, pin: int | None = None) -> int:
+    """Rows per group: min(m, 16) snapped down to a power of two (msl.py:1562-1601)."""
+    if pin is not None:
+        return pin
+    r = min(m, DENSE_R_MAX)
+    while r & (r - 1):
+        r &= r - 1
+    return max(1, r)
+
+
+class EschaWeight:
+    """One dense linear's coded stream and folded transform vectors (dense.py:158-265)."""
+
+    def __init__(self, code, rin, rout, s_in=None, s_out=None, config=None, device="cuda"):
+        if isinstance(code, torch.Tensor):
+            tk, tn, wpt = code.shape
+            if wpt % 8:
+                raise ValueError(f"packed escha code last dim must be 8*K, got {wpt}")
+            self.K = wpt // 8
+            code_dev = code.to(device)
+        else:
+            tk, tn, wpt2 = np.shape(code)
+            if wpt2 % 16:
+                raise ValueError(f"escha code last dim must be 16*K, got {wpt2}")
+            self.K = wpt2 // 16
+            code_dev = None
+        if self.K not in SUPPORTED_K:
+            raise ValueError(f"escha code implies K={self.K}; this runtime implements "
+                             f"K in {sorted(SUPPORTED_K)}")
+        self.IC, self.OC = tk * 16, tn * 16
+        if np.shape(rin) != (self.IC,) or np.shape(rout) != (self.OC,):
+            raise ValueError(
+                f"transform vectors {np.shape(rin)}/{np.shape(rout)} do not match the code "
+                f"stream's {self.IC}x{self.OC}; both must be 1-D ({self.IC},)/({self.OC},)")
+        if self.IC % 128 or self.OC % 128:
+            raise ValueError(f"escha linear dimensions must be multiples of 128, got "
+                             f"{self.IC}x{self.OC}")
+        if config is not None:
+            cfg = [int(v) for v in np.asarray(config).ravel()]
+            if len(cfg) != _CONFIG_LEN:
+                raise ValueError(f"escha_config has {len(cfg)} fields, expected {_CONFIG_LEN} "
+                                 "([L, K, V, codebook_id, in_features, out_features])")
+            _, k_cfg, _, cb, ic_cfg, oc_cfg = cfg
+            if (k_cfg, ic_cfg, oc_cfg) != (self.K, self.IC, self.OC):
+                raise ValueError(f"escha_config {(k_cfg, ic_cfg, oc_cfg)} disagrees with the "
+                                 f"code stream {(self.K, self.IC, self.OC)}")
+            if cb != _PRODUCTION_CODEBOOK:
+                raise ValueError(f"escha_config selects codebook id {cb}; this runtime "
+                                 f"implements the production codebook (id {_PRODUCTION_CODEBOOK}) only")
+        _check_scale("escha_s_in", s_in, self.IC)
+        _check_scale("escha_s_out", s_out, self.OC)
+        self.code = code_dev if code_dev is not None else pack_code(np.asarray(code), device)
+        ri, ro = fold_scales(rin, rout, s_in, s_out)
+        self.rin = torch.from_numpy(ri).to(device)
+        self.rout = torch.from_numpy(ro).to(device)
+
+    def arrays(self) -> list[torch.Tensor]:
+        return [self.code, self.rin, self.rout]
+
+
+class EschaLinear(torch.nn.Module):
+    """A trellis-coded dense linear, drop-in for nn.Linear (dense.py:268-362)."""
+
+    def __init__(self, w: EschaWeight, bias=None) -> None:
+        super().__init__()
+        self._w = w
+        self.bias = None if bias is None else torch.as_tensor(
+            np.asarray(bias, dtype=np.float16)).to(w.code.device)
+        # latched at construction, like the reference (dense.py:278-281)
+        self._lut = envs.use_lut()
+        self._exact = envs.use_exact()
+        self._block_r_pin = envs.dense_block_r_pin()
+
+    @property
+    def K(self) -> int:
+        return self._w.K
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        w = self._w
+        shape = x.shape
+        rows = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
+        m = rows.shape[0]
+        xh = ops.scaled_had(rows, w.rin, None)
+        r = dense_block_r(m, self._block_r_pin)
+        if m > 1 and r <= 8:
+            y = ops.dense_gemm_rows_direct_out(xh, w.code, w.rout, w.K, w.IC, w.OC, r,
+                                               lut=self._lut)
+        elif r > 1:
+            y = ops.scaled_had_out(ops.dense_gemm_rows(xh, w.code, w.K, w.IC, w.OC, r,
+                                                       lut=self._lut), w.rout, None)
+        elif self._exact:
+            y = ops.scaled_had_out(ops.dense_gemv(xh, w.code, w.K, w.IC, w.OC, lut=self._lut),
+                                   w.rout, None)
+        else:
+            y = ops.gemv_fast_out(xh, w.code, None, w.rout, w.K, w.IC, w.OC, lut=self._lut)
+        if self.bias is not None:
+            y = (y.float() + self.bias.float()).to(torch.float16)
+        return y.reshape(*shape[:-1], w.OC).to(x.dtype)
+
+
+def build(group: dict, device="cuda") -> EschaLinear:
+    """Assemble one linear from its tensors keyed by HF leaf name (dense.py:440-452)."""
+    w = EschaWeight(group["escha_code"], group["escha_rin"], group["escha_rout"],
+                    group.get("escha_s_in"), group.get("escha_s_out"), group.get("escha_config"),
+                    device=device)
+    bias = group.get("bias") if apply_bias() else None
+    return EschaLinear(w, bias)
+
+
+def coded_bytes(obj) -> int:
+    """Bytes of every coded stream under obj (dense.py:455-483)."""
+    total, stack, seen = 0, [obj], set()
+    while stack:
+        node = stack.pop()
+        if id(node) in seen:
+            continue
+        seen.add(id(node))
+        if isinstance(node, EschaLinear):
+            total += sum(a.numel() * a.element_size() for a in node._w.arrays())
+            continue
+        if isinstance(node, torch.nn.Module):
+            stack.extend(node.children())
+        elif isinstance(node, dict):
+            stack.extend(node.values())
+        elif isinstance(node, (list, tuple)):
+            stack.extend(node)
+    return total
+
+
+LEAVES = frozenset({"escha_code", "escha_rin", "escha_rout", "escha_s_in", "escha_s_out",
+                    "escha_config", "bias"})
+REQUIRED = frozenset({"escha_code", "escha_rin", "escha_rout"})

@@ -1,0 +1,151 @@
+"""Routed-expert toolkit: the escha_mlx.moe call surface plus the expert path.
+
+``EschaExperts`` (E-stacked coded projection), ``build_groups``,
+``n_groups_bound`` follow escha_mlx/moe.py:30-105.  ``EschaMoEExperts`` is the
+routed part of EschaSparseMoeBlock (escha_mlx/models/qwen3_5_moe.py:97-253):
+token-major rows, gate_up leg, swiglu, down leg, f16(score)-weighted
+slot-order combine, rounded to f16.  ``route`` is its router step on given
+float32 logits (models/qwen3_5_moe.py:257-263, in ref.moe_block's stable
+order, escha_mlx/ref.py:326-331).
+
+Two execution paths with the same rounding points:
+  * fused (default) — ``esc_moe_expert_path``: decode fused into split-K
+    GEMVs, transforms / swiglu / combine fused into their epilogues; GEMV
+    sums reassociated (tolerance contract), decode bit-exact.
+  * exact (ESCHA_HIP_EXACT=1) — the reference kernel chain with the
+    reference accumulation order (bit-reproducible against the oracle),
+    row-blocked by the reference's R policy.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import envs, ops
+
+RS = ops.RS
+
+
+def n_groups_bound(m: int, E: int, R: int) -> int:
+    """Static upper bound on groups: every expert may waste up to R-1 slots (moe.py:81-83)."""
+    return (m + E * (R - 1) + R - 1) // R
+
+
+def build_groups(row_expert: torch.Tensor, E: int, R: int, n_groups: int):
+    """Rows sorted by expert into R-row groups, on the device (moe.py:30-78)."""
+    return ops.build_groups(row_expert.to(torch.int32).contiguous(), E, R, n_groups)
+
+
+class EschaExperts:
+    """One projection's E-stacked arrays (moe.py:86-105): code [E, TK, TN, 8K]
+    words (int32 storage), rin [E, IC] f32, rout [E, OC] f32."""
+
+    def __init__(self, code_i16: np.ndarray, rin: np.ndarray, rout: np.ndarray,
+                 device="cuda") -> None:
+        if code_i16.ndim != 4:
+            raise ValueError(f"expert code must be [E, TK, TN, 16K], got {code_i16.shape}")
+        e, tk, tn, wpt2 = code_i16.shape
+        if wpt2 % 16 or wpt2 // 16 not in (2, 3):
+            raise ValueError(f"escha code last dim {wpt2} implies an unsupported K")
+        self.K = wpt2 // 16
+        self.E, self.IC, self.OC = e, tk * 16, tn * 16
+        if self.IC % 128 or self.OC % 128:
+            raise ValueError(f"expert dimensions must be multiples of 128, got {self.IC}x{self.OC}")
+        if np.shape(rin) != (e, self.IC) or np.shape(rout) != (e, self.OC):
+            raise ValueError("rin/rout must be [E, IC] / [E, OC]")
+        self.code = ops.to_device_code(code_i16, device)
+        self.rin = torch.from_numpy(np.asarray(rin).astype(np.float32)).to(device)
+        self.rout = torch.from_numpy(np.asarray(rout).astype(np.float32)).to(device)
+
+    @classmethod
+    def from_device(cls, code: torch.Tensor, rin: torch.Tensor, rout: torch.Tensor, K: int):
+        self = cls.__new__(cls)
+        self.K = K
+        self.E, tk, tn, _ = code.shape
+        self.IC, self.OC = tk * 16, tn * 16
+        self.code, self.rin, self.rout = code, rin, rout
+        return self
+
+    def arrays(self) -> list[torch.Tensor]:
+        return [self.code, self.rin, self.rout]
+
+
+def route(logits: torch.Tensor, top_k: int):
+    """float32 logits [T, E] -> (ids [T, k] int32, scores [T, k] float32)."""
+    return ops.route_topk(logits.to(torch.float32).contiguous(), top_k)
+
+
+def blocked_R(m: int, pin: int | None = None) -> int:
+    """Rows per expert group for the row-blocked GEMM, 1 = per-row GEMV
+    (models/qwen3_5_moe.py:124-170)."""
+    if pin is not None:
+        return pin
+    if m >= 2048:
+        return 12
+    if m >= 1024:
+        return 4
+    if m >= 320:
+        return 3
+    if m >= 128:
+        return 2
+    return 1
+
+
+class EschaMoEExperts(torch.nn.Module):
+    """Routed experts of one MoE layer: forward(x [T, H] f16, ids [T, k], scores [T, k])
+    -> routed sum f16 [T, H] (models/qwen3_5_moe.py:207-253)."""
+
+    def __init__(self, gu: EschaExperts, dn: EschaExperts, num_experts: int, top_k: int) -> None:
+        super().__init__()
+        if gu.OC != 2 * dn.IC or dn.OC != gu.IC:
+            raise ValueError("gate_up [H -> 2I] and down [I -> H] shapes disagree")
+        self._gu, self._dn = gu, dn
+        self.num_experts, self.top_k = num_experts, top_k
+        self._inter = dn.IC
+        self._lut = envs.use_lut()
+        self._exact = envs.use_exact()
+        self._block_r = envs.block_r_pin()
+        self._ws = None
+
+    def _rows(self, t: int, ids: torch.Tensor):
+        """Token-major rows: slot s of token t is row t*k + s (qwen3_5_moe.py:97-101)."""
+        row_expert = ids.reshape(t * self.top_k).to(torch.int32).contiguous()
+        row_token = torch.arange(t, device=ids.device, dtype=torch.int64).repeat_interleave(self.top_k)
+        return row_expert, row_token
+
+    def _gemv(self, xh, row_expert, ex: EschaExperts):
+        m = xh.shape[0]
+        r = blocked_R(m, self._block_r)
+        if r == 1:
+            return ops.moe_gemv(xh, ex.code, row_expert, ex.K, ex.IC, ex.OC, lut=self._lut)
+        ng = n_groups_bound(m, self.num_experts, r)
+        rows_idx, group_expert = build_groups(row_expert, self.num_experts, r, ng)
+        xh_pad = torch.cat([xh, torch.zeros((1, xh.shape[1]), dtype=xh.dtype, device=xh.device)])
+        mid = ops.moe_gemm_rows(xh_pad, ex.code, rows_idx, group_expert, ex.K, ex.IC, ex.OC, r,
+                                m, lut=self._lut)
+        return mid[:m].contiguous()
+
+    def _forward_exact(self, x, ids, scores):
+        t = x.shape[0]
+        row_expert, row_token = self._rows(t, ids)
+        gu, dn = self._gu, self._dn
+        xh = ops.scaled_had(x[row_token].contiguous(), gu.rin, row_expert)
+        gu16 = ops.scaled_had_out(self._gemv(xh, row_expert, gu), gu.rout, row_expert)
+        h = ops.swiglu(gu16)
+        xh2 = ops.scaled_had(h, dn.rin, row_expert)
+        d16 = ops.scaled_had_out(self._gemv(xh2, row_expert, dn), dn.rout, row_expert)
+        return ops.moe_combine(d16, scores.reshape(-1).contiguous(), self.top_k)
+
+    def forward(self, x: torch.Tensor, ids: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
+        x = x.to(torch.float16).contiguous()
+        ids = ids.to(torch.int32).contiguous()
+        scores = scores.to(torch.float32).contiguous()
+        if self._exact:
+            return self._forward_exact(x, ids, scores)
+        t, h = x.shape
+        need = ops.moe_expert_path_workspace(t, self.top_k, self.num_experts, h, self._inter)
+        if self._ws is None or self._ws.numel() < need or self._ws.device != x.device:
+            self._ws = torch.empty(max(need, 4), dtype=torch.uint8, device=x.device)
+        gu, dn = self._gu, self._dn
+        return ops.moe_expert_path(x, ids, scores, gu.code, gu.rin, gu.rout, gu.K, dn.code,
+                                   dn.rin, dn.rout, dn.K, lut=self._lut, ws=self._ws)

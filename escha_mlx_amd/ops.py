@@ -1,0 +1,269 @@
+"""Kernel entry points over torch tensors — the escha_mlx.msl call surface.
+
+Same names, argument meaning and result shapes as the reference's kernel
+wrappers (escha_mlx/msl.py); tensors are device tensors on a ROCm GPU and
+every call enqueues on torch's current stream.  Code streams are the export's
+int16 data viewed as little-endian uint32 words, held in torch as int32
+(``code_to_u32``); f16 activations are torch.float16.
+
+Errors: shape / K / row-count preconditions raise ValueError (as the
+reference does, escha_mlx/dense.py:170-242, msl.py:1794-1823); a HIP failure
+raises EschaHipError.  There is no CPU path: a tensor not on the GPU is an
+error.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib, envs
+
+RS = 0.088388347648  # 1/sqrt(128) as pinned by the format (escha_mlx/ref.py:30)
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(*ts: torch.Tensor | None) -> None:
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("escha_mlx_amd kernels take GPU tensors (no CPU path)")
+        if not t.is_contiguous():
+            raise ValueError("escha_mlx_amd kernels take contiguous tensors")
+
+
+def _as_u32(code: torch.Tensor) -> torch.Tensor:
+    if code.dtype not in (torch.int32, torch.uint32):
+        raise ValueError(f"packed code must be 32-bit words, got {code.dtype}")
+    return code
+
+
+def _lut_flag(lut: bool | None) -> int:
+    return int(envs.use_lut() if lut is None else lut)
+
+
+def code_to_u32(code_i16: np.ndarray) -> np.ndarray:
+    """View an int16 code tensor [..., 16K] as little-endian uint32 [..., 8K]
+    (escha_mlx/msl.py:1398-1401)."""
+    a = np.ascontiguousarray(code_i16).view(np.uint16).astype(np.uint32)
+    return (a[..., 0::2] | (a[..., 1::2] << np.uint32(16))).astype(np.uint32)
+
+
+def to_device_code(code: np.ndarray, device="cuda") -> torch.Tensor:
+    """int16 [..., 16K] export (or uint32 [..., 8K]) -> int32 device words."""
+    u = code if code.dtype == np.uint32 else code_to_u32(code)
+    return torch.from_numpy(np.ascontiguousarray(u).view(np.int32)).to(device)
+
+
+def init() -> None:
+    """Build the decode table on the current device (needed before graph capture)."""
+    _lib.call("esc_init")
+
+
+def decode_tiles(code_u32: torch.Tensor, K: int, IC: int, OC: int,
+                 lut: bool | None = None) -> torch.Tensor:
+    """One projection's packed stream -> f16 bare weight [IC, OC] (msl.py:1404-1421)."""
+    _dev(code_u32)
+    code_u32 = _as_u32(code_u32)
+    if code_u32.numel() != (IC // 16) * (OC // 16) * 8 * K:
+        raise ValueError(f"code has {code_u32.numel()} words, expected a {IC}x{OC} K={K} stream")
+    w = torch.empty((IC, OC), dtype=torch.float16, device=code_u32.device)
+    _lib.call("esc_decode_tiles", _ptr(code_u32), K, IC, OC, _lut_flag(lut), _ptr(w), _stream())
+    return w
+
+
+def scaled_had(rows: torch.Tensor, rin: torch.Tensor, row_expert: torch.Tensor | None,
+               rs: float = RS) -> torch.Tensor:
+    """rows [m, IC] f16, rin [E, IC] f32 (or [IC] with row_expert None) -> [m, IC] f16
+    (msl.py:1029-1047, dense variant msl.py:1481-1483)."""
+    _dev(rows, rin, row_expert)
+    m, ic = rows.shape
+    _check_rows(rows, torch.float16, rin, row_expert, m, ic)
+    out = torch.empty_like(rows)
+    _lib.call("esc_input_transform", _ptr(rows), _ptr(rin), _ptr(row_expert), m, ic, rs,
+              _ptr(out), _stream())
+    return out
+
+
+def scaled_had_out(mid: torch.Tensor, rout: torch.Tensor, row_expert: torch.Tensor | None,
+                   rs: float = RS, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """mid [m, OC] f32, rout [E, OC] f32 (or [OC]) -> f16 [m, OC] (msl.py:1050-1067)."""
+    _dev(mid, rout, row_expert, bias)
+    m, oc = mid.shape
+    _check_rows(mid, torch.float32, rout, row_expert, m, oc)
+    out = torch.empty((m, oc), dtype=torch.float16, device=mid.device)
+    _lib.call("esc_output_transform", _ptr(mid), _ptr(rout), _ptr(row_expert), _ptr(bias), m, oc,
+              rs, _ptr(out), _stream())
+    return out
+
+
+def _check_rows(x, dtype, vec, row_expert, m, dim):
+    if x.dtype != dtype:
+        raise ValueError(f"expected {dtype}, got {x.dtype}")
+    if vec.dtype != torch.float32:
+        raise ValueError(f"transform vector must be float32, got {vec.dtype}")
+    if row_expert is None:
+        if tuple(vec.shape) != (dim,):
+            raise ValueError(f"dense transform vector must be ({dim},), got {tuple(vec.shape)}")
+    else:
+        if vec.dim() != 2 or vec.shape[1] != dim:
+            raise ValueError(f"expert transform vectors must be [E, {dim}], got {tuple(vec.shape)}")
+        if row_expert.dtype != torch.int32 or tuple(row_expert.shape) != (m,):
+            raise ValueError("row_expert must be int32 [m]")
+
+
+def moe_gemv(xh: torch.Tensor, code_u32: torch.Tensor, row_expert: torch.Tensor | None,
+             K: int, IC: int, OC: int, lut: bool | None = None) -> torch.Tensor:
+    """mid[r] = xh[r] @ decode(code[row_expert[r]]) in the reference kernel order
+    (bit-reproducible; msl.py:1424-1478 with splits=1).  row_expert None = dense."""
+    _dev(xh, code_u32, row_expert)
+    m = xh.shape[0]
+    if xh.dtype != torch.float16 or tuple(xh.shape) != (m, IC):
+        raise ValueError(f"xh must be f16 [m, {IC}]")
+    mid = torch.empty((m, OC), dtype=torch.float32, device=xh.device)
+    _lib.call("esc_gemv", _ptr(xh), _ptr(_as_u32(code_u32)), _ptr(row_expert), m, K, IC, OC,
+              _lut_flag(lut), _ptr(mid), _stream())
+    return mid
+
+
+def dense_gemv(xh, code_u32, K, IC, OC, lut=None):
+    """Dense single-stream GEMV (msl.py:1530-1538)."""
+    return moe_gemv(xh, code_u32, None, K, IC, OC, lut)
+
+
+def gemv_fast_out(xh: torch.Tensor, code_u32: torch.Tensor, row_expert: torch.Tensor | None,
+                  rout: torch.Tensor, K: int, IC: int, OC: int, lut: bool | None = None,
+                  rs: float = RS) -> torch.Tensor:
+    """Split-K GEMV + fused output transform (tolerance contract) -> f16 [m, OC]."""
+    _dev(xh, code_u32, row_expert, rout)
+    m = xh.shape[0]
+    if xh.dtype != torch.float16 or tuple(xh.shape) != (m, IC):
+        raise ValueError(f"xh must be f16 [m, {IC}]")
+    out = torch.empty((m, OC), dtype=torch.float16, device=xh.device)
+    nbytes = _lib.load().esc_gemv_fast_workspace(m, K, IC, OC) if m else 0
+    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=xh.device)
+    _lib.call("esc_gemv_fast_out", _ptr(xh), _ptr(_as_u32(code_u32)), _ptr(row_expert),
+              _ptr(rout), m, K, IC, OC, _lut_flag(lut), rs, _ptr(out), _ptr(ws), nbytes,
+              _stream())
+    return out
+
+
+def moe_gemm_rows(xh: torch.Tensor, code_u32: torch.Tensor, rows_idx: torch.Tensor,
+                  group_expert: torch.Tensor, K: int, IC: int, OC: int, R: int, n_rows: int,
+                  lut: bool | None = None) -> torch.Tensor:
+    """Row-blocked expert GEMM (msl.py:1366-1395).  xh [n_rows+1, IC] with a zero
+    row at n_rows; returns mid [n_rows+1, OC] (the caller slices the sink off)."""
+    _dev(xh, code_u32, rows_idx, group_expert)
+    n_groups = group_expert.shape[0]
+    if tuple(xh.shape) != (n_rows + 1, IC):
+        raise ValueError(f"xh must be [n_rows+1, {IC}] with a zero sink row")
+    if rows_idx.numel() != n_groups * R:
+        raise ValueError("rows_idx must hold n_groups*R entries")
+    mid = torch.zeros((n_rows + 1, OC), dtype=torch.float32, device=xh.device)
+    _lib.call("esc_gemm_rows", _ptr(xh), _ptr(_as_u32(code_u32)), _ptr(rows_idx),
+              _ptr(group_expert), n_groups, R, n_rows, K, IC, OC, _lut_flag(lut), _ptr(mid),
+              _stream())
+    return mid
+
+
+def dense_gemm_rows(xh: torch.Tensor, code_u32: torch.Tensor, K: int, IC: int, OC: int,
+                    R: int, lut: bool | None = None) -> torch.Tensor:
+    """Dense row-blocked GEMM, bit-identical to dense_gemv (msl.py:1785-1841)."""
+    _dev(xh, code_u32)
+    m = xh.shape[0]
+    mid = torch.empty((m, OC), dtype=torch.float32, device=xh.device)
+    _lib.call("esc_dense_gemm_rows", _ptr(xh), _ptr(_as_u32(code_u32)), m, R, K, IC, OC,
+              _lut_flag(lut), _ptr(mid), _stream())
+    return mid
+
+
+dense_gemm_rows_direct = dense_gemm_rows
+
+
+def dense_gemm_rows_direct_out(xh: torch.Tensor, code_u32: torch.Tensor, rout: torch.Tensor,
+                               K: int, IC: int, OC: int, R: int, rs: float = RS,
+                               lut: bool | None = None) -> torch.Tensor:
+    """Dense rows with the fused output transform -> f16 [m, OC] (msl.py:1844-1870)."""
+    _dev(xh, code_u32, rout)
+    m = xh.shape[0]
+    out = torch.empty((m, OC), dtype=torch.float16, device=xh.device)
+    _lib.call("esc_dense_gemm_rows_out", _ptr(xh), _ptr(_as_u32(code_u32)), _ptr(rout), m, R, K,
+              IC, OC, _lut_flag(lut), rs, _ptr(out), _stream())
+    return out
+
+
+def build_groups(row_expert: torch.Tensor, E: int, R: int, n_groups: int):
+    """Device sort-and-pack of rows into R-row expert groups (moe.py:30-78)."""
+    _dev(row_expert)
+    m = row_expert.shape[0]
+    rows_idx = torch.empty(n_groups * R, dtype=torch.int32, device=row_expert.device)
+    group_expert = torch.empty(n_groups, dtype=torch.int32, device=row_expert.device)
+    _lib.call("esc_build_groups", _ptr(row_expert), m, E, R, n_groups, _ptr(rows_idx),
+              _ptr(group_expert), _stream())
+    return rows_idx, group_expert
+
+
+def route_topk(logits: torch.Tensor, top_k: int):
+    """fp32 logits [T, E] -> ids [T, k] int32, scores [T, k] f32 (ref.py:326-331)."""
+    _dev(logits)
+    if logits.dtype != torch.float32:
+        raise ValueError("router logits must be float32")
+    t, e = logits.shape
+    ids = torch.empty((t, top_k), dtype=torch.int32, device=logits.device)
+    scores = torch.empty((t, top_k), dtype=torch.float32, device=logits.device)
+    _lib.call("esc_route_topk", _ptr(logits), t, e, top_k, _ptr(ids), _ptr(scores), _stream())
+    return ids, scores
+
+
+def moe_expert_path_workspace(T: int, top_k: int, E: int, H: int, I: int) -> int:
+    return int(_lib.load().esc_moe_expert_path_workspace(T, top_k, E, H, I))
+
+
+def moe_expert_path(x, ids, scores, gu_code, gu_rin, gu_rout, K_gu, dn_code, dn_rin, dn_rout,
+                    K_dn, lut=None, ws=None, out=None):
+    """Routed experts for T tokens -> f16 [T, H] (models/qwen3_5_moe.py:207-253)."""
+    _dev(x, ids, scores, gu_code, gu_rin, gu_rout, dn_code, dn_rin, dn_rout)
+    t, h = x.shape
+    k = ids.shape[1]
+    E = gu_code.shape[0]
+    I = gu_rout.shape[1] // 2
+    if ids.dtype != torch.int32 or scores.dtype != torch.float32:
+        raise ValueError("ids must be int32 and scores float32")
+    nbytes = moe_expert_path_workspace(t, k, E, h, I)
+    if ws is None:
+        ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=x.device)
+    y = out if out is not None else torch.empty((t, h), dtype=torch.float16, device=x.device)
+    _lib.call("esc_moe_expert_path", _ptr(x), _ptr(ids), _ptr(scores), t, k, E, h, I,
+              _ptr(_as_u32(gu_code)), _ptr(gu_rin), _ptr(gu_rout), K_gu,
+              _ptr(_as_u32(dn_code)), _ptr(dn_rin), _ptr(dn_rout), K_dn, _lut_flag(lut),
+              _ptr(y), _ptr(ws), ws.numel(), _stream())
+    return y
+
+
+def swiglu(gu16: torch.Tensor) -> torch.Tensor:
+    """f16 [m, 2I] -> f16 [m, I]: f16(f16(silu(g)) * u), gate = first half (ref.py:296-301)."""
+    _dev(gu16)
+    m, two_i = gu16.shape
+    h = torch.empty((m, two_i // 2), dtype=torch.float16, device=gu16.device)
+    _lib.call("esc_swiglu", _ptr(gu16), m, two_i // 2, _ptr(h), _stream())
+    return h
+
+
+def moe_combine(d16: torch.Tensor, scores: torch.Tensor, top_k: int) -> torch.Tensor:
+    """Token-major rows [T*k, H] f16 -> f16 [T, H], weighted slot-order sum
+    (models/qwen3_5_moe.py:227-253)."""
+    _dev(d16, scores)
+    m, h = d16.shape
+    t = m // top_k
+    y = torch.empty((t, h), dtype=torch.float16, device=d16.device)
+    _lib.call("esc_moe_combine", _ptr(d16), _ptr(scores), t, top_k, h, _ptr(y), _stream())
+    return y

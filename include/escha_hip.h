@@ -1,0 +1,142 @@
+/* escha_hip — C ABI of the MI355X (gfx950) coded-projection engine.
+ *
+ * Drop-in boundary for escha-mlx's kernel layer (escha_mlx/msl.py): every
+ * entry point takes device pointers and sizes, enqueues on the given HIP
+ * stream (hipStream_t passed as void*, NULL = default stream), never
+ * allocates, frees or synchronises (except esc_init, once per device), and
+ * writes caller-allocated outputs.  Pointer arguments follow the reference's
+ * tensors: code is the export's int16 stream viewed as little-endian uint32
+ * [..., TK, TN, 8K] (escha_mlx/msl.py:1398-1401); f16 data travels as
+ * uint16_t bit patterns.
+ *
+ * Return value: 0 on success, a negative ESC_E* code otherwise; the message
+ * is then available from esc_last_error() (thread-local).  Preconditions the
+ * reference raises ValueError for (escha_mlx/dense.py:170-242,
+ * msl.py:1794-1823) are checked here and return ESC_EINVAL.
+ */
+#ifndef ESCHA_HIP_H
+#define ESCHA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ESC_OK 0
+#define ESC_EINVAL (-1)   /* shape / K / pointer precondition violated */
+#define ESC_EHIP (-2)     /* the HIP runtime reported an error           */
+#define ESC_ENOSPACE (-3) /* workspace smaller than the *_workspace size */
+
+/* ABI version (major*100 + minor). */
+int esc_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* esc_last_error(void);
+
+/* Build the 65,536-entry decode table on the current device (idempotent,
+ * synchronous).  Called implicitly by the first table-decode entry point on
+ * a device; call it explicitly before capturing a HIP graph.
+ * Replaces the host-built table upload msl._lut_array (escha_mlx/msl.py:1074-1076). */
+int esc_init(void);
+
+/* code u32 [TK][TN][8K] -> w f16 [IC][OC] (bit-exact decode).
+ * Mirrors msl.decode_tiles (escha_mlx/msl.py:1404-1421). */
+int esc_decode_tiles(const uint32_t* code, int K, int IC, int OC, int use_lut, uint16_t* w,
+                     void* stream);
+
+/* xh = f16(H128(f32(rows) * rin[e]) * RS), rows f16 [m][IC]; rin f32 [E][IC]
+ * gathered by row_expert [m], or rin [IC] when row_expert is NULL.
+ * Mirrors msl.scaled_had / dense_scaled_had (escha_mlx/msl.py:1029-1047, 1481-1483). */
+int esc_input_transform(const uint16_t* rows, const float* rin, const int32_t* row_expert, int m,
+                        int IC, float rs, uint16_t* out, void* stream);
+
+/* y = f16((H128(mid) * RS) * rout[e]) [+ bias f16 [OC], added in f32].
+ * Mirrors msl.scaled_had_out / dense_scaled_had_out (escha_mlx/msl.py:1050-1067, 1486-1488)
+ * and the bias step of EschaLinear.__call__ (escha_mlx/dense.py:356-361). */
+int esc_output_transform(const float* mid, const float* rout, const int32_t* row_expert,
+                         const uint16_t* bias, int m, int OC, float rs, uint16_t* out,
+                         void* stream);
+
+/* mid f32 [M][OC] = xh f16 [M][IC] @ decode(code[row_expert[r]]), in the
+ * reference kernels' exact float32 order (bit-reproducible).  code is
+ * [E][TK][TN][8K], or [TK][TN][8K] with row_expert NULL (dense).
+ * Mirrors msl.moe_gemv / dense_gemv with splits=1 (escha_mlx/msl.py:1424-1478, 1530-1538). */
+int esc_gemv(const uint16_t* xh, const uint32_t* code, const int32_t* row_expert, int M, int K,
+             int IC, int OC, int use_lut, float* mid, void* stream);
+
+/* Tolerance-contract GEMV (split-K, reassociated float32 sum, deterministic):
+ * same arguments and result shape as esc_gemv; ws = float workspace of
+ * esc_gemv_fast_workspace(M, K, IC, OC) bytes; out f16 [M][OC] is the fused
+ * output transform with rout ([E][OC] gathered by row_expert, or [OC]).
+ * Replaces msl.moe_gemv + msl.scaled_had_out (escha_mlx/msl.py:1424, 1050). */
+size_t esc_gemv_fast_workspace(int M, int K, int IC, int OC);
+int esc_gemv_fast_out(const uint16_t* xh, const uint32_t* code, const int32_t* row_expert,
+                      const float* rout, int M, int K, int IC, int OC, int use_lut, float rs,
+                      uint16_t* out, void* ws, size_t ws_bytes, void* stream);
+
+/* Row-blocked expert GEMM, bit-identical to esc_gemv per row.  xh
+ * [n_rows+1][IC] with row n_rows all zeros (padding sink); rows_idx
+ * [n_groups*R] (padding = n_rows); group_expert [n_groups] (-1 = skip);
+ * mid [n_rows+1][OC].  R in {1,2,3,4,8,12,16}.
+ * Mirrors msl.moe_gemm_rows (escha_mlx/msl.py:1366-1395). */
+int esc_gemm_rows(const uint16_t* xh, const uint32_t* code, const int32_t* rows_idx,
+                  const int32_t* group_expert, int n_groups, int R, int n_rows, int K, int IC,
+                  int OC, int use_lut, float* mid, void* stream);
+
+/* Dense row-blocked GEMM: group g owns rows [gR, gR+R); bit-identical to
+ * esc_gemv.  R in {1,2,4,8,16}.  Mirrors msl.dense_gemm_rows /
+ * dense_gemm_rows_direct (escha_mlx/msl.py:1785-1841). */
+int esc_dense_gemm_rows(const uint16_t* xh, const uint32_t* code, int M, int R, int K, int IC,
+                        int OC, int use_lut, float* mid, void* stream);
+
+/* Dense rows with the output transform fused: out f16 [M][OC].  R in {1,2,4,8}.
+ * Mirrors msl.dense_gemm_rows_direct_out (escha_mlx/msl.py:1844-1870). */
+int esc_dense_gemm_rows_out(const uint16_t* xh, const uint32_t* code, const float* rout, int M,
+                            int R, int K, int IC, int OC, int use_lut, float rs, uint16_t* out,
+                            void* stream);
+
+/* Sort rows by expert into R-row groups (integer only, on device).
+ * rows_idx [n_groups*R], group_expert [n_groups].
+ * Mirrors moe.build_groups (escha_mlx/moe.py:30-78). */
+int esc_build_groups(const int32_t* row_expert, int m, int E, int R, int n_groups,
+                     int32_t* rows_idx, int32_t* group_expert, void* stream);
+
+/* Router: logits f32 [T][E] -> ids [T][k] (descending, ties -> lower id) and
+ * scores f32 [T][k] (softmax over the k values).  E <= 1024, k <= 32.
+ * Mirrors the routing of EschaSparseMoeBlock.__call__
+ * (escha_mlx/models/qwen3_5_moe.py:257-263) in ref.moe_block's stable order
+ * (escha_mlx/ref.py:326-331). */
+int esc_route_topk(const float* logits, int T, int E, int top_k, int32_t* ids, float* scores,
+                   void* stream);
+
+/* h f16 [m][I] = f16(f16(g / (1 + exp(-g))) * u), gate = first half of gu f16 [m][2I].
+ * Mirrors ref.swiglu (escha_mlx/ref.py:296-301) / models/qwen3_5_moe.py:221-223. */
+int esc_swiglu(const uint16_t* gu, int m, int I, uint16_t* h, void* stream);
+
+/* y f16 [T][H] = f16(sum over slots s in order of f32(d16[t*k+s]) * f32(f16(scores[t*k+s]))).
+ * Mirrors the weighted segmented sum of _expert_path (escha_mlx/models/qwen3_5_moe.py:227-253). */
+int esc_moe_combine(const uint16_t* d16, const float* scores, int T, int top_k, int H,
+                    uint16_t* y, void* stream);
+
+/* Routed-expert path for T tokens: y f16 [T][H] = f16(sum over the k slots,
+ * in slot order, of f32(d16) * f32(f16(score))), where per (token, slot):
+ * gate_up linear (H -> 2I, K_gu) -> swiglu -> down linear (I -> H, K_dn).
+ * gu_code [E][H/16][2I/16][8K_gu], gu_rin [E][H], gu_rout [E][2I],
+ * dn_code [E][I/16][H/16][8K_dn], dn_rin [E][I], dn_rout [E][H] (f32).
+ * Tolerance contract (reassociated GEMV sums; decode bit-exact).
+ * Replaces EschaSparseMoeBlock._expert_path (escha_mlx/models/qwen3_5_moe.py:207-253). */
+size_t esc_moe_expert_path_workspace(int T, int top_k, int E, int H, int I);
+int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, int T,
+                        int top_k, int E, int H, int I, const uint32_t* gu_code,
+                        const float* gu_rin, const float* gu_rout, int K_gu,
+                        const uint32_t* dn_code, const float* dn_rin, const float* dn_rout,
+                        int K_dn, int use_lut, uint16_t* y, void* ws, size_t ws_bytes,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ESCHA_HIP_H */

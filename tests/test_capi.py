@@ -1,0 +1,193 @@
+"""C-ABI library and host logic on the CPU (no GPU compute calls).
+
+Precondition failures return ESC_EINVAL before the library touches HIP, so
+they are forced here on a machine without a GPU (failure handling runs on the
+CPU).
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from escha_mlx_amd import _lib, dense, envs, moe, ops
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "escha_hip.h"
+DUMMY = ctypes.c_void_p(0x1000)  # never dereferenced: the calls fail validation first
+
+
+def header_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(esc_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    syms = header_symbols()
+    assert len(syms) >= 15
+    for s in syms:
+        assert hasattr(lib, s), f"{s} declared in include/escha_hip.h but not exported"
+
+
+def test_binding_table_matches_header():
+    assert sorted(_lib.SIGNATURES) == header_symbols()
+
+
+def test_version_and_empty_error():
+    lib = _lib.load()
+    assert lib.esc_version() == 100
+    assert isinstance(lib.esc_last_error(), bytes)
+
+
+def _rc_msg(fn, *args):
+    lib = _lib.load()
+    rc = getattr(lib, fn)(*args)
+    return rc, lib.esc_last_error().decode()
+
+
+def test_rejects_unsupported_K():
+    rc, msg = _rc_msg("esc_decode_tiles", DUMMY, 4, 128, 128, 0, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "K=4" in msg
+
+
+@pytest.mark.parametrize("ic,oc", [(100, 128), (128, 144), (0, 128), (256, -128)])
+def test_rejects_non_128_multiple(ic, oc):
+    rc, msg = _rc_msg("esc_gemv", DUMMY, DUMMY, None, 1, 2, ic, oc, 0, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "multiples of 128" in msg
+
+
+def test_rejects_null_pointers():
+    rc, msg = _rc_msg("esc_gemv", None, DUMMY, None, 1, 2, 128, 128, 0, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "null" in msg
+
+
+def test_rejects_bad_rows_per_group():
+    rc, msg = _rc_msg("esc_dense_gemm_rows", DUMMY, DUMMY, 4, 3, 2, 128, 128, 0, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "R=3" in msg
+
+
+def test_rejects_small_workspace():
+    rc, msg = _rc_msg("esc_gemv_fast_out", DUMMY, DUMMY, None, DUMMY, 1, 2, 2048, 1024, 0,
+                      ctypes.c_float(0.1), DUMMY, DUMMY, 16, None)
+    assert rc == _lib.ESC_ENOSPACE and "workspace" in msg
+
+
+def test_rejects_topk_above_experts():
+    rc, msg = _rc_msg("esc_route_topk", DUMMY, 1, 4, 8, DUMMY, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "top_k" in msg
+
+
+def test_rejects_groups_below_bound():
+    rc, msg = _rc_msg("esc_build_groups", DUMMY, 64, 16, 4, 3, DUMMY, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "bound" in msg
+
+
+def test_workspace_sizes_are_positive():
+    lib = _lib.load()
+    assert lib.esc_gemv_fast_workspace(8, 2, 2048, 1024) > 0
+    assert lib.esc_moe_expert_path_workspace(1, 8, 256, 2048, 512) > 0
+    assert lib.esc_gemv_fast_workspace(8, 4, 2048, 1024) == 0
+
+
+def test_check_maps_status_to_exceptions():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ESC_EINVAL, "x")
+    with pytest.raises(_lib.EschaHipError):
+        _lib.check(_lib.ESC_EHIP, "x")
+
+
+def test_ops_refuse_cpu_tensors():
+    with pytest.raises(ValueError, match="GPU"):
+        ops.decode_tiles(torch.zeros(16 * 8, dtype=torch.int32), 2, 128, 128)
+
+
+def test_code_to_u32_little_endian():
+    code = np.array([[0x1234, -0x0001, 0x0000, 0x7FFF]], dtype=np.int16)
+    assert ops.code_to_u32(code).tolist() == [[0xFFFF1234, 0x7FFF0000]]
+
+
+# ---------------------------------------------------------------- host policies
+
+def test_dense_block_r_policy():
+    """min(m, 16) snapped down to a power of two (escha_mlx/msl.py:1562-1601)."""
+    assert [dense.dense_block_r(m) for m in (1, 2, 3, 4, 5, 8, 9, 16, 17, 2048)] == \
+        [1, 2, 2, 4, 4, 8, 8, 16, 16, 16]
+    assert dense.dense_block_r(100, pin=4) == 4
+
+
+def test_moe_blocked_r_policy():
+    """models/qwen3_5_moe.py:124-170."""
+    assert [moe.blocked_R(m) for m in (8, 64, 127, 128, 256, 320, 1024, 2048)] == \
+        [1, 1, 1, 2, 2, 3, 4, 12]
+
+
+def test_n_groups_bound():
+    assert moe.n_groups_bound(256, 256, 2) == (256 + 256 + 1) // 2
+
+
+def _weight(K=2, ic=128, oc=128, **kw):
+    rng = np.random.default_rng(0)
+    code = rng.integers(-32768, 32768, size=(ic // 16, oc // 16, 16 * K), dtype=np.int16)
+    return dense.EschaWeight(code, np.ones(ic, np.float16), np.ones(oc, np.float16),
+                             device="cpu", **kw)
+
+
+def test_weight_infers_K_and_folds_scales():
+    w = _weight(K=3, s_in=np.full(128, 0.5, np.float32), s_out=np.full(128, 2.0, np.float32))
+    assert w.K == 3 and w.IC == 128 and w.OC == 128
+    assert torch.all(w.rin == 0.5) and torch.all(w.rout == 2.0)
+    assert w.code.dtype == torch.int32 and tuple(w.code.shape) == (8, 8, 24)
+
+
+def test_weight_rejects_unsupported_K():
+    code = np.zeros((8, 8, 64), np.int16)
+    with pytest.raises(ValueError, match="K=4"):
+        dense.EschaWeight(code, np.ones(128), np.ones(128), device="cpu")
+
+
+def test_weight_rejects_non_128():
+    code = np.zeros((1, 8, 32), np.int16)
+    with pytest.raises(ValueError, match="multiples of 128"):
+        dense.EschaWeight(code, np.ones(16), np.ones(128), device="cpu")
+
+
+def test_weight_rejects_2d_transform_vectors():
+    code = np.zeros((8, 8, 32), np.int16)
+    with pytest.raises(ValueError, match="1-D"):
+        dense.EschaWeight(code, np.ones((1, 128)), np.ones(128), device="cpu")
+
+
+@pytest.mark.parametrize("cfg,msg", [([16, 2, 2, 1, 128], "fields"),
+                                     ([16, 3, 2, 1, 128, 128], "disagrees"),
+                                     ([16, 2, 2, 2, 128, 128], "codebook")])
+def test_weight_config_guards(cfg, msg):
+    with pytest.raises(ValueError, match=msg):
+        _weight(K=2, config=np.array(cfg))
+
+
+def test_weight_scale_shape_guard():
+    with pytest.raises(ValueError, match="escha_s_in"):
+        _weight(s_in=np.ones((2, 128), np.float32))
+
+
+def test_env_validation(monkeypatch):
+    monkeypatch.setenv("ESCHA_MLX_LUT", "yes")
+    with pytest.raises(ValueError, match="ESCHA_MLX_LUT"):
+        envs.use_lut()
+    monkeypatch.setenv("ESCHA_MLX_DENSE_BLOCK_R", "3")
+    with pytest.raises(ValueError, match="ESCHA_MLX_DENSE_BLOCK_R"):
+        envs.dense_block_r_pin()
+
+
+def test_experts_container_validation():
+    with pytest.raises(ValueError):
+        moe.EschaExperts(np.zeros((2, 8, 8, 64), np.int16), np.ones((2, 128)), np.ones((2, 128)),
+                         device="cpu")
+    ex = moe.EschaExperts(np.zeros((2, 8, 16, 32), np.int16), np.ones((2, 128)),
+                          np.ones((2, 256)), device="cpu")
+    assert (ex.E, ex.IC, ex.OC, ex.K) == (2, 128, 256, 2)

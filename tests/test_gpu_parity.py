@@ -1,0 +1,370 @@
+"""GPU parity: HIP kernels through the C ABI vs the NumPy oracle.
+
+Bar: bit-exact for decode, transforms, routing ids, grouping and every
+order-exact GEMV / GEMM (the reference kernels' float32 order); the split-K
+GEMV and the fused MoE path are held to a float16 tolerance against float64
+(and to bit-exactness where the sum has one non-zero term: one-hot inputs).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref_np as R
+
+from .conftest import has_gpu, sha256
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not has_gpu(), reason="needs a ROCm GPU")]
+
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    print(f"\n[gpu case] {request.node.nodeid}", flush=True)
+    yield
+    torch.cuda.synchronize()
+
+
+def ops():
+    from escha_mlx_amd import ops as o
+    return o
+
+
+def bits16(t):
+    return t.cpu().numpy().view(np.uint16)
+
+
+def rand_code(rng, shape_words):
+    return rng.integers(0, 2**32, size=shape_words, dtype=np.uint64).astype(np.uint32)
+
+
+def dcode(u32: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(u32).view(np.int32)).to(DEV)
+
+
+# ---------------------------------------------------------------- decode
+
+@pytest.mark.parametrize("lut", [False, True], ids=["hash", "lut"])
+@pytest.mark.parametrize("which", ["k2", "k3"])
+def test_decode_tiles_bit_exact_vs_goldens(which, lut, k2_golden, k3_golden):
+    packed, meta, head = k2_golden if which == "k2" else k3_golden
+    K = 2 if which == "k2" else 3
+    ic, oc = meta["shape"]
+    w = ops().decode_tiles(ops().to_device_code(packed, DEV), K, ic, oc, lut=lut)
+    got = w.cpu().numpy()
+    assert np.array_equal(got[: meta["head_rows"]].view(np.uint16), head.view(np.uint16))
+    assert sha256(got) == meta["sha256"], "decoded golden differs"
+
+
+@pytest.mark.parametrize("K", [2, 3])
+def test_decode_hash_equals_lut_equals_oracle_random(K):
+    rng = np.random.default_rng(42 + K)
+    code = rand_code(rng, (16, 24, 8 * K))
+    d = dcode(code)
+    a = bits16(ops().decode_tiles(d, K, 256, 384, lut=False))
+    b = bits16(ops().decode_tiles(d, K, 256, 384, lut=True))
+    want = R.reconstruct(code, 256, 384, K).view(np.uint16)
+    assert np.array_equal(a, want) and np.array_equal(b, want)
+
+
+# ---------------------------------------------------------------- transforms
+
+@pytest.mark.parametrize("m,IC,E", [(8, 512, 256), (96, 2048, 64), (3, 128, 1)])
+def test_input_transform_bit_exact(m, IC, E):
+    rng = np.random.default_rng(m * 7 + IC)
+    rows = rng.standard_normal((m, IC)).astype(np.float16)
+    rin = rng.standard_normal((E, IC)).astype(np.float32)
+    re = rng.integers(0, E, size=m).astype(np.int32)
+    got = ops().scaled_had(torch.from_numpy(rows).to(DEV), torch.from_numpy(rin).to(DEV),
+                           torch.from_numpy(re).to(DEV))
+    want = R.input_transform(rows, rin[re])
+    assert np.array_equal(bits16(got), want.view(np.uint16))
+    # dense variant
+    got_d = ops().scaled_had(torch.from_numpy(rows).to(DEV), torch.from_numpy(rin[0]).to(DEV), None)
+    assert np.array_equal(bits16(got_d), R.input_transform(rows, rin[0]).view(np.uint16))
+
+
+@pytest.mark.parametrize("m,OC,E", [(8, 1024, 256), (33, 384, 7)])
+def test_output_transform_bit_exact(m, OC, E):
+    rng = np.random.default_rng(m + OC)
+    mid = (rng.standard_normal((m, OC)) * 5).astype(np.float32)
+    rout = (rng.standard_normal((E, OC)) * 0.01).astype(np.float32)
+    re = rng.integers(0, E, size=m).astype(np.int32)
+    got = ops().scaled_had_out(torch.from_numpy(mid).to(DEV), torch.from_numpy(rout).to(DEV),
+                               torch.from_numpy(re).to(DEV))
+    assert np.array_equal(bits16(got), R.output_transform(mid, rout[re]).view(np.uint16))
+
+
+def test_transforms_match_reference_vectors(ref_vectors):
+    v = ref_vectors
+    got = ops().scaled_had(torch.from_numpy(v["in_x"]).to(DEV), torch.from_numpy(v["in_rin"]).to(DEV), None)
+    assert np.array_equal(bits16(got), v["in_y"].view(np.uint16))
+    got = ops().scaled_had_out(torch.from_numpy(v["out_mid"]).to(DEV),
+                               torch.from_numpy(v["out_rout"]).to(DEV), None)
+    assert np.array_equal(bits16(got), v["out_y"].view(np.uint16))
+
+
+def test_swiglu_vs_reference_vectors(ref_vectors):
+    x = ref_vectors["swiglu_x"]
+    got = bits16(ops().swiglu(torch.from_numpy(x).to(DEV)))
+    want = ref_vectors["swiglu_y"].view(np.uint16)
+    # device expf vs numpy exp: identical f16 except where an f32 ulp crosses a tie
+    mism = int((got != want).sum())
+    assert mism <= max(1, got.size // 1000), mism
+    g = got.view(np.float16).astype(np.float32)
+    w = want.view(np.float16).astype(np.float32)
+    assert np.abs(g - w).max() <= np.abs(w).max() * 2 ** -10
+
+
+# ---------------------------------------------------------------- order-exact GEMV
+
+def _expert_stack(rng, K, ic, oc, E):
+    return rand_code(rng, (E, ic // 16, oc // 16, 8 * K))
+
+
+@pytest.mark.parametrize("lut", [False, True], ids=["hash", "lut"])
+@pytest.mark.parametrize("K,IC,OC", [(2, 2048, 1024), (3, 512, 2048)])
+def test_moe_gemv_bit_exact_mixed_experts(K, IC, OC, lut):
+    """Expert-stride indexing with 0 and E-1 included (reference tests/test_metal.py:46-72),
+    held to bit-exactness against the oracle's kernel-order GEMV."""
+    rng = np.random.default_rng(K)
+    E = 4
+    codes = _expert_stack(rng, K, IC, OC, E)
+    xh = (rng.standard_normal((8, IC)) * 0.05).astype(np.float16)
+    re = np.array([0, E - 1, 1, 2, E - 1, 0, 2, 1], dtype=np.int32)
+    mid = ops().moe_gemv(torch.from_numpy(xh).to(DEV), dcode(codes), torch.from_numpy(re).to(DEV),
+                         K, IC, OC, lut=lut).cpu().numpy()
+    w = [R.reconstruct(codes[e], IC, OC, K) for e in range(E)]
+    for r in range(8):
+        want = R.gemv_ordered(xh[r:r + 1], w[re[r]])[0]
+        assert np.array_equal(mid[r].view(np.uint32), want.view(np.uint32)), r
+
+
+def test_dense_gemv_golden_stream_bit_exact(k2_golden):
+    packed, meta, _ = k2_golden
+    ic, oc = meta["shape"]
+    rng = np.random.default_rng(0)
+    xh = rng.standard_normal((3, ic)).astype(np.float16)
+    mid = ops().dense_gemv(torch.from_numpy(xh).to(DEV), ops().to_device_code(packed, DEV), 2, ic, oc)
+    want = R.gemv_ordered(xh, R.reconstruct(packed, ic, oc, 2))
+    assert np.array_equal(mid.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("R_", [2, 3, 4, 12])
+def test_gemm_rows_bit_identical_to_per_row(R_):
+    """Row blocking changes only the loop nest (reference tests/test_blocked.py:69-161)."""
+    from escha_mlx_amd import moe
+    rng = np.random.default_rng(R_)
+    K, IC, OC, E, m = 2, 512, 256, 16, 45
+    codes = _expert_stack(rng, K, IC, OC, E)
+    re = rng.integers(0, E, size=m).astype(np.int32)
+    re[:9] = 3  # skew: one expert with many rows
+    xh = rng.standard_normal((m, IC)).astype(np.float16)
+    d_xh, d_code, d_re = torch.from_numpy(xh).to(DEV), dcode(codes), torch.from_numpy(re).to(DEV)
+    per_row = ops().moe_gemv(d_xh, d_code, d_re, K, IC, OC).cpu().numpy()
+    ng = moe.n_groups_bound(m, E, R_)
+    rows_idx, group_expert = moe.build_groups(d_re, E, R_, ng)
+    ri, ge = R.build_groups(re, E, R_, ng)
+    assert np.array_equal(rows_idx.cpu().numpy(), ri) and np.array_equal(group_expert.cpu().numpy(), ge)
+    xh_pad = torch.cat([d_xh, torch.zeros((1, IC), dtype=torch.float16, device=DEV)])
+    mid = ops().moe_gemm_rows(xh_pad, d_code, rows_idx, group_expert, K, IC, OC, R_, m).cpu().numpy()
+    assert np.array_equal(mid[:m].view(np.uint32), per_row.view(np.uint32))
+
+
+@pytest.mark.parametrize("R_", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("m", [1, 5, 17])
+def test_dense_rows_bit_identical_to_gemv(R_, m):
+    rng = np.random.default_rng(R_ * 100 + m)
+    K, IC, OC = 3, 256, 384
+    code = rand_code(rng, (IC // 16, OC // 16, 8 * K))
+    xh = rng.standard_normal((m, IC)).astype(np.float16)
+    d_xh, d_code = torch.from_numpy(xh).to(DEV), dcode(code)
+    a = ops().dense_gemv(d_xh, d_code, K, IC, OC).cpu().numpy()
+    b = ops().dense_gemm_rows(d_xh, d_code, K, IC, OC, R_).cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(a.view(np.uint32), R.gemv_ordered(xh, R.reconstruct(code, IC, OC, K)).view(np.uint32))
+
+
+@pytest.mark.parametrize("R_", [1, 2, 4, 8])
+def test_dense_rows_out_bit_identical_to_chain(R_):
+    rng = np.random.default_rng(9 + R_)
+    K, IC, OC, m = 2, 384, 256, 7
+    code = rand_code(rng, (IC // 16, OC // 16, 8 * K))
+    xh = rng.standard_normal((m, IC)).astype(np.float16)
+    rout = (rng.standard_normal(OC) * 0.01).astype(np.float32)
+    d = ops().dense_gemm_rows_direct_out(torch.from_numpy(xh).to(DEV), dcode(code),
+                                         torch.from_numpy(rout).to(DEV), K, IC, OC, R_)
+    want = R.output_transform(R.gemv_ordered(xh, R.reconstruct(code, IC, OC, K)), rout)
+    assert np.array_equal(bits16(d), want.view(np.uint16))
+
+
+# ---------------------------------------------------------------- split-K GEMV
+
+def _fast_case(K, IC, OC, E, m, seed):
+    rng = np.random.default_rng(seed)
+    codes = _expert_stack(rng, K, IC, OC, E)
+    rout = (rng.choice([-1.0, 1.0], (E, OC)) * rng.uniform(0.5, 1.5, (E, OC)) * 1e-2).astype(np.float32)
+    re = rng.integers(0, E, size=m).astype(np.int32)
+    return rng, codes, rout, re
+
+
+@pytest.mark.parametrize("lut", [False, True], ids=["hash", "lut"])
+@pytest.mark.parametrize("K,IC,OC", [(2, 2048, 1024), (2, 512, 2048), (3, 512, 2048), (3, 2048, 1024)])
+def test_fast_gemv_one_hot_bit_exact(K, IC, OC, lut):
+    """One non-zero input per row: every reassociated sum is exact, so the fused
+    decode + output transform must equal the oracle bit-for-bit."""
+    rng, codes, rout, re = _fast_case(K, IC, OC, 3, 5, 100 + K + IC)
+    xh = np.zeros((5, IC), np.float16)
+    hot = rng.integers(0, IC, size=5)
+    for r in range(5):
+        xh[r, hot[r]] = np.float16(rng.choice([1.0, -2.0, 0.5]))
+    out = ops().gemv_fast_out(torch.from_numpy(xh).to(DEV), dcode(codes), torch.from_numpy(re).to(DEV),
+                              torch.from_numpy(rout).to(DEV), K, IC, OC, lut=lut)
+    w = [R.reconstruct(codes[e], IC, OC, K) for e in range(3)]
+    for r in range(5):
+        mid = xh[r, hot[r]].astype(np.float32) * w[re[r]][hot[r]].astype(np.float32)
+        want = R.output_transform(mid[None], rout[re[r]])[0]
+        assert np.array_equal(bits16(out)[r], want.view(np.uint16)), r
+
+
+@pytest.mark.parametrize("K,IC,OC,m", [(2, 2048, 1024, 8), (2, 512, 2048, 8), (3, 5120, 1024, 1),
+                                       (3, 1024, 2048, 4)])
+def test_fast_gemv_tolerance_vs_f64(K, IC, OC, m):
+    rng, codes, rout, re = _fast_case(K, IC, OC, 4, m, K * 31 + m)
+    xh = rng.standard_normal((m, IC)).astype(np.float16)
+    out = ops().gemv_fast_out(torch.from_numpy(xh).to(DEV), dcode(codes), torch.from_numpy(re).to(DEV),
+                              torch.from_numpy(rout).to(DEV), K, IC, OC).cpu().numpy().astype(np.float32)
+    worst = 0.0
+    for r in range(m):
+        w = R.reconstruct(codes[re[r]], IC, OC, K)
+        mid64 = R.gemv_f64(xh[r:r + 1], w)[0]
+        exact = (R.h128(mid64[None].astype(np.float32)) * R.RS * rout[re[r]])[0]
+        err = np.abs(out[r] - exact).max() / np.abs(exact).max()
+        worst = max(worst, err)
+    # f16 output rounding (2^-11 relative) + f32 reassociation: 2e-3 of the row max
+    assert worst < 2e-3, worst
+
+
+def test_fast_gemv_deterministic():
+    rng, codes, rout, re = _fast_case(2, 2048, 1024, 8, 8, 5)
+    xh = torch.from_numpy(rng.standard_normal((8, 2048)).astype(np.float16)).to(DEV)
+    args = (xh, dcode(codes), torch.from_numpy(re).to(DEV), torch.from_numpy(rout).to(DEV), 2, 2048, 1024)
+    first = bits16(ops().gemv_fast_out(*args))
+    for _ in range(8):
+        assert np.array_equal(bits16(ops().gemv_fast_out(*args)), first)
+
+
+# ---------------------------------------------------------------- routing / MoE
+
+def test_route_topk_matches_oracle(ref_vectors):
+    lg = ref_vectors["route_logits"]
+    ids, sc = ops().route_topk(torch.from_numpy(lg).to(DEV), 8)
+    assert np.array_equal(ids.cpu().numpy(), ref_vectors["route_ids"])
+    assert np.allclose(sc.cpu().numpy(), ref_vectors["route_scores"], rtol=2e-6, atol=0)
+    rng = np.random.default_rng(3)
+    lg = rng.standard_normal((32, 256)).astype(np.float32)
+    lg[5, :] = 0.25  # all tied: lowest ids win
+    ids, sc = ops().route_topk(torch.from_numpy(lg).to(DEV), 8)
+    want_ids, want_sc = R.route_topk(lg, 8)
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+    assert np.allclose(sc.cpu().numpy(), want_sc, rtol=2e-6, atol=0)
+
+
+def _moe_case(E, H, I, K_gu, K_dn, T, k, seed):
+    rng = np.random.default_rng(seed)
+    gu_code = rand_code(rng, (E, H // 16, 2 * I // 16, 8 * K_gu))
+    dn_code = rand_code(rng, (E, I // 16, H // 16, 8 * K_dn))
+    gu_rin = rng.choice([-1.0, 1.0], (E, H)).astype(np.float32)
+    dn_rin = rng.choice([-1.0, 1.0], (E, I)).astype(np.float32)
+    gu_rout = (rng.choice([-1.0, 1.0], (E, 2 * I)) * rng.uniform(0.5, 1.5, (E, 2 * I)) * 4e-2).astype(np.float32)
+    dn_rout = (rng.choice([-1.0, 1.0], (E, H)) * rng.uniform(0.5, 1.5, (E, H)) * 4e-2).astype(np.float32)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    return dict(gu_code=gu_code, dn_code=dn_code, gu_rin=gu_rin, dn_rin=dn_rin, gu_rout=gu_rout,
+                dn_rout=dn_rout, x=x, logits=logits)
+
+
+def _block(c, E, k, K_gu, K_dn, monkeypatch, exact):
+    from escha_mlx_amd import moe
+    monkeypatch.setenv("ESCHA_HIP_EXACT", "1" if exact else "0")
+    gu = moe.EschaExperts.from_device(dcode(c["gu_code"]), torch.from_numpy(c["gu_rin"]).to(DEV),
+                                      torch.from_numpy(c["gu_rout"]).to(DEV), K_gu)
+    dn = moe.EschaExperts.from_device(dcode(c["dn_code"]), torch.from_numpy(c["dn_rin"]).to(DEV),
+                                      torch.from_numpy(c["dn_rout"]).to(DEV), K_dn)
+    return moe.EschaMoEExperts(gu, dn, E, k)
+
+
+def _oracle_moe(c, ids, sc, E, H, I, K_gu, K_dn, used):
+    w_gu = np.zeros((E, H, 2 * I), np.float16)
+    w_dn = np.zeros((E, I, H), np.float16)
+    for e in used:
+        w_gu[e] = R.reconstruct(c["gu_code"][e], H, 2 * I, K_gu)
+        w_dn[e] = R.reconstruct(c["dn_code"][e], I, H, K_dn)
+    return R.moe_routed(c["x"], ids, sc, {"w": w_gu, "rin": c["gu_rin"], "rout": c["gu_rout"]},
+                        {"w": w_dn, "rin": c["dn_rin"], "rout": c["dn_rout"]}, K_gu, K_dn,
+                        ordered=True)
+
+
+@pytest.mark.parametrize("exact", [False, True], ids=["fused", "exact"])
+@pytest.mark.parametrize("E,H,I,K_gu,K_dn,T,k", [(16, 256, 128, 2, 2, 1, 8), (32, 512, 256, 2, 3, 3, 4)])
+def test_moe_expert_path_vs_oracle(E, H, I, K_gu, K_dn, T, k, exact, monkeypatch):
+    c = _moe_case(E, H, I, K_gu, K_dn, T, k, E + H + T)
+    blk = _block(c, E, k, K_gu, K_dn, monkeypatch, exact)
+    ids, sc = ops().route_topk(torch.from_numpy(c["logits"]).to(DEV), k)
+    y = blk(torch.from_numpy(c["x"]).to(DEV), ids, sc).cpu().numpy()
+    ids_np, sc_np = ids.cpu().numpy(), sc.cpu().numpy()
+    want = _oracle_moe(c, ids_np, sc_np, E, H, I, K_gu, K_dn, np.unique(ids_np))
+    g, w = y.astype(np.float32), want.astype(np.float32)
+    rel = np.abs(g - w).max() / np.abs(w).max()
+    if exact:
+        # same order and rounding points; only swiglu's exp may differ by an f32 ulp
+        assert (y.view(np.uint16) != want.view(np.uint16)).mean() < 0.01 and rel < 1e-3, rel
+    else:
+        assert rel < 5e-3, rel
+
+
+def test_moe_fused_is_deterministic(monkeypatch):
+    c = _moe_case(64, 512, 256, 2, 2, 2, 8, 77)
+    blk = _block(c, 64, 8, 2, 2, monkeypatch, exact=False)
+    ids, sc = ops().route_topk(torch.from_numpy(c["logits"]).to(DEV), 8)
+    x = torch.from_numpy(c["x"]).to(DEV)
+    first = bits16(blk(x, ids, sc))
+    for _ in range(8):
+        assert np.array_equal(bits16(blk(x, ids, sc)), first)
+
+
+def test_moe_config3_shape_fused_vs_exact(monkeypatch):
+    """BASELINE config 3 shapes (E=256, H=2048, I=512, top-8, K=2): fused path
+    against the order-exact chain, plus the exact chain against the oracle."""
+    E, H, I, k = 256, 2048, 512, 8
+    c = _moe_case(E, H, I, 2, 2, 1, k, 2)
+    ids, sc = ops().route_topk(torch.from_numpy(c["logits"]).to(DEV), k)
+    x = torch.from_numpy(c["x"]).to(DEV)
+    y_fast = _block(c, E, k, 2, 2, monkeypatch, False)(x, ids, sc).cpu().numpy().astype(np.float32)
+    y_ex = _block(c, E, k, 2, 2, monkeypatch, True)(x, ids, sc).cpu().numpy()
+    ids_np, sc_np = ids.cpu().numpy(), sc.cpu().numpy()
+    want = _oracle_moe(c, ids_np, sc_np, E, H, I, 2, 2, np.unique(ids_np)).astype(np.float32)
+    assert np.abs(y_ex.astype(np.float32) - want).max() / np.abs(want).max() < 1e-3
+    assert np.abs(y_fast - want).max() / np.abs(want).max() < 5e-3
+
+
+# ---------------------------------------------------------------- dense module
+
+def test_dense_linear_module_vs_deploy_and_oracle(dense_linear_golden, monkeypatch):
+    from escha_mlx_amd import dense
+    monkeypatch.setenv("ESCHA_MLX_BIAS", "1")
+    g = dense_linear_golden
+    lin = dense.build({"escha_code": g["code"], "escha_rin": g["rin"], "escha_rout": g["rout"],
+                       "escha_s_in": g["s_in"], "escha_s_out": g["s_out"], "bias": g["bias"]}, device=DEV)
+    y = lin(torch.from_numpy(g["x"]).to(DEV)).cpu().numpy()   # M=8 -> fused rows-out, exact order
+    rin, rout = R.fold_scales(g["rin"], g["rout"], g["s_in"], g["s_out"])
+    want = R.dense_linear(g["x"], g["code"], rin, rout, g["K"], bias=g["bias"], ordered=True)
+    assert np.array_equal(y.view(np.uint16), want.view(np.uint16))
+    dep = g["deploy"].astype(np.float32)
+    rel = np.abs(y.astype(np.float32) - dep).mean() / np.abs(dep).mean()
+    assert rel < 3e-3
+    y1 = lin(torch.from_numpy(g["x"][:1]).to(DEV)).cpu().numpy().astype(np.float32)  # M=1 split-K
+    w1 = want[:1].astype(np.float32)
+    assert np.abs(y1 - w1).max() <= 2e-3 * np.abs(w1).max()
