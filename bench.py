@@ -109,7 +109,7 @@ def main():
     torch.cuda.set_device(0)
     ops.init()
     layers = make_layers(torch, args.layers, dev)
-    ws = torch.empty(ops.moe_expert_path_workspace(1, TOP_K, E, H, I), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(ops.moe_expert_path_workspace(1, TOP_K, E, H, I), dtype=torch.uint8, device=dev)
     routes = [moe.route(L["logits"], TOP_K) for L in layers]
     x0 = torch.randn(1, H, generator=torch.Generator(device=dev).manual_seed(7), device=dev).half()
     outs = [torch.empty(1, H, dtype=torch.float16, device=dev) for _ in layers]

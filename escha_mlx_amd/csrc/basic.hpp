@@ -66,8 +66,8 @@ __global__ __launch_bounds__(64) void k_input_transform(const uint16_t* __restri
   float v0 = (float)__builtin_bit_cast(half_t, rows[off]) * r[0];
   float v1 = (float)__builtin_bit_cast(half_t, rows[off + 1]) * r[1];
   h128_wave(v0, v1);
-  out[off] = __builtin_bit_cast(uint16_t, (half_t)(v0 * rs));
-  out[off + 1] = __builtin_bit_cast(uint16_t, (half_t)(v1 * rs));
+  out[off] = __builtin_bit_cast(uint16_t, to_f16(v0 * rs));
+  out[off + 1] = __builtin_bit_cast(uint16_t, to_f16(v1 * rs));
 }
 
 // y = f16((H128(mid) * RS) * rout) [+ bias, added in f32 after the f16 round]
@@ -84,11 +84,11 @@ __global__ __launch_bounds__(64) void k_output_transform(const float* __restrict
   const float* r = rout + (row_expert ? (size_t)row_expert[row] * OC : 0) + c;
   float v0 = mid[off], v1 = mid[off + 1];
   h128_wave(v0, v1);
-  half_t y0 = (half_t)((v0 * rs) * r[0]);
-  half_t y1 = (half_t)((v1 * rs) * r[1]);
+  half_t y0 = to_f16((v0 * rs) * r[0]);
+  half_t y1 = to_f16((v1 * rs) * r[1]);
   if (bias) {
-    y0 = (half_t)((float)y0 + (float)__builtin_bit_cast(half_t, bias[c]));
-    y1 = (half_t)((float)y1 + (float)__builtin_bit_cast(half_t, bias[c + 1]));
+    y0 = to_f16((float)y0 + (float)__builtin_bit_cast(half_t, bias[c]));
+    y1 = to_f16((float)y1 + (float)__builtin_bit_cast(half_t, bias[c + 1]));
   }
   out[off] = __builtin_bit_cast(uint16_t, y0);
   out[off + 1] = __builtin_bit_cast(uint16_t, y1);

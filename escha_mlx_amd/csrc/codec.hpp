@@ -28,6 +28,15 @@ constexpr float kRS = 0.088388347648f;
 typedef _Float16 half_t;
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
+// float32 -> f16 with the float32 value materialised first.  Without the
+// barrier the backend folds fptrunc(fmul(a, b)) into v_fma_mixlo_f16, which
+// rounds the exact product once to f16 instead of to f32 and then f16 — a
+// different rounding point from the reference's (escha_mlx/ref.py:221-228).
+__device__ __forceinline__ half_t to_f16(float x) {
+  __asm__ volatile("" : "+v"(x));
+  return (half_t)x;
+}
+
 // ---------------------------------------------------------------- lane map
 // Row / column of trellis step t inside its 16x16 tile.
 __host__ __device__ constexpr int step_row(int t) {

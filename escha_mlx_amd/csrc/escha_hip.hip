@@ -10,7 +10,7 @@
 #include <string>
 
 #include "../../include/escha_hip.h"
-#include "moe.hpp"
+#include "fused.hpp"
 
 namespace {
 
@@ -326,6 +326,8 @@ int esc_moe_combine(const uint16_t* d16, const float* scores, int T, int top_k, 
   return launched("k_combine");
 }
 
+}  // extern "C"
+
 // ---- routed experts: input transform -> gate_up -> swiglu/transform -> down -> combine
 namespace {
 struct MoePlan {
@@ -345,7 +347,46 @@ MoePlan moe_plan(int T, int top_k, int H, int I, int K_gu, int K_dn) {
   p.total = al(p.off_p2 + (size_t)p.S2 * p.M * H * 4);
   return p;
 }
+
+// One-launch path (fused.hpp) for decode-sized row counts.
+constexpr int kFusedMaxRows = 64;
+
+struct FusedPlan {
+  int M, NB, NKC, NCP, nA, nB, grid;
+  size_t off_pa, off_pb, off_int, total;
+  int n_int;
+};
+
+bool fused_eligible(int T, int top_k, int H, int I) {
+  return T * top_k <= kFusedMaxRows && H % 256 == 0 && I % 128 == 0;
+}
+
+FusedPlan fused_plan(int T, int top_k, int H, int I) {
+  FusedPlan f;
+  f.M = T * top_k;
+  f.NB = I / 128;
+  f.NKC = H / 256;
+  f.NCP = H / 256;
+  f.nA = f.M * f.NB * f.NKC;
+  f.nB = f.M * f.NCP * f.NB;
+  f.grid = std::min(std::max(f.nA, f.nB), 2048);
+  auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
+  f.off_pa = 0;
+  f.off_pb = al((size_t)f.nA * 256 * 4);
+  f.off_int = f.off_pb + al((size_t)f.nB * 256 * 4);
+  f.n_int = f.M * f.NB + f.nA + T * f.NCP + 2;
+  f.total = f.off_int + al((size_t)f.n_int * 4);
+  return f;
+}
+
+template <int KG, int KD>
+int launch_fused(const esc::FusedMoe& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((esc::k_moe_fused<KG, KD>), dim3(grid), dim3(esc::kFusedThreads), 0, s, p);
+  return launched("k_moe_fused");
+}
 }  // namespace
+
+extern "C" {
 
 size_t esc_moe_expert_path_workspace(int T, int top_k, int E, int H, int I) {
   (void)E;
@@ -353,7 +394,24 @@ size_t esc_moe_expert_path_workspace(int T, int top_k, int E, int H, int I) {
   // the plan's sizes depend on K only through the split counts; take the max
   size_t a = moe_plan(T, top_k, H, I, 2, 2).total, b = moe_plan(T, top_k, H, I, 3, 3).total;
   size_t c = moe_plan(T, top_k, H, I, 2, 3).total, d = moe_plan(T, top_k, H, I, 3, 2).total;
-  return std::max(std::max(a, b), std::max(c, d));
+  size_t m = std::max(std::max(a, b), std::max(c, d));
+  if (fused_eligible(T, top_k, H, I)) m = std::max(m, fused_plan(T, top_k, H, I).total);
+  return m;
+}
+
+int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int I,
+                   int32_t* host_flag, void* stream) {
+  ESC_REQUIRE(ws && host_flag, "null pointer");
+  *host_flag = 0;
+  if (!fused_eligible(T, top_k, H, I)) return ESC_OK;
+  const FusedPlan f = fused_plan(T, top_k, H, I);
+  ESC_REQUIRE(ws_bytes >= f.total, "workspace smaller than the plan");
+  const int32_t* err = reinterpret_cast<const int32_t*>(static_cast<const char*>(ws) + f.off_int) +
+                       (f.n_int - 1);
+  if (int rc = hip_check(hipMemcpyAsync(host_flag, err, 4, hipMemcpyDeviceToHost, S(stream)),
+                         "hipMemcpyAsync"))
+    return rc;
+  return hip_check(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
 }
 
 int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, int T,
@@ -370,6 +428,43 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
   if (int rc = check_proj(K_dn, I, H)) return rc;
   ESC_REQUIRE(T >= 0, "negative token count");
   if (T == 0) return ESC_OK;
+  if (fused_eligible(T, top_k, H, I)) {
+    const FusedPlan f = fused_plan(T, top_k, H, I);
+    if (!ws || ws_bytes < f.total)
+      return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, f.total);
+    char* w = static_cast<char*>(ws);
+    int* ints = reinterpret_cast<int*>(w + f.off_int);
+    esc::FusedMoe p{};
+    p.x = x;
+    p.ids = ids;
+    p.scores = scores;
+    p.gu_code = gu_code;
+    p.gu_rin = gu_rin;
+    p.gu_rout = gu_rout;
+    p.dn_code = dn_code;
+    p.dn_rin = dn_rin;
+    p.dn_rout = dn_rout;
+    p.y = y;
+    p.partA = reinterpret_cast<float*>(w + f.off_pa);
+    p.partB = reinterpret_cast<float*>(w + f.off_pb);
+    p.cntA = ints;
+    p.claimA = p.cntA + f.M * f.NB;
+    p.cntB = p.claimA + f.nA;
+    p.done = p.cntB + T * f.NCP;
+    p.err = p.done + 1;
+    p.T = T;
+    p.top_k = top_k;
+    p.H = H;
+    p.I = I;
+    p.NB = f.NB;
+    p.NKC = f.NKC;
+    p.NCP = f.NCP;
+    p.nA = f.nA;
+    p.nB = f.nB;
+    hipStream_t s = S(stream);
+    if (K_gu == 2) return K_dn == 2 ? launch_fused<2, 2>(p, f.grid, s) : launch_fused<2, 3>(p, f.grid, s);
+    return K_dn == 2 ? launch_fused<3, 2>(p, f.grid, s) : launch_fused<3, 3>(p, f.grid, s);
+  }
   const MoePlan p = moe_plan(T, top_k, H, I, K_gu, K_dn);
   if (!ws || ws_bytes < p.total)
     return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, p.total);

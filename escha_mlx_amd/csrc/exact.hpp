@@ -181,8 +181,8 @@ __global__ __launch_bounds__(512) void k_gemm_exact_out(const uint16_t* __restri
     h128_wave(v0, v1);
     const int c = blockIdx.x * 128 + 2 * lane;
     const size_t o = (size_t)dst[r] * OC + c;
-    out[o] = __builtin_bit_cast(uint16_t, (half_t)((v0 * rs) * rout[c]));
-    out[o + 1] = __builtin_bit_cast(uint16_t, (half_t)((v1 * rs) * rout[c + 1]));
+    out[o] = __builtin_bit_cast(uint16_t, to_f16((v0 * rs) * rout[c]));
+    out[o + 1] = __builtin_bit_cast(uint16_t, to_f16((v1 * rs) * rout[c + 1]));
   }
 }
 

@@ -167,15 +167,23 @@ __global__ __launch_bounds__(64) void k_splitk_out(const float* __restrict__ par
   const int blk = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
   const int c = blk * 128 + 2 * lane;
   float v0 = 0.f, v1 = 0.f;
-  for (int z = 0; z < S; ++z) {
-    const float* p = part + ((size_t)z * M + row) * OC + c;
-    v0 = v0 + p[0];
-    v1 = v1 + p[1];
+  for (int z0 = 0; z0 < S; z0 += 8) {
+    float2 pv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (z0 + j < S)
+        pv[j] = *reinterpret_cast<const float2*>(part + ((size_t)(z0 + j) * M + row) * OC + c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (z0 + j < S) {
+        v0 = v0 + pv[j].x;
+        v1 = v1 + pv[j].y;
+      }
   }
   h128_wave(v0, v1);
   const float* r = rout + (row_expert ? (size_t)row_expert[row] * OC : 0) + c;
-  out[(size_t)row * OC + c] = __builtin_bit_cast(uint16_t, (half_t)((v0 * rs) * r[0]));
-  out[(size_t)row * OC + c + 1] = __builtin_bit_cast(uint16_t, (half_t)((v1 * rs) * r[1]));
+  out[(size_t)row * OC + c] = __builtin_bit_cast(uint16_t, to_f16((v0 * rs) * r[0]));
+  out[(size_t)row * OC + c + 1] = __builtin_bit_cast(uint16_t, to_f16((v1 * rs) * r[1]));
 }
 
 }  // namespace esc

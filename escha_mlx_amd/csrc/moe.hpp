@@ -22,16 +22,16 @@ __global__ __launch_bounds__(64) void k_moe_input(const uint16_t* __restrict__ x
   float v1 = (float)__builtin_bit_cast(half_t, xr[1]) * r[1];
   h128_wave(v0, v1);
   uint16_t* o = xh + (size_t)row * H + c;
-  o[0] = __builtin_bit_cast(uint16_t, (half_t)(v0 * rs));
-  o[1] = __builtin_bit_cast(uint16_t, (half_t)(v1 * rs));
+  o[0] = __builtin_bit_cast(uint16_t, to_f16(v0 * rs));
+  o[1] = __builtin_bit_cast(uint16_t, to_f16(v1 * rs));
 }
 
 // h = f16(f16(silu(g)) * u) with silu(g) = g / (1 + exp(-g)) in float32
 // (escha_mlx/ref.py:296-301).
 __device__ __forceinline__ half_t swiglu1(half_t g, half_t u) {
   const float gf = (float)g;
-  const half_t s16 = (half_t)(gf / (1.0f + expf(-gf)));
-  return (half_t)((float)s16 * (float)u);
+  const half_t s16 = to_f16(gf / (1.0f + expf(-gf)));
+  return to_f16((float)s16 * (float)u);
 }
 
 // One 128-block of the gate_up output of one row, from split-K partials:
@@ -42,14 +42,23 @@ __device__ __forceinline__ void gu_block(const float* __restrict__ part, int S, 
   const int lane = threadIdx.x & 63;
   const int c = blk * 128 + 2 * lane;
   float v0 = 0.f, v1 = 0.f;
-  for (int z = 0; z < S; ++z) {
-    const float* p = part + ((size_t)z * M + row) * OC + c;
-    v0 = v0 + p[0];
-    v1 = v1 + p[1];
+  // loads issued 8 at a time so their latencies overlap; summed in z order
+  for (int z0 = 0; z0 < S; z0 += 8) {
+    float2 pv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (z0 + j < S)
+        pv[j] = *reinterpret_cast<const float2*>(part + ((size_t)(z0 + j) * M + row) * OC + c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (z0 + j < S) {
+        v0 = v0 + pv[j].x;
+        v1 = v1 + pv[j].y;
+      }
   }
   h128_wave(v0, v1);
-  y0 = (half_t)((v0 * rs) * rout_e[c]);
-  y1 = (half_t)((v1 * rs) * rout_e[c + 1]);
+  y0 = to_f16((v0 * rs) * rout_e[c]);
+  y1 = to_f16((v1 * rs) * rout_e[c + 1]);
 }
 
 // gate_up epilogue -> swiglu -> down input transform, one wave per
@@ -73,8 +82,8 @@ __global__ __launch_bounds__(64) void k_moe_mid(const float* __restrict__ part, 
   float v1 = (float)h1 * ri[1];
   h128_wave(v0, v1);
   uint16_t* o = xh2 + (size_t)row * I + c;
-  o[0] = __builtin_bit_cast(uint16_t, (half_t)(v0 * rs));
-  o[1] = __builtin_bit_cast(uint16_t, (half_t)(v1 * rs));
+  o[0] = __builtin_bit_cast(uint16_t, to_f16(v0 * rs));
+  o[1] = __builtin_bit_cast(uint16_t, to_f16(v1 * rs));
 }
 
 // down epilogue + weighted combine: y[t] = f16(sum_s f32(d16[t*k+s]) * f32(f16(score)))

@@ -105,7 +105,7 @@ class EschaMoEExperts(torch.nn.Module):
         self._lut = envs.use_lut()
         self._exact = envs.use_exact()
         self._block_r = envs.block_r_pin()
-        self._ws = None
+        self._ws = {}
 
     def _rows(self, t: int, ids: torch.Tensor):
         """Token-major rows: slot s of token t is row t*k + s (qwen3_5_moe.py:97-101)."""
@@ -143,9 +143,13 @@ class EschaMoEExperts(torch.nn.Module):
         if self._exact:
             return self._forward_exact(x, ids, scores)
         t, h = x.shape
-        need = ops.moe_expert_path_workspace(t, self.top_k, self.num_experts, h, self._inter)
-        if self._ws is None or self._ws.numel() < need or self._ws.device != x.device:
-            self._ws = torch.empty(max(need, 4), dtype=torch.uint8, device=x.device)
+        # one zero-initialised workspace per token count: the one-launch path
+        # keeps its counters there and leaves them zero after every call
+        key = (t, x.device)
+        ws = self._ws.get(key)
+        if ws is None:
+            need = ops.moe_expert_path_workspace(t, self.top_k, self.num_experts, h, self._inter)
+            ws = self._ws[key] = torch.zeros(max(need, 4), dtype=torch.uint8, device=x.device)
         gu, dn = self._gu, self._dn
         return ops.moe_expert_path(x, ids, scores, gu.code, gu.rin, gu.rout, gu.K, dn.code,
-                                   dn.rin, dn.rout, dn.K, lut=self._lut, ws=self._ws)
+                                   dn.rin, dn.rout, dn.K, lut=self._lut, ws=ws)

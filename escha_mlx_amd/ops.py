@@ -240,7 +240,9 @@ def moe_expert_path(x, ids, scores, gu_code, gu_rin, gu_rout, K_gu, dn_code, dn_
         raise ValueError("ids must be int32 and scores float32")
     nbytes = moe_expert_path_workspace(t, k, E, h, I)
     if ws is None:
-        ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=x.device)
+        # the one-launch path's counters must start at zero; the kernel leaves
+        # them zero, so a workspace is reusable for calls of the same shape
+        ws = torch.zeros(max(nbytes, 4), dtype=torch.uint8, device=x.device)
     y = out if out is not None else torch.empty((t, h), dtype=torch.float16, device=x.device)
     _lib.call("esc_moe_expert_path", _ptr(x), _ptr(ids), _ptr(scores), t, k, E, h, I,
               _ptr(_as_u32(gu_code)), _ptr(gu_rin), _ptr(gu_rout), K_gu,
@@ -267,3 +269,10 @@ def moe_combine(d16: torch.Tensor, scores: torch.Tensor, top_k: int) -> torch.Te
     y = torch.empty((t, h), dtype=torch.float16, device=d16.device)
     _lib.call("esc_moe_combine", _ptr(d16), _ptr(scores), t, top_k, h, _ptr(y), _stream())
     return y
+
+
+def moe_status(ws: torch.Tensor, T: int, top_k: int, H: int, I: int) -> int:
+    """1 if a one-launch expert path using ``ws`` ever hit its bounded wait (synchronises)."""
+    flag = ctypes.c_int32(0)
+    _lib.call("esc_moe_status", _ptr(ws), ws.numel(), T, top_k, H, I, ctypes.byref(flag), _stream())
+    return int(flag.value)

@@ -135,6 +135,13 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
                         int K_dn, int use_lut, uint16_t* y, void* ws, size_t ws_bytes,
                         void* stream);
 
+/* Diagnostic: *host_flag = 1 if the one-launch expert path run with this
+ * workspace ever hit its bounded wait (never expected: the kernel's work
+ * claiming guarantees progress).  Synchronises the stream.  No counterpart in
+ * the reference (its expert path has no cross-workgroup hand-off). */
+int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int I,
+                   int32_t* host_flag, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
