@@ -45,6 +45,8 @@ SIGNATURES = {
     "esc_moe_combine": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "esc_moe_expert_path_workspace": (_Z, [_I, _I, _I, _I, _I]),
     "esc_moe_status": (_I, [_P, _Z, _I, _I, _I, _I, _P, _P]),
+    "esc_moe_layers_workspace": (_Z, [_I, _I, _I, _I, _I]),
+    "esc_moe_expert_path_layers": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
     "esc_moe_expert_path": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _P,
                                  _I, _I, _P, _P, _Z, _P]),
 }

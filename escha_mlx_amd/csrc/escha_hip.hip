@@ -348,46 +348,93 @@ MoePlan moe_plan(int T, int top_k, int H, int I, int K_gu, int K_dn) {
   return p;
 }
 
-// One-launch path (fused.hpp) for decode-sized row counts.
+// One-launch path (fused.hpp).  Latency mode: small items over the whole GPU
+// for one token-layer; throughput mode: large items for many token-layers.
 constexpr int kFusedMaxRows = 64;
 
 struct FusedPlan {
-  int M, NB, NKC, NCP, nA, nB, grid;
+  int L, M, NB, NKC, NKB, NCP, nA, nB, grid;
   size_t off_pa, off_pb, off_int, total;
   int n_int;
 };
 
+// H/(16*KTA) <= 62: one polling wave reads the counter and every claim flag
+// at once; top_k <= 32: the combine stages one row of d16 per slot in LDS.
 bool fused_eligible(int T, int top_k, int H, int I) {
-  return T * top_k <= kFusedMaxRows && H % 256 == 0 && I % 128 == 0;
+  return T * top_k <= kFusedMaxRows && top_k <= 32 && H % 256 == 0 && H / 128 <= 62 &&
+         I % 128 == 0;
 }
 
-FusedPlan fused_plan(int T, int top_k, int H, int I) {
+FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput) {
+  const int kta = throughput ? 32 : 8, ktb = throughput ? 32 : 4;
   FusedPlan f;
+  f.L = L;
   f.M = T * top_k;
   f.NB = I / 128;
-  f.NKC = H / 256;
+  f.NKC = std::max(1, H / (16 * kta));
+  f.NKB = std::max(1, I / (16 * ktb));
   f.NCP = H / 256;
   f.nA = f.M * f.NB * f.NKC;
-  f.nB = f.M * f.NCP * f.NB;
-  f.grid = std::min(std::max(f.nA, f.nB), 2048);
+  f.nB = f.M * f.NCP * f.NKB;
+  f.grid = throughput ? std::min(L * std::max(f.nA, f.nB), 1024)
+                      : std::min(std::max(f.nA, f.nB), 2048);
   auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
   f.off_pa = 0;
-  f.off_pb = al((size_t)f.nA * 256 * 4);
-  f.off_int = f.off_pb + al((size_t)f.nB * 256 * 4);
-  f.n_int = f.M * f.NB + f.nA + T * f.NCP + 2;
+  f.off_pb = al((size_t)L * f.nA * 256 * 4);
+  f.off_int = f.off_pb + al((size_t)L * f.nB * 256 * 4);
+  f.n_int = L * (f.M * f.NB + f.nA + T * f.NCP) + 2;
   f.total = f.off_int + al((size_t)f.n_int * 4);
   return f;
 }
 
-template <int KG, int KD>
-int launch_fused(const esc::FusedMoe& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((esc::k_moe_fused<KG, KD>), dim3(grid), dim3(esc::kFusedThreads), 0, s, p);
+// Throughput mode needs the item sizes to divide the shapes.
+bool throughput_ok(int H, int I) { return H % 512 == 0 && I % 512 == 0; }
+
+esc::FusedMoe fused_args(const FusedPlan& f, void* ws, int T, int top_k, int H, int I) {
+  char* w = static_cast<char*>(ws);
+  int* ints = reinterpret_cast<int*>(w + f.off_int);
+  esc::FusedMoe p{};
+  p.partA = reinterpret_cast<float*>(w + f.off_pa);
+  p.partB = reinterpret_cast<float*>(w + f.off_pb);
+  p.cntA = ints;
+  p.claimA = p.cntA + (size_t)f.L * f.M * f.NB;
+  p.cntB = p.claimA + (size_t)f.L * f.nA;
+  p.done = p.cntB + (size_t)f.L * T * f.NCP;
+  p.err = p.done + 1;
+  p.L = f.L;
+  p.T = T;
+  p.top_k = top_k;
+  p.H = H;
+  p.I = I;
+  p.NB = f.NB;
+  p.NKC = f.NKC;
+  p.NKB = f.NKB;
+  p.NCP = f.NCP;
+  p.nA = f.nA;
+  p.nB = f.nB;
+  return p;
+}
+
+template <int KG, int KD, bool TP>
+int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
+  if constexpr (TP)
+    hipLaunchKernelGGL((esc::k_moe_fused<KG, KD, 32, 32, false>), dim3(grid),
+                       dim3(esc::kFusedThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((esc::k_moe_fused<KG, KD, 8, 4, true>), dim3(grid),
+                       dim3(esc::kFusedThreads), 0, s, p);
   return launched("k_moe_fused");
+}
+
+template <bool TP>
+int launch_fused(const esc::FusedMoe& p, int K_gu, int K_dn, int grid, hipStream_t s) {
+  if (K_gu == 2)
+    return K_dn == 2 ? launch_fused_k<2, 2, TP>(p, grid, s) : launch_fused_k<2, 3, TP>(p, grid, s);
+  return K_dn == 2 ? launch_fused_k<3, 2, TP>(p, grid, s) : launch_fused_k<3, 3, TP>(p, grid, s);
 }
 }  // namespace
 
 extern "C" {
-
 size_t esc_moe_expert_path_workspace(int T, int top_k, int E, int H, int I) {
   (void)E;
   if (T <= 0 || top_k <= 0 || H <= 0 || I <= 0) return 0;
@@ -395,7 +442,7 @@ size_t esc_moe_expert_path_workspace(int T, int top_k, int E, int H, int I) {
   size_t a = moe_plan(T, top_k, H, I, 2, 2).total, b = moe_plan(T, top_k, H, I, 3, 3).total;
   size_t c = moe_plan(T, top_k, H, I, 2, 3).total, d = moe_plan(T, top_k, H, I, 3, 2).total;
   size_t m = std::max(std::max(a, b), std::max(c, d));
-  if (fused_eligible(T, top_k, H, I)) m = std::max(m, fused_plan(T, top_k, H, I).total);
+  if (fused_eligible(T, top_k, H, I)) m = std::max(m, fused_plan(1, T, top_k, H, I, false).total);
   return m;
 }
 
@@ -404,7 +451,7 @@ int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int
   ESC_REQUIRE(ws && host_flag, "null pointer");
   *host_flag = 0;
   if (!fused_eligible(T, top_k, H, I)) return ESC_OK;
-  const FusedPlan f = fused_plan(T, top_k, H, I);
+  const FusedPlan f = fused_plan(1, T, top_k, H, I, false);
   ESC_REQUIRE(ws_bytes >= f.total, "workspace smaller than the plan");
   const int32_t* err = reinterpret_cast<const int32_t*>(static_cast<const char*>(ws) + f.off_int) +
                        (f.n_int - 1);
@@ -429,41 +476,13 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
   ESC_REQUIRE(T >= 0, "negative token count");
   if (T == 0) return ESC_OK;
   if (fused_eligible(T, top_k, H, I)) {
-    const FusedPlan f = fused_plan(T, top_k, H, I);
+    const FusedPlan f = fused_plan(1, T, top_k, H, I, false);
     if (!ws || ws_bytes < f.total)
       return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, f.total);
-    char* w = static_cast<char*>(ws);
-    int* ints = reinterpret_cast<int*>(w + f.off_int);
-    esc::FusedMoe p{};
-    p.x = x;
-    p.ids = ids;
-    p.scores = scores;
-    p.gu_code = gu_code;
-    p.gu_rin = gu_rin;
-    p.gu_rout = gu_rout;
-    p.dn_code = dn_code;
-    p.dn_rin = dn_rin;
-    p.dn_rout = dn_rout;
-    p.y = y;
-    p.partA = reinterpret_cast<float*>(w + f.off_pa);
-    p.partB = reinterpret_cast<float*>(w + f.off_pb);
-    p.cntA = ints;
-    p.claimA = p.cntA + f.M * f.NB;
-    p.cntB = p.claimA + f.nA;
-    p.done = p.cntB + T * f.NCP;
-    p.err = p.done + 1;
-    p.T = T;
-    p.top_k = top_k;
-    p.H = H;
-    p.I = I;
-    p.NB = f.NB;
-    p.NKC = f.NKC;
-    p.NCP = f.NCP;
-    p.nA = f.nA;
-    p.nB = f.nB;
-    hipStream_t s = S(stream);
-    if (K_gu == 2) return K_dn == 2 ? launch_fused<2, 2>(p, f.grid, s) : launch_fused<2, 3>(p, f.grid, s);
-    return K_dn == 2 ? launch_fused<3, 2>(p, f.grid, s) : launch_fused<3, 3>(p, f.grid, s);
+    esc::FusedMoe p = fused_args(f, ws, T, top_k, H, I);
+    p.l0 = esc::MoeLayer{x, ids, scores, gu_code, gu_rin, gu_rout, dn_code, dn_rin, dn_rout, y};
+    p.layers = nullptr;
+    return launch_fused<false>(p, K_gu, K_dn, f.grid, S(stream));
   }
   const MoePlan p = moe_plan(T, top_k, H, I, K_gu, K_dn);
   if (!ws || ws_bytes < p.total)
@@ -492,6 +511,34 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
   hipLaunchKernelGGL(esc::k_moe_combine, dim3(H / 128, T), dim3(64), 0, s, p2, p.S2, p.M, H, ids,
                      scores, top_k, dn_rout, rs, y);
   return launched("k_moe_combine");
+}
+
+size_t esc_moe_layers_workspace(int L, int T, int top_k, int H, int I) {
+  if (L <= 0 || T <= 0 || top_k <= 0 || !fused_eligible(T, top_k, H, I) || !throughput_ok(H, I))
+    return 0;
+  return fused_plan(L, T, top_k, H, I, true).total;
+}
+
+int esc_moe_expert_path_layers(const esc_moe_layer* layers, int L, int T, int top_k, int E, int H,
+                               int I, int K_gu, int K_dn, void* ws, size_t ws_bytes,
+                               void* stream) {
+  static_assert(sizeof(esc_moe_layer) == sizeof(esc::MoeLayer), "layer record layout");
+  ESC_REQUIRE(layers, "null pointer");
+  ESC_REQUIRE(L >= 0 && T >= 0, "negative size");
+  ESC_REQUIRE(E > 0 && top_k >= 1 && top_k <= E, "bad E=%d / top_k=%d", E, top_k);
+  if (int rc = check_proj(K_gu, H, 2 * I)) return rc;
+  if (int rc = check_proj(K_dn, I, H)) return rc;
+  ESC_REQUIRE(fused_eligible(T, top_k, H, I) && throughput_ok(H, I),
+              "multi-layer expert path needs T*top_k <= %d, top_k <= 32, H and I multiples of "
+              "512, H <= 7936 (got T=%d top_k=%d H=%d I=%d)",
+              kFusedMaxRows, T, top_k, H, I);
+  if (L == 0 || T == 0) return ESC_OK;
+  const FusedPlan f = fused_plan(L, T, top_k, H, I, true);
+  if (!ws || ws_bytes < f.total)
+    return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, f.total);
+  esc::FusedMoe p = fused_args(f, ws, T, top_k, H, I);
+  p.layers = reinterpret_cast<const esc::MoeLayer*>(layers);
+  return launch_fused<true>(p, K_gu, K_dn, f.grid, S(stream));
 }
 
 }  // extern "C"

@@ -1,21 +1,35 @@
 // One-launch routed-expert path (replaces the ~10 launches of
-// EschaSparseMoeBlock._expert_path, escha_mlx/models/qwen3_5_moe.py:207-253).
+// EschaSparseMoeBlock._expert_path, escha_mlx/models/qwen3_5_moe.py:207-253),
+// for one token-layer or for a list of independent token-layers.
 //
 // Work is split into two kinds of items, each one block of 4 waves:
-//   gate_up item (r, b, kc): row r, output columns gate[128b, 128b+128) and
-//     up[I+128b, I+128b+128), input rows [256kc, 256kc+256).  The block
-//     input-transforms its own 256 inputs of x (no global hand-off), decodes
-//     and multiplies 16 tiles x 16 kt, and writes 256 float32 partials.
-//   down item (r, p, kb): row r, output columns [256p, 256p+256), input rows
-//     [128kb, 128kb+128) = one 128-block of h.  It waits until all gate_up
-//     items of (r, b=kb) are published, sums their partials in fixed kc order,
-//     applies the gate_up output transform, swiglu and the down input
-//     transform to get its 128 inputs, then decodes and multiplies 16 tiles x
-//     8 kt and writes 256 float32 partials.  The last down item to finish a
-//     (token, 256-column) tile sums every slot's partials in fixed order,
-//     transforms them and combines the slots in slot order (f16(score)
-//     weights, float32 sum, one f16 rounding): no float atomics anywhere, the
-//     result is deterministic.
+//   gate_up item (l, r, b, kc): layer l, row r, output columns
+//     gate[128b, 128b+128) and up[I+128b, I+128b+128), input rows
+//     [16*KTA*kc, 16*KTA*(kc+1)).  The block input-transforms its own inputs of
+//     x (no global hand-off), decodes and multiplies 16 tiles x KTA kt, and
+//     publishes 256 float32 partials.
+//   down item (l, r, p, kb): row r, output columns [256p, 256p+256), input rows
+//     [16*KTB*kb, 16*KTB*(kb+1)) of h.  It waits until every gate_up item of
+//     the h-blocks it reads is published, sums their partials in fixed kc
+//     order, applies the gate_up output transform, swiglu and the down input
+//     transform to get its inputs, decodes and multiplies 16 tiles x KTB kt and
+//     publishes 256 partials.  The last down item to finish a (token,
+//     256-column) tile sums every slot's partials in fixed order, transforms
+//     them and combines the slots in slot order (f16(score) weights, float32
+//     sum, one f16 rounding).  No float atomics: the result is deterministic.
+//
+// Two item sizes: small items (KTA=8, KTB=4) spread one token-layer over the
+// whole GPU for latency; large items (KTA=32, KTB=32) cut the partial traffic
+// when many token-layers share a launch (throughput).  In the single-layer
+// mode each block requests its first down item's code before doing anything
+// else, so that code is in registers by the time the item's inputs are ready.
+//
+// Hand-off across the GPU's XCDs (each has its own L2): partials are written
+// and read with agent-scope monotonic atomics, which the gfx9 memory model
+// keeps coherent device-wide without L2 write-back / invalidate; a producer
+// waits for its stores to complete (s_waitcnt vmcnt(0)) before the counter
+// increment that publishes them, and a consumer reads them only after
+// observing the counter.
 //
 // Forward progress: blocks never wait on a block that has not started.  Every
 // gate_up item is claimed (integer CAS) by the block that runs it; a down item
@@ -33,45 +47,63 @@ namespace esc {
 __device__ __forceinline__ int ld_relaxed(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ int add_acq_rel(int* p, int v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ int add_relaxed(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ bool claim(int* p) {
   int expected = 0;
-  return __hip_atomic_compare_exchange_strong(p, &expected, 1, __ATOMIC_ACQ_REL,
+  return __hip_atomic_compare_exchange_strong(p, &expected, 1, __ATOMIC_RELAXED,
                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void fence_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
-__device__ __forceinline__ void fence_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 ld_coherent2(const float* p) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__builtin_bit_cast(float, (uint32_t)v),
+                     __builtin_bit_cast(float, (uint32_t)(v >> 32)));
+}
+// this wave's global stores (and loads) have completed
+__device__ __forceinline__ void wait_vm() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-struct FusedMoe {
-  const uint16_t* x;
-  const int* ids;
-  const float* scores;
+// One token-layer of routed experts (all device pointers).
+struct MoeLayer {
+  const uint16_t* x;      // [T][H] f16
+  const int* ids;         // [T*k]
+  const float* scores;    // [T*k]
   const uint32_t* gu_code;
   const float* gu_rin;
   const float* gu_rout;
   const uint32_t* dn_code;
   const float* dn_rin;
   const float* dn_rout;
-  uint16_t* y;
-  float* partA;  // [nA][256]
-  float* partB;  // [nB][256]
-  int* cntA;     // [M*NB]  published gate_up items per (row, h-block)
-  int* claimA;   // [nA]
-  int* cntB;     // [T*NCP] finished down items per (token, column pair)
+  uint16_t* y;            // [T][H] f16
+};
+
+struct FusedMoe {
+  MoeLayer l0;              // the layer when `layers` is null
+  const MoeLayer* layers;   // [L] device array for multi-layer launches
+  float* partA;  // [L][nA][256]
+  float* partB;  // [L][nB][256]
+  int* cntA;     // [L][M*NB]  published gate_up items per (row, h-block)
+  int* claimA;   // [L][nA]
+  int* cntB;     // [L][T*NCP] finished down items per (token, column pair)
   int* done;     // [1]
   int* err;      // [1] sticky: a spin bound was hit
-  int T, top_k, H, I;
-  int NB;   // I / 128
-  int NKC;  // H / 256
-  int NCP;  // H / 256
-  int nA, nB;
+  int L, T, top_k, H, I;
+  int NB;   // I / 128        h-blocks
+  int NKC;  // H / (16*KTA)   gate_up items per (row, h-block), <= 62
+  int NKB;  // I / (16*KTB)   down items per (row, column pair)
+  int NCP;  // H / 256        column pairs
+  int nA, nB;  // items per layer
+  __device__ __forceinline__ const MoeLayer& layer(int l) const { return layers ? layers[l] : l0; }
 };
 
 constexpr int kFusedThreads = 256;
-constexpr int kSpinLimit = 1 << 11;  // outer polls of 64 (x s_sleep) before giving up
-enum { kReady = -1, kWait = -2, kTimeout = -3 };
+constexpr int kSpinLimit = 1 << 18;  // polls (one round trip + s_sleep each) before giving up
+enum { kReady = -1, kTimeout = -3 };
 
 // Inverse of Geo<K>::col: tile column c -> (lane within tile, column slot).
 template <int K>
@@ -85,37 +117,60 @@ __device__ __forceinline__ void col_owner(int c, int& q, int& ci) {
   }
 }
 
-// 16 tiles x nkt kt of one stream: float32 partial of the item's 256 columns
-// (item column j = 16 * item_tile + tile_col) written to dst.  nt_of(it) maps
-// the item's tile 0..15 to the stream's tile column.
-template <int K, typename NtFn>
-__device__ __forceinline__ void item_gemv(const uint32_t* __restrict__ code_e, int TN, int kt_base,
-                                          int nkt, NtFn nt_of, const uint32_t* s_x,
-                                          float (*s_red)[64][4], float* __restrict__ dst) {
+// One item = 16 tiles x NKT kt of one stream.  Waves split the tiles into
+// 16/TPW groups and the kt range among the WPG waves of a group; each lane
+// holds its NSTEP kt-steps of code in VGPRs.
+template <int K, int NKT>
+struct ItemGeo {
+  static constexpr int NG = 16 / Geo<K>::TPW;
+  static constexpr int WPG = 4 / NG;
+  static constexpr int NSTEP = NKT / WPG;
+};
+
+template <int K, int NKT>
+struct ItemCode {
+  LaneWords<K> w[ItemGeo<K, NKT>::NSTEP];
+};
+
+template <int K, int NKT, typename NtFn>
+__device__ __forceinline__ ItemCode<K, NKT> load_item(const uint32_t* __restrict__ code_e, int TN,
+                                                      int kt_base, NtFn nt_of) {
   using G = Geo<K>;
-  constexpr int NG = 16 / G::TPW;  // tile groups per item
-  constexpr int WPG = 4 / NG;      // waves per group
+  using IG = ItemGeo<K, NKT>;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int g = wave / WPG, wi = wave % WPG;
+  const int g = wave / IG::WPG, wi = wave % IG::WPG;
   const int q = lane % G::LPT, i = lane / G::LPT;
-  const int nt = nt_of(g * G::TPW + i);
-  const int src = i * G::LPT + (q + G::LPT - 1) % G::LPT;
-  const int kper = nkt / WPG, k0 = wi * kper;
   const size_t kstride = (size_t)TN * (8 * K);
-  const uint32_t* lp = code_e + (size_t)nt * (8 * K) + q * G::WPL + (size_t)(kt_base + k0) * kstride;
+  const uint32_t* lp = code_e + (size_t)nt_of(g * G::TPW + i) * (8 * K) + q * G::WPL +
+                       (size_t)(kt_base + wi * IG::NSTEP) * kstride;
+  ItemCode<K, NKT> c;
+#pragma unroll
+  for (int k = 0; k < IG::NSTEP; ++k) c.w[k] = load_lane_words<K>(lp + (size_t)k * kstride);
+  return c;
+}
+
+// Decode + multiply the item (inputs: 8 f16-pair words per kt in s_x) and
+// publish its 256 float32 column partials to dst (coherent stores).
+template <int K, int NKT>
+__device__ __forceinline__ void compute_item(const ItemCode<K, NKT>& code, const uint32_t* s_x,
+                                             float (*s_red)[64][4], float* __restrict__ dst) {
+  using G = Geo<K>;
+  using IG = ItemGeo<K, NKT>;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wi = wave % IG::WPG;
+  const int q = lane % G::LPT, i = lane / G::LPT;
+  const int src = i * G::LPT + (q + G::LPT - 1) % G::LPT;
   float acc[G::NCOL];
 #pragma unroll
   for (int c = 0; c < G::NCOL; ++c) acc[c] = 0.f;
-  LaneWords<K> cur = load_lane_words<K>(lp);
-  for (int k = 0; k < kper; ++k) {
-    LaneWords<K> nxt = cur;
-    if (k + 1 < kper) nxt = load_lane_words<K>(lp + (size_t)(k + 1) * kstride);
+#pragma unroll
+  for (int k = 0; k < IG::NSTEP; ++k) {
+    const int kl = wi * IG::NSTEP + k;
     uint32_t xw[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) xw[j] = s_x[8 * (k0 + k) + j];
-    const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
-    fast_tile<K, false>(cur, wprev, xw, nullptr, acc);
-    cur = nxt;
+    for (int j = 0; j < 8; ++j) xw[j] = s_x[8 * kl + j];
+    const uint32_t wprev = __shfl(code.w[k].w[G::WPL - 1], src);
+    fast_tile<K, false>(code.w[k], wprev, xw, nullptr, acc);
   }
 #pragma unroll
   for (int c = 0; c < G::NCOL; ++c) s_red[wave][lane][c] = acc[c];
@@ -127,186 +182,282 @@ __device__ __forceinline__ void item_gemv(const uint32_t* __restrict__ code_e, i
     col_owner<K>(c, qq, ci);
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < WPG; ++w) v = v + s_red[gg * WPG + w][ii * G::LPT + qq][ci];
-    dst[j] = v;
+    for (int w = 0; w < IG::WPG; ++w) v = v + s_red[gg * IG::WPG + w][ii * G::LPT + qq][ci];
+    st_coherent(dst + j, v);
   }
+  wait_vm();
+  __syncthreads();
 }
 
 __device__ __forceinline__ uint32_t pack2(half_t a, half_t b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-template <int K>
-__device__ void run_gate_up(const FusedMoe& p, int a, uint32_t* s_x, float (*s_red)[64][4]) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+template <int K, int KTA>
+__device__ __forceinline__ ItemCode<K, KTA> load_gate_up(const FusedMoe& p, int l, int a) {
+  const MoeLayer& L = p.layer(l);
   const int kc = a % p.NKC, rb = a / p.NKC, b = rb % p.NB, r = rb / p.NB;
-  const int t = r / p.top_k, e = p.ids[r];
-  const int TK = p.H / 16, TN = 2 * p.I / 16;
-  if (wave < 2) {
-    const int c = 256 * kc + 128 * wave + 2 * lane;
-    const uint16_t* xr = p.x + (size_t)t * p.H + c;
-    const float* ri = p.gu_rin + (size_t)e * p.H + c;
+  const int TK = p.H / 16, TN = 2 * p.I / 16, half_tn = p.I / 16;
+  return load_item<K, KTA>(L.gu_code + (size_t)L.ids[r] * TK * TN * (8 * K), TN, KTA * kc,
+                           [&](int it) { return it < 8 ? 8 * b + it : half_tn + 8 * b + (it - 8); });
+}
+
+template <int K, int KTB>
+__device__ __forceinline__ ItemCode<K, KTB> load_down(const FusedMoe& p, int l, int bi) {
+  const MoeLayer& L = p.layer(l);
+  const int kb = bi % p.NKB, cp = (bi / p.NKB) % p.NCP, r = bi / p.NKB / p.NCP;
+  const int TK = p.I / 16, TN = p.H / 16;
+  return load_item<K, KTB>(L.dn_code + (size_t)L.ids[r] * TK * TN * (8 * K), TN, KTB * kb,
+                           [&](int it) { return 16 * cp + it; });
+}
+
+// gate_up item a of layer l with its code already in flight: transform the
+// item's 16*KTA inputs (one wave per 128-block), decode + multiply, publish.
+template <int K, int KTA>
+__device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, KTA>& code,
+                            uint32_t* s_x, float (*s_red)[64][4]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const MoeLayer& L = p.layer(l);
+  const int kc = a % p.NKC, rb = a / p.NKC, b = rb % p.NB, r = rb / p.NB;
+  const int t = r / p.top_k, e = L.ids[r];
+  if (wave < KTA / 8) {
+    const int c = 16 * KTA * kc + 128 * wave + 2 * lane;
+    const uint16_t* xr = L.x + (size_t)t * p.H + c;
+    const float* ri = L.gu_rin + (size_t)e * p.H + c;
     float v0 = (float)__builtin_bit_cast(half_t, xr[0]) * ri[0];
     float v1 = (float)__builtin_bit_cast(half_t, xr[1]) * ri[1];
     h128_wave(v0, v1);
     s_x[64 * wave + lane] = pack2(to_f16(v0 * kRS), to_f16(v1 * kRS));
   }
   __syncthreads();
-  const int half_tn = p.I / 16;
-  item_gemv<K>(p.gu_code + (size_t)e * TK * TN * (8 * K), TN, 16 * kc, 16,
-               [&](int it) { return it < 8 ? 8 * b + it : half_tn + 8 * b + (it - 8); }, s_x, s_red,
-               p.partA + (size_t)a * 256);
-  fence_release();
-  __syncthreads();
-  if (threadIdx.x == 0) add_acq_rel(&p.cntA[r * p.NB + b], 1);
+  compute_item<K, KTA>(code, s_x, s_red, p.partA + ((size_t)l * p.nA + a) * 256);
+  if (threadIdx.x == 0) add_relaxed(&p.cntA[(size_t)l * p.T * p.top_k * p.NB + r * p.NB + b], 1);
 }
 
-// h-block kb of row r -> the 128 down inputs (f16 pairs) in s_x[0..63].
-__device__ void down_inputs(const FusedMoe& p, int r, int kb, uint32_t* s_x) {
+// h-block kb of row r (layer l) -> its 128 down inputs (f16 pairs) in s_x[0..63].
+__device__ void down_inputs(const FusedMoe& p, int l, int r, int kb, uint32_t* s_x) {
   const int lane = threadIdx.x & 63;
-  const int e = p.ids[r];
-  const float* base = p.partA + (size_t)(r * p.NB + kb) * p.NKC * 256;
+  const MoeLayer& L = p.layer(l);
+  const int e = L.ids[r];
+  const float* base =
+      p.partA + ((size_t)l * p.nA + (size_t)(r * p.NB + kb) * p.NKC) * 256 + 2 * lane;
   float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
-  for (int kc = 0; kc < p.NKC; ++kc) {
-    const float2 gv = *reinterpret_cast<const float2*>(base + (size_t)kc * 256 + 2 * lane);
-    const float2 uv = *reinterpret_cast<const float2*>(base + (size_t)kc * 256 + 128 + 2 * lane);
-    g0 = g0 + gv.x;
-    g1 = g1 + gv.y;
-    u0 = u0 + uv.x;
-    u1 = u1 + uv.y;
+  for (int kc0 = 0; kc0 < p.NKC; kc0 += 16) {
+    float2 gv[16], uv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (kc0 + j < p.NKC) {
+        gv[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256);
+        uv[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256 + 128);
+      }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (kc0 + j < p.NKC) {
+        g0 = g0 + gv[j].x;
+        g1 = g1 + gv[j].y;
+        u0 = u0 + uv[j].x;
+        u1 = u1 + uv[j].y;
+      }
   }
   h128_wave(g0, g1);
   h128_wave(u0, u1);
   const int cg = 128 * kb + 2 * lane, cu = p.I + cg;
-  const float* ro = p.gu_rout + (size_t)e * 2 * p.I;
+  const float* ro = L.gu_rout + (size_t)e * 2 * p.I;
   const half_t h0 = swiglu1(to_f16((g0 * kRS) * ro[cg]), to_f16((u0 * kRS) * ro[cu]));
   const half_t h1 = swiglu1(to_f16((g1 * kRS) * ro[cg + 1]), to_f16((u1 * kRS) * ro[cu + 1]));
-  const float* ri = p.dn_rin + (size_t)e * p.I + cg;
+  const float* ri = L.dn_rin + (size_t)e * p.I + cg;
   float v0 = (float)h0 * ri[0];
   float v1 = (float)h1 * ri[1];
   h128_wave(v0, v1);
   s_x[lane] = pack2(to_f16(v0 * kRS), to_f16(v1 * kRS));
 }
 
-// Last down item of (token t, column pair cp): transform every slot and combine.
-__device__ void combine_tile(const FusedMoe& p, int t, int cp) {
+// Last down item of (layer l, token t, column pair cp): every slot's 256
+// columns are summed (fixed kb order) and transformed to d16 in LDS by the 4
+// waves (slot s on wave s % 4, two slots' loads issued together), then each
+// thread combines one column over the slots in slot order.
+__device__ void combine_tile(const FusedMoe& p, int l, int t, int cp, uint16_t (*s_d)[256]) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (wave >= 2) return;
-  const int col = 256 * cp + 128 * wave + 2 * lane;
-  float a0 = 0.f, a1 = 0.f;
-  for (int s = 0; s < p.top_k; ++s) {
-    const int row = t * p.top_k + s, e = p.ids[row];
-    const float* pb = p.partB + (size_t)(row * p.NCP + cp) * p.NB * 256 + 128 * wave + 2 * lane;
-    float v0 = 0.f, v1 = 0.f;
-    for (int kb = 0; kb < p.NB; ++kb) {
-      const float2 pv = *reinterpret_cast<const float2*>(pb + (size_t)kb * 256);
-      v0 = v0 + pv.x;
-      v1 = v1 + pv.y;
+  const MoeLayer& L = p.layer(l);
+  for (int s0 = wave; s0 < p.top_k; s0 += 8) {
+    float v[2][2][2] = {};
+    for (int kb0 = 0; kb0 < p.NKB; kb0 += 8) {
+      float2 pv[2][2][8];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int s = s0 + 4 * u;
+        if (s >= p.top_k) continue;
+        const float* pb = p.partB +
+                          ((size_t)l * p.nB + (size_t)((t * p.top_k + s) * p.NCP + cp) * p.NKB) * 256 +
+                          2 * lane;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (kb0 + j < p.NKB) {
+            pv[u][0][j] = ld_coherent2(pb + (size_t)(kb0 + j) * 256);
+            pv[u][1][j] = ld_coherent2(pb + (size_t)(kb0 + j) * 256 + 128);
+          }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (s0 + 4 * u < p.top_k && kb0 + j < p.NKB) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              v[u][h][0] = v[u][h][0] + pv[u][h][j].x;
+              v[u][h][1] = v[u][h][1] + pv[u][h][j].y;
+            }
+          }
     }
-    h128_wave(v0, v1);
-    const float* ro = p.dn_rout + (size_t)e * p.H + col;
-    const half_t d0 = to_f16((v0 * kRS) * ro[0]);
-    const half_t d1 = to_f16((v1 * kRS) * ro[1]);
-    const float w = (float)(half_t)p.scores[row];
-    a0 = a0 + (float)d0 * w;
-    a1 = a1 + (float)d1 * w;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int s = s0 + 4 * u;
+      if (s >= p.top_k) continue;
+      const int e = L.ids[t * p.top_k + s];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        h128_wave(v[u][h][0], v[u][h][1]);
+        const int col = 256 * cp + 128 * h + 2 * lane;
+        const float* ro = L.dn_rout + (size_t)e * p.H + col;
+        s_d[s][128 * h + 2 * lane] = __builtin_bit_cast(uint16_t, to_f16((v[u][h][0] * kRS) * ro[0]));
+        s_d[s][128 * h + 2 * lane + 1] =
+            __builtin_bit_cast(uint16_t, to_f16((v[u][h][1] * kRS) * ro[1]));
+      }
+    }
   }
-  p.y[(size_t)t * p.H + col] = __builtin_bit_cast(uint16_t, (half_t)a0);
-  p.y[(size_t)t * p.H + col + 1] = __builtin_bit_cast(uint16_t, (half_t)a1);
+  __syncthreads();
+  const int j = threadIdx.x;
+  float a = 0.f;
+  for (int s = 0; s < p.top_k; ++s) {
+    const float w = (float)(half_t)L.scores[t * p.top_k + s];
+    a = a + (float)__builtin_bit_cast(half_t, s_d[s][j]) * w;
+  }
+  L.y[(size_t)t * p.H + 256 * cp + j] = __builtin_bit_cast(uint16_t, (half_t)a);
 }
 
-template <int K_GU, int K_DN>
-__device__ void run_down(const FusedMoe& p, int bi, uint32_t* s_x, float (*s_red)[64][4],
-                         int* s_flag) {
-  const int tid = threadIdx.x;
-  const int kb = bi % p.NB, rc = bi / p.NB, cp = rc % p.NCP, r = rc / p.NCP;
-  const int t = r / p.top_k, e = p.ids[r];
-  // wait for the gate_up items of (r, kb); run unclaimed ones ourselves
-  int* cnt = &p.cntA[r * p.NB + kb];
-  int spins = 0;
-  for (;;) {
-    if (tid == 0) {
-      int st = kWait;
-      for (int poll = 0; poll < 64 && st == kWait; ++poll) {
-        if (ld_relaxed(cnt) >= p.NKC) {
-          st = kReady;
-          break;
-        }
-        for (int kc = 0; kc < p.NKC; ++kc) {
-          const int a = (r * p.NB + kb) * p.NKC + kc;
-          if (ld_relaxed(&p.claimA[a]) == 0 && claim(&p.claimA[a])) {
-            st = a;
+// Block-uniform wait for the gate_up items of (layer l, row r, h-block kb):
+// one wave polls; an unclaimed item is claimed and returned (>= 0, the item
+// index within the layer) for the block to run.
+__device__ int wait_gate_up(const FusedMoe& p, int l, int r, int kb, int* s_flag) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave == 0) {
+    const int abase = (r * p.NB + kb) * p.NKC;
+    const int* cnt = &p.cntA[(size_t)l * p.T * p.top_k * p.NB + r * p.NB + kb];
+    int* claims = p.claimA + (size_t)l * p.nA + abase;
+    int st = kTimeout;
+    for (int spin = 0; spin < kSpinLimit; ++spin) {
+      // the counter every poll; the claim flags and the error flag only on
+      // every 32nd (they change rarely, and each is a device-coherent load)
+      const bool full = (spin & 31) == 0;
+      int v = full ? 0 : 1;
+      if (lane == 0)
+        v = ld_relaxed(cnt);
+      else if (full && lane <= p.NKC)
+        v = ld_relaxed(&claims[lane - 1]);
+      else if (full && lane == 63)
+        v = ld_relaxed(p.err);
+      else if (lane == 63)
+        v = 0;
+      if (__shfl(v, 0) >= p.NKC) {
+        st = kReady;
+        break;
+      }
+      if (__shfl(v, 63) != 0) break;  // another block timed out: give up too
+      uint64_t free_mask = __ballot(lane >= 1 && lane <= p.NKC && v == 0);
+      int got = -1;
+      if (lane == 0) {
+        while (free_mask) {
+          const int i = __builtin_ctzll(free_mask);
+          free_mask &= free_mask - 1;
+          if (claim(&claims[i - 1])) {
+            got = abase + i - 1;
             break;
           }
         }
-        if (st == kWait) __builtin_amdgcn_s_sleep(2);
       }
-      if (st == kWait && (++spins > kSpinLimit || ld_relaxed(p.err) != 0)) st = kTimeout;
-      *s_flag = st;
+      got = __shfl(got, 0);
+      if (got >= 0) {
+        st = got;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
     }
-    __syncthreads();
-    const int st = *s_flag;
-    __syncthreads();
-    if (st == kReady) break;
-    if (st >= 0) {
-      run_gate_up<K_GU>(p, st, s_x, s_red);
-      __syncthreads();
-      continue;
-    }
-    if (st == kTimeout) {
-      if (tid == 0) atomicOr(p.err, 1);
-      break;
-    }
+    if (lane == 0) *s_flag = st;
   }
-  fence_acquire();
-  if ((tid >> 6) == 0) down_inputs(p, r, kb, s_x);
   __syncthreads();
-  const int TK = p.I / 16, TN = p.H / 16;
-  item_gemv<K_DN>(p.dn_code + (size_t)e * TK * TN * (8 * K_DN), TN, 8 * kb, 8,
-                  [&](int it) { return 16 * cp + it; }, s_x, s_red, p.partB + (size_t)bi * 256);
-  fence_release();
+  const int st = *s_flag;
   __syncthreads();
-  if (tid == 0) *s_flag = (add_acq_rel(&p.cntB[t * p.NCP + cp], 1) == p.top_k * p.NB - 1);
-  __syncthreads();
-  const int last = *s_flag;
-  __syncthreads();
-  if (last) {
-    fence_acquire();
-    combine_tile(p, t, cp);
-  }
+  return st;
 }
 
-template <int K_GU, int K_DN>
+template <int KG, int KD, int KTA, int KTB, bool PRE>
 __global__ __launch_bounds__(kFusedThreads) void k_moe_fused(FusedMoe p) {
+  static_assert(KTA % 8 == 0 && KTA <= 32 && (KTB == 4 || (KTB % 8 == 0 && KTB <= 32)), "");
   __shared__ float s_red[4][64][4];
-  __shared__ uint32_t s_x[128];
+  __shared__ uint32_t s_x[256];
+  __shared__ uint16_t s_d[32][256];
   __shared__ int s_flag;
   const int tid = threadIdx.x;
-  for (int a = blockIdx.x; a < p.nA; a += gridDim.x) {
-    if (tid == 0) s_flag = claim(&p.claimA[a]);
+  const int nA_all = p.L * p.nA, nB_all = p.L * p.nB;
+  const int M = p.T * p.top_k;
+
+  // single-layer latency mode: the block's first down item's code is
+  // requested now and used after its inputs are ready
+  const int g0 = blockIdx.x;
+  ItemCode<KD, KTB> code0{};
+  if (PRE && g0 < nB_all) code0 = load_down<KD, KTB>(p, g0 / p.nB, g0 % p.nB);
+
+  for (int ga = blockIdx.x; ga < nA_all; ga += gridDim.x) {
+    const int l = ga / p.nA, a = ga % p.nA;
+    const auto code = load_gate_up<KG, KTA>(p, l, a);  // in flight while the claim resolves
+    if (tid == 0) s_flag = claim(&p.claimA[(size_t)l * p.nA + a]);
     __syncthreads();
     const int mine = s_flag;
     __syncthreads();
-    if (mine) {
-      run_gate_up<K_GU>(p, a, s_x, s_red);
-      __syncthreads();
-    }
+    if (mine) run_gate_up<KG, KTA>(p, l, a, code, s_x, s_red);
   }
-  for (int bi = blockIdx.x; bi < p.nB; bi += gridDim.x) {
-    run_down<K_GU, K_DN>(p, bi, s_x, s_red, &s_flag);
+
+  constexpr int kHB = KTB >= 8 ? KTB / 8 : 1;  // h-blocks read by one down item
+  for (int gb = blockIdx.x; gb < nB_all; gb += gridDim.x) {
+    const int l = gb / p.nB, bi = gb % p.nB;
+    const int kb = bi % p.NKB, rc = bi / p.NKB, cp = rc % p.NCP, r = rc / p.NCP;
+    const int t = r / p.top_k, hb0 = (KTB * kb) / 8;
+    const auto code = (PRE && gb == g0) ? code0 : load_down<KD, KTB>(p, l, bi);
+    bool ok = true;
+    for (int h = 0; h < kHB; ++h) {
+      int st;
+      while ((st = wait_gate_up(p, l, r, hb0 + h, &s_flag)) >= 0)
+        run_gate_up<KG, KTA>(p, l, st, load_gate_up<KG, KTA>(p, l, st), s_x, s_red);
+      ok = ok && st != kTimeout;
+    }
+    if (!ok) {
+      if (tid == 0) atomicOr(p.err, 1);
+    } else if ((tid >> 6) < kHB) {
+      down_inputs(p, l, r, hb0 + (tid >> 6), s_x + 64 * (tid >> 6));
+    }
+    __syncthreads();
+    // a 4-kt item reads the first or second half of its 128-block
+    compute_item<KD, KTB>(code, s_x + ((KTB * kb) % 8) * 8, s_red,
+                          p.partB + ((size_t)l * p.nB + bi) * 256);
+    if (tid == 0)
+      s_flag = (add_relaxed(&p.cntB[(size_t)l * p.T * p.NCP + t * p.NCP + cp], 1) ==
+                p.top_k * p.NKB - 1);
+    __syncthreads();
+    const int last = s_flag;
+    __syncthreads();
+    if (last) combine_tile(p, l, t, cp, s_d);
     __syncthreads();
   }
+
   // teardown: the last block resets the integer workspace for the next call
-  fence_release();
+  wait_vm();
   __syncthreads();
-  if (tid == 0) s_flag = (add_acq_rel(p.done, 1) == (int)gridDim.x - 1);
+  if (tid == 0) s_flag = (add_relaxed(p.done, 1) == (int)gridDim.x - 1);
   __syncthreads();
   if (s_flag) {
-    fence_acquire();
-    const int M = p.T * p.top_k;
-    for (int i = tid; i < M * p.NB; i += kFusedThreads) p.cntA[i] = 0;
-    for (int i = tid; i < p.nA; i += kFusedThreads) p.claimA[i] = 0;
-    for (int i = tid; i < p.T * p.NCP; i += kFusedThreads) p.cntB[i] = 0;
+    for (int i = tid; i < p.L * M * p.NB; i += kFusedThreads) p.cntA[i] = 0;
+    for (int i = tid; i < nA_all; i += kFusedThreads) p.claimA[i] = 0;
+    for (int i = tid; i < p.L * p.T * p.NCP; i += kFusedThreads) p.cntB[i] = 0;
     __syncthreads();
     if (tid == 0) *p.done = 0;
   }

@@ -276,3 +276,35 @@ def moe_status(ws: torch.Tensor, T: int, top_k: int, H: int, I: int) -> int:
     flag = ctypes.c_int32(0)
     _lib.call("esc_moe_status", _ptr(ws), ws.numel(), T, top_k, H, I, ctypes.byref(flag), _stream())
     return int(flag.value)
+
+
+# one esc_moe_layer record: x, ids, scores, gu_code, gu_rin, gu_rout,
+# dn_code, dn_rin, dn_rout, y (device pointers, in that order)
+MOE_LAYER_FIELDS = ("x", "ids", "scores", "gu_code", "gu_rin", "gu_rout", "dn_code", "dn_rin",
+                    "dn_rout", "y")
+
+
+def moe_layers_table(layers: list[dict], device) -> torch.Tensor:
+    """Device array of esc_moe_layer records for moe_expert_path_layers."""
+    rows = []
+    for lay in layers:
+        _dev(*(lay[f] for f in MOE_LAYER_FIELDS))
+        rows.append([lay[f].data_ptr() for f in MOE_LAYER_FIELDS])
+    return torch.tensor(rows, dtype=torch.int64).to(device)
+
+
+def moe_layers_workspace(L: int, T: int, top_k: int, H: int, I: int) -> int:
+    return int(_lib.load().esc_moe_layers_workspace(L, T, top_k, H, I))
+
+
+def moe_expert_path_layers(table: torch.Tensor, T: int, top_k: int, E: int, H: int, I: int,
+                           K_gu: int, K_dn: int, ws: torch.Tensor | None = None) -> None:
+    """L independent token-layers of routed experts in one launch; each layer's
+    y is written in place (see esc_moe_expert_path_layers)."""
+    _dev(table)
+    L = table.shape[0]
+    if ws is None:
+        ws = torch.zeros(max(moe_layers_workspace(L, T, top_k, H, I), 4), dtype=torch.uint8,
+                         device=table.device)
+    _lib.call("esc_moe_expert_path_layers", _ptr(table), L, T, top_k, E, H, I, K_gu, K_dn,
+              _ptr(ws), ws.numel(), _stream())

@@ -135,6 +135,34 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
                         int K_dn, int use_lut, uint16_t* y, void* ws, size_t ws_bytes,
                         void* stream);
 
+/* One token-layer of routed experts for esc_moe_expert_path_layers (device
+ * pointers; the same tensors esc_moe_expert_path takes). */
+typedef struct {
+  const uint16_t* x;
+  const int32_t* ids;
+  const float* scores;
+  const uint32_t* gu_code;
+  const float* gu_rin;
+  const float* gu_rout;
+  const uint32_t* dn_code;
+  const float* dn_rin;
+  const float* dn_rout;
+  uint16_t* y;
+} esc_moe_layer;
+
+/* L independent token-layers of routed experts in one launch (throughput
+ * mode: large items, the layers' work overlaps).  layers = device array of L
+ * records; every layer has the same T, top_k, E, H, I, K_gu, K_dn.  ws must be
+ * zero-filled before its first use (esc_moe_layers_workspace bytes); the call
+ * leaves its counters zero.  No counterpart in the reference: it is the
+ * steady-state form of EschaSparseMoeBlock._expert_path
+ * (escha_mlx/models/qwen3_5_moe.py:207-253) for callers that hold several
+ * independent token-layers at once (pipelined or multi-request decode). */
+size_t esc_moe_layers_workspace(int L, int T, int top_k, int H, int I);
+int esc_moe_expert_path_layers(const esc_moe_layer* layers, int L, int T, int top_k, int E, int H,
+                               int I, int K_gu, int K_dn, void* ws, size_t ws_bytes,
+                               void* stream);
+
 /* Diagnostic: *host_flag = 1 if the one-launch expert path run with this
  * workspace ever hit its bounded wait (never expected: the kernel's work
  * claiming guarantees progress).  Synchronises the stream.  No counterpart in

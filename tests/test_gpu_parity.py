@@ -397,6 +397,36 @@ def test_moe_one_launch_status_and_reuse(monkeypatch):
     assert ops().moe_status(ws, 1, k, H, I) == 0
 
 
+def test_moe_layers_one_launch_vs_oracle():
+    """Independent token-layers in one launch (throughput mode): every layer's
+    output against the oracle, bit-identical across repeated launches."""
+    E, H, I, k, T, L = 32, 1024, 512, 8, 1, 3
+    o = ops()
+    cases = [_moe_case(E, H, I, 2, 2, T, k, 40 + l) for l in range(L)]
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    lays, keep = [], []
+    for c in cases:
+        ids, sc = o.route_topk(dv(c["logits"]), k)
+        lay = {"x": dv(c["x"]), "ids": ids, "scores": sc, "gu_code": dcode(c["gu_code"]),
+               "gu_rin": dv(c["gu_rin"]), "gu_rout": dv(c["gu_rout"]), "dn_code": dcode(c["dn_code"]),
+               "dn_rin": dv(c["dn_rin"]), "dn_rout": dv(c["dn_rout"]),
+               "y": torch.empty((T, H), dtype=torch.float16, device=DEV)}
+        lays.append(lay)
+    table = o.moe_layers_table(lays, DEV)
+    ws = torch.zeros(o.moe_layers_workspace(L, T, k, H, I), dtype=torch.uint8, device=DEV)
+    o.moe_expert_path_layers(table, T, k, E, H, I, 2, 2, ws=ws)
+    first = [bits16(l["y"]).copy() for l in lays]
+    for c, lay in zip(cases, lays):
+        ids_np, sc_np = lay["ids"].cpu().numpy(), lay["scores"].cpu().numpy()
+        want = _oracle_moe(c, ids_np, sc_np, E, H, I, 2, 2, np.unique(ids_np)).astype(np.float32)
+        got = lay["y"].cpu().numpy().astype(np.float32)
+        assert np.abs(got - want).max() / np.abs(want).max() < 5e-3
+    for _ in range(3):
+        o.moe_expert_path_layers(table, T, k, E, H, I, 2, 2, ws=ws)
+        for f, lay in zip(first, lays):
+            assert np.array_equal(bits16(lay["y"]), f)
+
+
 def test_moe_fused_is_deterministic(monkeypatch):
     c = _moe_case(64, 512, 256, 2, 2, 2, 8, 77)
     blk = _block(c, 64, 8, 2, 2, monkeypatch, exact=False)
