@@ -160,7 +160,7 @@ def main():
             "sustained_us_per_token_layer": round(ms * 1e3 / nl, 3),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                         "kernel": "k_moe_fused<2,2,32,32,false> (esc_moe_expert_path_layers)",
+                         "kernel": "k_moe_fused<2,2,16,32,false> (esc_moe_expert_path_layers)",
                          "bytes_per_launch": BYTES_TOKEN_LAYER * nl,
                          "avg_launch_us": round(ms * 1e3, 2)},
         })

@@ -366,7 +366,7 @@ bool fused_eligible(int T, int top_k, int H, int I) {
 }
 
 FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput) {
-  const int kta = throughput ? 32 : 8, ktb = throughput ? 32 : 4;
+  const int kta = throughput ? 16 : 8, ktb = throughput ? 16 : 4;
   FusedPlan f;
   f.L = L;
   f.M = T * top_k;
@@ -417,13 +417,20 @@ esc::FusedMoe fused_args(const FusedPlan& f, void* ws, int T, int top_k, int H, 
 
 template <int KG, int KD, bool TP>
 int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
-  if constexpr (TP)
-    hipLaunchKernelGGL((esc::k_moe_fused<KG, KD, 32, 32, false>), dim3(grid),
+  if constexpr (TP) {
+    // two launches: every gate_up item, then every down item (grid unused)
+    (void)grid;
+    hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 16>), dim3(p.L * p.nA),
                        dim3(esc::kFusedThreads), 0, s, p);
-  else
+    if (int rc = launched("k_moe_gate_up_items")) return rc;
+    hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, 16>), dim3(p.L * p.nB),
+                       dim3(esc::kFusedThreads), 0, s, p);
+    return launched("k_moe_down_items");
+  } else {
     hipLaunchKernelGGL((esc::k_moe_fused<KG, KD, 8, 4, true>), dim3(grid),
                        dim3(esc::kFusedThreads), 0, s, p);
-  return launched("k_moe_fused");
+    return launched("k_moe_fused");
+  }
 }
 
 template <bool TP>

@@ -99,6 +99,106 @@ __device__ __forceinline__ void fast_tile(const LaneWords<K>& lw, uint32_t wprev
   }
 }
 
+// ---------------------------------------------------------------- packed decode
+// Hash decode of two states at a time, written against the gfx950 VALU:
+//   x = s * 0xCBAC1FED mod 2^32 = s*0x1FED + (lo16(s*0xCBAC) << 16) for a
+//   16-bit s: v_mul_lo_u16 with an SDWA destination in the high half, then
+//   v_mad_u32_u16 (2 full-rate ops instead of one quarter-rate v_mul_lo_u32);
+//   r = (x & 0x8FFF8FFF) ^ 0x3B603B60 (one v_bitop3_b32);
+//   w = f16(lo16 r) + f16(hi16 r), RNE, written by an SDWA add straight into
+//   one half of a packed pair, so two weights feed one v_dot2_f32_f16.
+// The weights are bit-identical to decode_hash(); only the multiply-add is
+// pairwise (tolerance contract).
+constexpr uint32_t kClo = 0x1FEDu, kChi = 0xCBACu;
+
+// x of the state in the low (HI=false) or high (HI=true) half of p.
+template <bool HI>
+__device__ __forceinline__ uint32_t hash_x(uint32_t p, uint32_t clo, uint32_t chi) {
+  uint32_t y, x;
+  if constexpr (HI) {
+    __asm__("v_mul_lo_u16_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:WORD_0"
+            : "=v"(y) : "v"(p), "v"(chi));
+    __asm__("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(x) : "v"(p), "v"(clo), "v"(y));
+  } else {
+    __asm__("v_mul_lo_u16_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_0"
+            : "=v"(y) : "v"(p), "v"(chi));
+    __asm__("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(x) : "v"(p), "v"(clo), "v"(y));
+  }
+  return x;
+}
+
+// packed [w(r_lo), w(r_hi)] from two hash words
+__device__ __forceinline__ uint32_t halves_sum2(uint32_t r_lo, uint32_t r_hi) {
+  uint32_t w;
+  __asm__("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+          : "=v"(w) : "v"(r_lo));
+  __asm__("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+          : "+v"(w) : "v"(r_hi));
+  return w;
+}
+
+__device__ __forceinline__ uint32_t mask_xor(uint32_t x) { return (x & kHashMask) ^ kHashXor; }
+
+__device__ __forceinline__ float dot2(uint32_t xp, uint32_t wp, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, xp), __builtin_bit_cast(half2_t, wp),
+                                acc, false);
+}
+
+// The 8 input pairs [x(r+2), x(r)] (r = 0,1,4,5,8,9,12,13 -> index
+// 2(r>>2) | (r&1)) one kt's pairs of trellis steps (u, u+8) multiply.
+__device__ __forceinline__ void x_pairs(const uint32_t* xw, uint32_t* xp) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * (i >> 1) + (i & 1);
+    const uint32_t sel = (r & 1) ? 0x07060302u : 0x05040100u;
+    xp[i] = __builtin_amdgcn_perm(xw[r >> 1], xw[(r >> 1) + 1], sel);
+  }
+}
+__device__ constexpr int xpair_index(int r) { return 2 * (r >> 2) | (r & 1); }
+
+// Packed-decode variant of fast_tile (hash only): steps u and u+8 of the lane
+// (u>>3 even) share a tile column and sit 2 rows apart, so they form one
+// dot2 pair.  K=2: their 16-bit windows are adjacent, one v_alignbit gives both.
+template <int K>
+__device__ __forceinline__ void fast_tile_packed(const LaneWords<K>& lw, uint32_t wprev,
+                                                 const uint32_t* xp, float* acc) {
+  using G = Geo<K>;
+  const uint32_t clo = kClo, chi = kChi;
+#pragma unroll
+  for (int u = 0; u < G::SPL; ++u) {
+    if ((u >> 3) & 1) continue;  // u+8 handled with u
+    uint32_t w2;
+    if constexpr (K == 2) {
+      // 32-bit window starting at step u's first bit: [s_u | s_{u+8}]
+      const int rel = 2 * (u + 1) - 16;
+      const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
+      const uint32_t hi = a < 0 ? wprev : lw.w[a];
+      uint32_t p;
+      if (off == 0)
+        p = hi;
+      else
+        p = __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 32 - off);
+      w2 = halves_sum2(mask_xor(hash_x<false>(p, clo, chi)), mask_xor(hash_x<true>(p, clo, chi)));
+    } else {
+      uint32_t s2[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int uu = u + 8 * (1 - h);  // low half: step u+8, high half: step u
+        const int rel = 3 * (uu + 1) - 16;
+        const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
+        const uint32_t hi = a < 0 ? wprev : lw.w[a];
+        // the state in the low 16 bits (bits above are ignored by the u16 ops)
+        s2[h] = off <= 16 ? hi >> (16 - off)
+                          : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 48 - off);
+      }
+      w2 = halves_sum2(mask_xor(hash_x<false>(s2[0], clo, chi)),
+                       mask_xor(hash_x<false>(s2[1], clo, chi)));
+    }
+    const int ci = G::col_slot(u);
+    acc[ci] = dot2(xp[xpair_index(fast_row(u))], w2, acc[ci]);
+  }
+}
+
 // Partial GEMV: part[z][row][OC] = sum over the block's kt range.
 // grid (TN/TPW, M, S), block 256; KS = TK/S kt per block, KS % 4 == 0.
 // row_expert null -> dense (single stream).
@@ -140,7 +240,13 @@ __global__ __launch_bounds__(256) void k_gemv_fast(const uint16_t* __restrict__ 
 #pragma unroll
     for (int i = 0; i < 8; ++i) xw[i] = xrow[8 * kt + i];
     const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
-    fast_tile<K, LUT>(cur, wprev, xw, s_lut, acc);
+    if constexpr (LUT) {
+      fast_tile<K, true>(cur, wprev, xw, s_lut, acc);
+    } else {
+      uint32_t xp[8];
+      x_pairs(xw, xp);
+      fast_tile_packed<K>(cur, wprev, xp, acc);
+    }
     cur = nxt;
   }
 #pragma unroll

@@ -19,7 +19,7 @@
 //     sum, one f16 rounding).  No float atomics: the result is deterministic.
 //
 // Two item sizes: small items (KTA=8, KTB=4) spread one token-layer over the
-// whole GPU for latency; large items (KTA=32, KTB=32) cut the partial traffic
+// whole GPU for latency; large items (KTA=16, KTB=32) cut the partial traffic
 // when many token-layers share a launch (throughput).  In the single-layer
 // mode each block requests its first down item's code before doing anything
 // else, so that code is in registers by the time the item's inputs are ready.
@@ -151,7 +151,7 @@ __device__ __forceinline__ ItemCode<K, NKT> load_item(const uint32_t* __restrict
 
 // Decode + multiply the item (inputs: 8 f16-pair words per kt in s_x) and
 // publish its 256 float32 column partials to dst (coherent stores).
-template <int K, int NKT>
+template <int K, int NKT, bool WAIT = true>
 __device__ __forceinline__ void compute_item(const ItemCode<K, NKT>& code, const uint32_t* s_x,
                                              float (*s_red)[64][4], float* __restrict__ dst) {
   using G = Geo<K>;
@@ -170,7 +170,9 @@ __device__ __forceinline__ void compute_item(const ItemCode<K, NKT>& code, const
 #pragma unroll
     for (int j = 0; j < 8; ++j) xw[j] = s_x[8 * kl + j];
     const uint32_t wprev = __shfl(code.w[k].w[G::WPL - 1], src);
-    fast_tile<K, false>(code.w[k], wprev, xw, nullptr, acc);
+    uint32_t xp[8];
+    x_pairs(xw, xp);
+    fast_tile_packed<K>(code.w[k], wprev, xp, acc);
   }
 #pragma unroll
   for (int c = 0; c < G::NCOL; ++c) s_red[wave][lane][c] = acc[c];
@@ -185,8 +187,10 @@ __device__ __forceinline__ void compute_item(const ItemCode<K, NKT>& code, const
     for (int w = 0; w < IG::WPG; ++w) v = v + s_red[gg * IG::WPG + w][ii * G::LPT + qq][ci];
     st_coherent(dst + j, v);
   }
-  wait_vm();
-  __syncthreads();
+  if constexpr (WAIT) {
+    wait_vm();
+    __syncthreads();
+  }
 }
 
 __device__ __forceinline__ uint32_t pack2(half_t a, half_t b) {
@@ -211,9 +215,15 @@ __device__ __forceinline__ ItemCode<K, KTB> load_down(const FusedMoe& p, int l, 
                            [&](int it) { return 16 * cp + it; });
 }
 
+// count gate_up item a of layer l as published (its partials are complete)
+__device__ __forceinline__ void publish_gate_up(const FusedMoe& p, int l, int a) {
+  const int rb = a / p.NKC, b = rb % p.NB, r = rb / p.NB;
+  add_relaxed(&p.cntA[(size_t)l * p.T * p.top_k * p.NB + r * p.NB + b], 1);
+}
+
 // gate_up item a of layer l with its code already in flight: transform the
 // item's 16*KTA inputs (one wave per 128-block), decode + multiply, publish.
-template <int K, int KTA>
+template <int K, int KTA, bool PUBLISH = true>
 __device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, KTA>& code,
                             uint32_t* s_x, float (*s_red)[64][4]) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -230,8 +240,8 @@ __device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, K
     s_x[64 * wave + lane] = pack2(to_f16(v0 * kRS), to_f16(v1 * kRS));
   }
   __syncthreads();
-  compute_item<K, KTA>(code, s_x, s_red, p.partA + ((size_t)l * p.nA + a) * 256);
-  if (threadIdx.x == 0) add_relaxed(&p.cntA[(size_t)l * p.T * p.top_k * p.NB + r * p.NB + b], 1);
+  compute_item<K, KTA, PUBLISH>(code, s_x, s_red, p.partA + ((size_t)l * p.nA + a) * 256);
+  if (PUBLISH && threadIdx.x == 0) publish_gate_up(p, l, a);
 }
 
 // h-block kb of row r (layer l) -> its 128 down inputs (f16 pairs) in s_x[0..63].
@@ -390,8 +400,48 @@ __device__ int wait_gate_up(const FusedMoe& p, int l, int r, int kb, int* s_flag
   return st;
 }
 
+// ---------------------------------------------------------------- throughput
+// Many independent token-layers: every gate_up item of every layer in one
+// launch, then every down item (plus the last-arriver combine) in a second,
+// one item per block.  The launch boundary is the only hand-off, nothing
+// waits, and the hardware dispatcher balances the items over the CUs.
+template <int KG, int KTA>
+__global__ __launch_bounds__(kFusedThreads, 4) void k_moe_gate_up_items(FusedMoe p) {
+  __shared__ float s_red[4][64][4];
+  __shared__ uint32_t s_x[256];
+  const int l = blockIdx.x / p.nA, a = blockIdx.x % p.nA;
+  const auto code = load_gate_up<KG, KTA>(p, l, a);
+  run_gate_up<KG, KTA, false>(p, l, a, code, s_x, s_red);
+}
+
+template <int KG, int KD, int KTB>
+__global__ __launch_bounds__(kFusedThreads, 4) void k_moe_down_items(FusedMoe p) {
+  __shared__ float s_red[4][64][4];
+  __shared__ uint32_t s_x[256];
+  __shared__ uint16_t s_d[32][256];
+  __shared__ int s_flag;
+  constexpr int kHB = KTB >= 8 ? KTB / 8 : 1;
+  const int tid = threadIdx.x;
+  const int l = blockIdx.x / p.nB, bi = blockIdx.x % p.nB;
+  const int kb = bi % p.NKB, rc = bi / p.NKB, cp = rc % p.NCP, r = rc / p.NCP;
+  const int t = r / p.top_k, hb0 = (KTB * kb) / 8;
+  const auto code = load_down<KD, KTB>(p, l, bi);
+  if ((tid >> 6) < kHB) down_inputs(p, l, r, hb0 + (tid >> 6), s_x + 64 * (tid >> 6));
+  __syncthreads();
+  compute_item<KD, KTB>(code, s_x + ((KTB * kb) % 8) * 8, s_red,
+                        p.partB + ((size_t)l * p.nB + bi) * 256);
+  if (tid == 0) {
+    int* c = &p.cntB[(size_t)l * p.T * p.NCP + t * p.NCP + cp];
+    const bool last = add_relaxed(c, 1) == p.top_k * p.NKB - 1;
+    if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_flag = last;
+  }
+  __syncthreads();
+  if (s_flag) combine_tile(p, l, t, cp, s_d);
+}
+
 template <int KG, int KD, int KTA, int KTB, bool PRE>
-__global__ __launch_bounds__(kFusedThreads) void k_moe_fused(FusedMoe p) {
+__global__ __launch_bounds__(kFusedThreads, 4) void k_moe_fused(FusedMoe p) {
   static_assert(KTA % 8 == 0 && KTA <= 32 && (KTB == 4 || (KTB % 8 == 0 && KTB <= 32)), "");
   __shared__ float s_red[4][64][4];
   __shared__ uint32_t s_x[256];
@@ -407,14 +457,30 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_fused(FusedMoe p) {
   ItemCode<KD, KTB> code0{};
   if (PRE && g0 < nB_all) code0 = load_down<KD, KTB>(p, g0 / p.nB, g0 % p.nB);
 
-  for (int ga = blockIdx.x; ga < nA_all; ga += gridDim.x) {
-    const int l = ga / p.nA, a = ga % p.nA;
-    const auto code = load_gate_up<KG, KTA>(p, l, a);  // in flight while the claim resolves
-    if (tid == 0) s_flag = claim(&p.claimA[(size_t)l * p.nA + a]);
-    __syncthreads();
-    const int mine = s_flag;
-    __syncthreads();
-    if (mine) run_gate_up<KG, KTA>(p, l, a, code, s_x, s_red);
+  // gate_up items, software-pipelined: the next item's code loads and claim
+  // are issued before waiting for this item's partial stores to complete
+  {
+    int ga = blockIdx.x;
+    ItemCode<KG, KTA> code{};
+    if (ga < nA_all) {
+      code = load_gate_up<KG, KTA>(p, ga / p.nA, ga % p.nA);
+      if (tid == 0) s_flag = claim(&p.claimA[ga]);
+    }
+    while (ga < nA_all) {
+      __syncthreads();
+      const int mine = s_flag;
+      __syncthreads();
+      const int l = ga / p.nA, a = ga % p.nA, gn = ga + gridDim.x;
+      if (mine) run_gate_up<KG, KTA, false>(p, l, a, code, s_x, s_red);
+      if (gn < nA_all) {
+        code = load_gate_up<KG, KTA>(p, gn / p.nA, gn % p.nA);
+        if (tid == 0) s_flag = claim(&p.claimA[gn]);
+      }
+      wait_vm();
+      __syncthreads();
+      if (mine && tid == 0) publish_gate_up(p, l, a);
+      ga = gn;
+    }
   }
 
   constexpr int kHB = KTB >= 8 ? KTB / 8 : 1;  // h-blocks read by one down item
