@@ -365,8 +365,13 @@ bool fused_eligible(int T, int top_k, int H, int I) {
          I % 128 == 0;
 }
 
+// Items per layer of the large (KTA=16) size; below kSmallItemsBelow of them
+// in total the two-launch path uses the small size to fill the GPU.
+constexpr int kSmallItemsBelow = 0;
+
 FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput) {
-  const int kta = throughput ? 16 : 8, ktb = throughput ? 16 : 4;
+  const bool large = throughput && L * T * top_k * (I / 128) * std::max(1, H / 256) >= kSmallItemsBelow;
+  const int kta = large ? 16 : 8, ktb = large ? 16 : 4;
   FusedPlan f;
   f.L = L;
   f.M = T * top_k;
@@ -418,8 +423,17 @@ esc::FusedMoe fused_args(const FusedPlan& f, void* ws, int T, int top_k, int H, 
 template <int KG, int KD, bool TP>
 int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
   if constexpr (TP) {
-    // two launches: every gate_up item, then every down item (grid unused)
+    // two launches: every gate_up item, then every down item (grid unused);
+    // small items when there are few layers, large ones otherwise
     (void)grid;
+    if (p.NKC == p.H / 128) {
+      hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 8>), dim3(p.L * p.nA),
+                         dim3(esc::kFusedThreads), 0, s, p);
+      if (int rc = launched("k_moe_gate_up_items")) return rc;
+      hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, 4>), dim3(p.L * p.nB),
+                         dim3(esc::kFusedThreads), 0, s, p);
+      return launched("k_moe_down_items");
+    }
     hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 16>), dim3(p.L * p.nA),
                        dim3(esc::kFusedThreads), 0, s, p);
     if (int rc = launched("k_moe_gate_up_items")) return rc;
@@ -449,7 +463,10 @@ size_t esc_moe_expert_path_workspace(int T, int top_k, int E, int H, int I) {
   size_t a = moe_plan(T, top_k, H, I, 2, 2).total, b = moe_plan(T, top_k, H, I, 3, 3).total;
   size_t c = moe_plan(T, top_k, H, I, 2, 3).total, d = moe_plan(T, top_k, H, I, 3, 2).total;
   size_t m = std::max(std::max(a, b), std::max(c, d));
-  if (fused_eligible(T, top_k, H, I)) m = std::max(m, fused_plan(1, T, top_k, H, I, false).total);
+  if (fused_eligible(T, top_k, H, I)) {
+    m = std::max(m, fused_plan(1, T, top_k, H, I, false).total);
+    if (throughput_ok(H, I)) m = std::max(m, fused_plan(1, T, top_k, H, I, true).total);
+  }
   return m;
 }
 
@@ -457,7 +474,8 @@ int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int
                    int32_t* host_flag, void* stream) {
   ESC_REQUIRE(ws && host_flag, "null pointer");
   *host_flag = 0;
-  if (!fused_eligible(T, top_k, H, I)) return ESC_OK;
+  // only the single persistent launch has a bounded wait
+  if (!fused_eligible(T, top_k, H, I) || throughput_ok(H, I)) return ESC_OK;
   const FusedPlan f = fused_plan(1, T, top_k, H, I, false);
   ESC_REQUIRE(ws_bytes >= f.total, "workspace smaller than the plan");
   const int32_t* err = reinterpret_cast<const int32_t*>(static_cast<const char*>(ws) + f.off_int) +
@@ -482,6 +500,17 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
   if (int rc = check_proj(K_dn, I, H)) return rc;
   ESC_REQUIRE(T >= 0, "negative token count");
   if (T == 0) return ESC_OK;
+  if (fused_eligible(T, top_k, H, I) && throughput_ok(H, I)) {
+    // two launches (gate_up items, down items + combine): measured faster
+    // than the single persistent launch for one token-layer on gfx950
+    const FusedPlan f = fused_plan(1, T, top_k, H, I, true);
+    if (!ws || ws_bytes < f.total)
+      return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, f.total);
+    esc::FusedMoe p = fused_args(f, ws, T, top_k, H, I);
+    p.l0 = esc::MoeLayer{x, ids, scores, gu_code, gu_rin, gu_rout, dn_code, dn_rin, dn_rout, y};
+    p.layers = nullptr;
+    return launch_fused<true>(p, K_gu, K_dn, f.grid, S(stream));
+  }
   if (fused_eligible(T, top_k, H, I)) {
     const FusedPlan f = fused_plan(1, T, top_k, H, I, false);
     if (!ws || ws_bytes < f.total)
