@@ -2,26 +2,37 @@
 
 Workload (config 3): 256 experts, hidden 2048, expert intermediate 512, top-8,
 2-bit (K=2) coded gate_up and down per expert, hash decode.  L=40 independent
-layer stacks (40 x 201,326,592 coded bytes = 8.05 GB, far above the 256 MB
-Infinity Cache), so every routed expert is read cold from HBM.  Router logits
-are seeded float32 N(0,1) per layer, routed top-8 with softmax weights.
+layer stacks (40 x 201,326,592 coded bytes = 8.05 GB).  Router logits are
+seeded float32 N(0,1), routed top-8 with softmax weights; there are
+ROUTE_SETS routings per layer and step i uses set i % ROUTE_SETS, so two
+consecutive steps read different experts (one step reads 251,658,240 coded
+bytes; the sets together about 1 GB, four times the 256 MB Infinity Cache):
+every step reads its experts cold.
 
 Two measurements, both one token per layer (batch 1):
   sustained (the `value`): the 40 token-layers are independent and go to the
-      GPU as ONE launch of esc_moe_expert_path_layers; steady-state coded-weight
-      throughput of the expert GEMV (the protocol "sustained, back-to-back over
-      independent layers").
-  chained (`tok_s`): a decode step — layer l's output is layer l+1's input —
-      as 40 launches of the drop-in esc_moe_expert_path; tok/s = 1 / step.
+      GPU as ONE esc_moe_expert_path_layers call (two kernels: every gate_up
+      item, then every down item); steady-state coded-weight throughput.
+  chained (`tok_s`): a decode step -- layer l's output is layer l+1's input --
+      as 40 calls of the drop-in esc_moe_expert_path; tok/s = 1 / step.
 Inputs are resident in HBM before timing starts; HIP events on the launch stream.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers 40]
+roofline.traffic: HBM bytes per sustained call from two rocprofv3 PMC passes
+over `bench.py --probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each
+scaled by what the same counter reads for a 1 GiB device copy in that run.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers 40] [--no-traffic]
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
+import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -35,6 +46,9 @@ BYTES_GU = H * 2 * I * K // 8          # 524,288 per expert
 BYTES_DN = I * H * K // 8              # 262,144 per expert
 BYTES_TOKEN_LAYER = TOP_K * (BYTES_GU + BYTES_DN)   # 6,291,456
 HBM_PEAK_GBS = 8000.0
+ROUTE_SETS = 4
+COPY_BYTES = 1 << 30                   # counter calibration copy
+KERNELS = ("k_moe_gate_up_items", "k_moe_down_items")
 
 
 def parse():
@@ -43,13 +57,19 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=40)
-    ap.add_argument("--cpu-sample", type=int, default=3, help="token-layers for the CPU baseline")
+    ap.add_argument("--cpu-sample", type=int, default=64,
+                    help="token-layers timed through the CPU oracle")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 PMC passes")
     ap.add_argument("--only", choices=["both", "sustained", "chained"], default="both")
+    ap.add_argument("--probe", action="store_true",
+                    help="run the calibration copy and two sustained calls, untimed (for PMC)")
     return ap.parse_args()
 
 
 def make_layers(torch, n_layers: int, dev: str, seed: int = 2):
+    """Per layer: E-stacked coded gate_up/down, rin/rout, input x and one
+    router-logit row per routing set."""
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     layers = []
@@ -62,23 +82,36 @@ def make_layers(torch, n_layers: int, dev: str, seed: int = 2):
         gu_rin, dn_rin = sgn(E, H), sgn(E, I)
         gu_rout = sgn(E, 2 * I) * (0.5 + torch.rand(E, 2 * I, generator=g, device=dev)) * 4e-2
         dn_rout = sgn(E, H) * (0.5 + torch.rand(E, H, generator=g, device=dev)) * 4e-2
-        logits = torch.randn(1, E, generator=g, device=dev, dtype=torch.float32)
+        logits = torch.randn(ROUTE_SETS, 1, E, generator=g, device=dev, dtype=torch.float32)
         x = torch.randn(1, H, generator=g, device=dev).half()
         layers.append(dict(gu_code=gu, dn_code=dn, gu_rin=gu_rin.float().contiguous(),
                            dn_rin=dn_rin.float().contiguous(), gu_rout=gu_rout.float().contiguous(),
-                           dn_rout=dn_rout.float().contiguous(), logits=logits, x=x))
+                           dn_rout=dn_rout.float().contiguous(), logits=logits, x=x,
+                           y=torch.empty(1, H, dtype=torch.float16, device=dev)))
     return layers
 
 
-def cpu_baseline(sample, n_sample: int):
+def route_sets(torch, layers):
+    """routes[s][l] = layer l's record with routing set s (ids, scores)."""
+    from escha_mlx_amd import moe
+    routes = []
+    for s in range(ROUTE_SETS):
+        per = []
+        for L in layers:
+            ids, scores = moe.route(L["logits"][s], TOP_K)
+            per.append(dict(L, ids=ids, scores=scores))
+        routes.append(per)
+    return routes
+
+
+def cpu_baseline(sample):
     """The NumPy oracle (decode + transforms + f32 matmul, no weight cache), one BLAS thread."""
     from threadpoolctl import threadpool_limits
 
     from oracle import ref_np
     t_total = 0.0
     with threadpool_limits(limits=1):
-        for s in range(n_sample):
-            L = sample[s % len(sample)]
+        for L in sample:
             t0 = time.perf_counter()
             w_gu = {e: ref_np.reconstruct(L["gu"][e], H, 2 * I, K) for e in L["ids"][0]}
             w_dn = {e: ref_np.reconstruct(L["dn"][e], I, H, K) for e in L["ids"][0]}
@@ -86,46 +119,132 @@ def cpu_baseline(sample, n_sample: int):
             dn = {"w": w_dn, "rin": L["dn_rin"], "rout": L["dn_rout"]}
             ref_np.moe_routed(L["x"], L["ids"], L["scores"], gu, dn, K, K, ordered=False)
             t_total += time.perf_counter() - t0
-    per = t_total / n_sample
+    per = t_total / len(sample)
     return {"value": round(BYTES_TOKEN_LAYER / per / 1e9, 4), "unit": "GB/s", "cores": 1,
             "kind": "port",
-            "sample": f"{n_sample} token-layers of config 3 through oracle/ref_np.py "
-                      f"(vectorised decode of 8 experts x 2 legs, no cache, f32 matmul, 1 BLAS "
-                      f"thread): {per * 1e3:.1f} ms per token-layer"}
+            "sample": f"{len(sample)} token-layers of config 3 (distinct layer x routing pairs) "
+                      f"through oracle/ref_np.py: vectorised decode of 8 experts x 2 legs, no "
+                      f"cache, f32 matmul, 1 BLAS thread; {per * 1e3:.1f} ms per token-layer, "
+                      f"{t_total:.1f} s total"}
+
+
+def cpu_sample(routes, n: int):
+    """Host copies of the routed experts of n (routing set, layer) token-layers."""
+    out = []
+    for i in range(n):
+        L = routes[(i // len(routes[0])) % ROUTE_SETS][i % len(routes[0])]
+        ids = L["ids"].cpu().numpy()
+
+        def sel(t):
+            rows = {int(e): t[int(e)].cpu().numpy() for e in ids[0]}
+            return {e: (a.view(np.uint32) if a.dtype == np.int32 else a) for e, a in rows.items()}
+        out.append({"gu": sel(L["gu_code"]), "dn": sel(L["dn_code"]),
+                    "gu_rin": sel(L["gu_rin"]), "dn_rin": sel(L["dn_rin"]),
+                    "gu_rout": sel(L["gu_rout"]), "dn_rout": sel(L["dn_rout"]),
+                    "ids": ids, "scores": L["scores"].cpu().numpy(), "x": L["x"].cpu().numpy()})
+    return out
 
 
 def timed(torch, fn, steps: int, warmup: int, stream) -> float:
-    """Average ms per call of fn(), HIP events on `stream` around `steps` calls."""
-    for _ in range(warmup):
-        fn()
+    """Average ms per call of fn(i), HIP events on `stream` around `steps` calls."""
+    for i in range(warmup):
+        fn(i)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
-    for _ in range(steps):
-        fn()
+    for i in range(steps):
+        fn(warmup + i)
     ev1.record(stream)
     torch.cuda.synchronize()
     return ev0.elapsed_time(ev1) / steps
+
+
+def _counter_rows(path: Path):
+    per = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            per.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return per
+
+
+def measure_traffic(layers: int):
+    """HBM bytes per sustained call, from FETCH_SIZE and WRITE_SIZE passes of
+    rocprofv3 over `bench.py --probe`, each calibrated by the 1 GiB copy the
+    probe runs first.  Runs before this process touches the GPU."""
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not found"
+    res = {}
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+            cmd = [exe, "--pmc", ctr, "--output-format", "csv", "-d", d, "-o", ctr, "--",
+                   sys.executable, str(ROOT / "bench.py"), "--probe", "--layers", str(layers)]
+            try:
+                subprocess.run(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"),
+                               stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=240,
+                               check=True)
+            except (subprocess.SubprocessError, OSError) as e:
+                return None, f"rocprofv3 --pmc {ctr} failed: {type(e).__name__}"
+            per = _counter_rows(Path(d) / f"{ctr}_counter_collection.csv")
+            copy = max(v for k, vals in per.items() if "copyBuffer" in k for v in vals)
+            factor = COPY_BYTES / (copy * 1024.0)
+            for kname in KERNELS:
+                vals = [v for k, vv in per.items() if kname in k for v in vv]
+                if not vals:
+                    return None, f"no {kname} dispatch in the {ctr} pass"
+                res[(ctr, kname)] = (sum(vals) / len(vals)) * 1024.0 * factor
+            res[(ctr, "factor")] = factor
+    total = sum(v for (c, k), v in res.items() if k != "factor")
+    detail = {f"{c.split('_')[0].lower()}_{k}": (round(v, 4) if k == "factor" else int(v))
+              for (c, k), v in res.items()}
+    return int(total), detail
+
+
+def probe(torch, args):
+    """Calibration copy, then two sustained calls (PMC target)."""
+    from escha_mlx_amd import ops
+    dev = "cuda:0"
+    ops.init()
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    layers = make_layers(torch, args.layers, dev)
+    routes = route_sets(torch, layers)
+    ws = torch.zeros(ops.moe_layers_workspace(args.layers, 1, TOP_K, H, I), dtype=torch.uint8,
+                     device=dev)
+    for s in range(2):
+        table = ops.moe_layers_table(routes[s], dev)
+        ops.moe_expert_path_layers(table, 1, TOP_K, E, H, I, K, K, ws=ws)
+    torch.cuda.synchronize()
+    print(f"probe: copy {COPY_BYTES} B, 2 calls x {BYTES_TOKEN_LAYER * args.layers} coded B",
+          flush=True)
 
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus N>1 is not supported "
-                                   "(DESIGN.md describes how the path would shard)"}))
+                                   "(the sharding design is described, not built)"}))
         sys.exit(2)
+    traffic, traffic_detail = None, "not measured (--no-traffic)"
+    if not args.probe and not args.no_traffic and args.only != "chained":
+        traffic, traffic_detail = measure_traffic(args.layers)
     import torch
 
-    from escha_mlx_amd import moe, ops
+    if args.probe:
+        torch.cuda.set_device(0)
+        probe(torch, args)
+        return
+    from escha_mlx_amd import ops
 
     dev = "cuda:0"
     torch.cuda.set_device(0)
     ops.init()
     nl = args.layers
     layers = make_layers(torch, nl, dev)
-    for L in layers:
-        L["ids"], L["scores"] = moe.route(L["logits"], TOP_K)
-        L["y"] = torch.empty(1, H, dtype=torch.float16, device=dev)
+    routes = route_sets(torch, layers)
     stream = torch.cuda.current_stream()
     t_wall = time.perf_counter()
     result = {
@@ -141,38 +260,40 @@ def main():
         "data": "synthetic: uniform-random code streams, seeded rin/rout/logits/x (random-init)",
         "config": {"workload": "config 3: routed MoE expert GEMV, batch 1 per layer, E=256, "
                                "H=2048, I=512, top-8, K=2 gate_up+down, hash decode, "
-                               f"{nl} cold layer stacks",
+                               f"{nl} layer stacks, {ROUTE_SETS} routings cycled per step",
                    "layers": nl, "bytes_per_token_layer": BYTES_TOKEN_LAYER},
     }
 
     if args.only in ("both", "sustained"):
-        table = ops.moe_layers_table(layers, dev)
+        tables = [ops.moe_layers_table(routes[s], dev) for s in range(ROUTE_SETS)]
         ws_l = torch.zeros(ops.moe_layers_workspace(nl, 1, TOP_K, H, I), dtype=torch.uint8,
                            device=dev)
-        ms = timed(torch, lambda: ops.moe_expert_path_layers(table, 1, TOP_K, E, H, I, K, K,
-                                                             ws=ws_l), args.steps, args.warmup,
-                   stream)
-        gbs = BYTES_TOKEN_LAYER * nl / (ms * 1e-3) / 1e9
+        ms = timed(torch, lambda i: ops.moe_expert_path_layers(
+            tables[i % ROUTE_SETS], 1, TOP_K, E, H, I, K, K, ws=ws_l),
+            args.steps, args.warmup, stream)
+        bytes_call = BYTES_TOKEN_LAYER * nl
+        gbs = bytes_call / (ms * 1e-3) / 1e9
         result.update({
             "value": round(gbs, 2),
             "ms_per_step": round(ms, 4),
             "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
             "sustained_us_per_token_layer": round(ms * 1e3 / nl, 3),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                         "kernel": "k_moe_fused<2,2,16,32,false> (esc_moe_expert_path_layers)",
-                         "bytes_per_launch": BYTES_TOKEN_LAYER * nl,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                         "traffic_detail": traffic_detail,
+                         "kernel": "k_moe_gate_up_items<2,16> + k_moe_down_items<2,2,16> "
+                                   "(one esc_moe_expert_path_layers call)",
+                         "bytes_per_launch": bytes_call,
                          "avg_launch_us": round(ms * 1e3, 2)},
         })
 
     if args.only in ("both", "chained"):
         ws = torch.zeros(ops.moe_expert_path_workspace(1, TOP_K, E, H, I), dtype=torch.uint8,
                          device=dev)
-        x0 = layers[0]["x"]
 
-        def chained():
-            x = x0
-            for L in layers:
+        def chained(i):
+            x = layers[0]["x"]
+            for L in routes[i % ROUTE_SETS]:
                 ops.moe_expert_path(x, L["ids"], L["scores"], L["gu_code"], L["gu_rin"],
                                     L["gu_rout"], K, L["dn_code"], L["dn_rin"], L["dn_rout"], K,
                                     ws=ws, out=L["y"])
@@ -190,17 +311,8 @@ def main():
             result.update({"value": round(gbs_c, 2), "ms_per_step": round(ms_c, 4)})
     result["wall_s"] = round(time.perf_counter() - t_wall, 3)
 
-    if not args.no_cpu:
-        sample = []
-        for L in layers[: min(args.cpu_sample, nl)]:
-            sample.append({
-                "gu": L["gu_code"].cpu().numpy().view(np.uint32),
-                "dn": L["dn_code"].cpu().numpy().view(np.uint32),
-                "gu_rin": L["gu_rin"].cpu().numpy(), "dn_rin": L["dn_rin"].cpu().numpy(),
-                "gu_rout": L["gu_rout"].cpu().numpy(), "dn_rout": L["dn_rout"].cpu().numpy(),
-                "ids": L["ids"].cpu().numpy(), "scores": L["scores"].cpu().numpy(),
-                "x": L["x"].cpu().numpy()})
-        result["cpu_baseline"] = cpu_baseline(sample, args.cpu_sample)
+    if not args.no_cpu and args.cpu_sample > 0:
+        result["cpu_baseline"] = cpu_baseline(cpu_sample(routes, args.cpu_sample))
     print(json.dumps(result))
 
 

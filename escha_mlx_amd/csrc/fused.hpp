@@ -19,7 +19,7 @@
 //     sum, one f16 rounding).  No float atomics: the result is deterministic.
 //
 // Two item sizes: small items (KTA=8, KTB=4) spread one token-layer over the
-// whole GPU for latency; large items (KTA=16, KTB=32) cut the partial traffic
+// whole GPU for latency; large items (KTA=16, KTB=16) cut the partial traffic
 // when many token-layers share a launch (throughput).  In the single-layer
 // mode each block requests its first down item's code before doing anything
 // else, so that code is in registers by the time the item's inputs are ready.
@@ -150,8 +150,10 @@ __device__ __forceinline__ ItemCode<K, NKT> load_item(const uint32_t* __restrict
 }
 
 // Decode + multiply the item (inputs: 8 f16-pair words per kt in s_x) and
-// publish its 256 float32 column partials to dst (coherent stores).
-template <int K, int NKT, bool WAIT = true>
+// publish its 256 float32 column partials to dst (device-coherent stores when
+// COH, for a consumer in the same launch; plain stores when the only consumer
+// runs in a later launch).
+template <int K, int NKT, bool WAIT = true, bool COH = true>
 __device__ __forceinline__ void compute_item(const ItemCode<K, NKT>& code, const uint32_t* s_x,
                                              float (*s_red)[64][4], float* __restrict__ dst) {
   using G = Geo<K>;
@@ -185,7 +187,10 @@ __device__ __forceinline__ void compute_item(const ItemCode<K, NKT>& code, const
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < IG::WPG; ++w) v = v + s_red[gg * IG::WPG + w][ii * G::LPT + qq][ci];
-    st_coherent(dst + j, v);
+    if constexpr (COH)
+      st_coherent(dst + j, v);
+    else
+      dst[j] = v;
   }
   if constexpr (WAIT) {
     wait_vm();
@@ -223,12 +228,12 @@ __device__ __forceinline__ void publish_gate_up(const FusedMoe& p, int l, int a)
 
 // gate_up item a of layer l with its code already in flight: transform the
 // item's 16*KTA inputs (one wave per 128-block), decode + multiply, publish.
-template <int K, int KTA, bool PUBLISH = true>
+template <int K, int KTA, bool PUBLISH = true, bool COH = true>
 __device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, KTA>& code,
                             uint32_t* s_x, float (*s_red)[64][4]) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const MoeLayer& L = p.layer(l);
-  const int kc = a % p.NKC, rb = a / p.NKC, b = rb % p.NB, r = rb / p.NB;
+  const int kc = a % p.NKC, r = a / p.NKC / p.NB;
   const int t = r / p.top_k, e = L.ids[r];
   if (wave < KTA / 8) {
     const int c = 16 * KTA * kc + 128 * wave + 2 * lane;
@@ -240,11 +245,14 @@ __device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, K
     s_x[64 * wave + lane] = pack2(to_f16(v0 * kRS), to_f16(v1 * kRS));
   }
   __syncthreads();
-  compute_item<K, KTA, PUBLISH>(code, s_x, s_red, p.partA + ((size_t)l * p.nA + a) * 256);
+  compute_item<K, KTA, PUBLISH, COH>(code, s_x, s_red, p.partA + ((size_t)l * p.nA + a) * 256);
   if (PUBLISH && threadIdx.x == 0) publish_gate_up(p, l, a);
 }
 
 // h-block kb of row r (layer l) -> its 128 down inputs (f16 pairs) in s_x[0..63].
+// COH: the gate_up partials were published in this launch (device-coherent
+// loads); otherwise by an earlier launch (plain loads, which may hit L2).
+template <bool COH = true>
 __device__ void down_inputs(const FusedMoe& p, int l, int r, int kb, uint32_t* s_x) {
   const int lane = threadIdx.x & 63;
   const MoeLayer& L = p.layer(l);
@@ -257,8 +265,13 @@ __device__ void down_inputs(const FusedMoe& p, int l, int r, int kb, uint32_t* s
 #pragma unroll
     for (int j = 0; j < 16; ++j)
       if (kc0 + j < p.NKC) {
-        gv[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256);
-        uv[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256 + 128);
+        if constexpr (COH) {
+          gv[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256);
+          uv[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256 + 128);
+        } else {
+          gv[j] = *reinterpret_cast<const float2*>(base + (size_t)(kc0 + j) * 256);
+          uv[j] = *reinterpret_cast<const float2*>(base + (size_t)(kc0 + j) * 256 + 128);
+        }
       }
 #pragma unroll
     for (int j = 0; j < 16; ++j)
@@ -400,18 +413,30 @@ __device__ int wait_gate_up(const FusedMoe& p, int l, int r, int kb, int* s_flag
   return st;
 }
 
-// ---------------------------------------------------------------- throughput
-// Many independent token-layers: every gate_up item of every layer in one
-// launch, then every down item (plus the last-arriver combine) in a second,
-// one item per block.  The launch boundary is the only hand-off, nothing
-// waits, and the hardware dispatcher balances the items over the CUs.
+// ---------------------------------------------------------------- two launches
+// Every gate_up item of every layer in one launch, then every down item (plus
+// the last-arriver combine) in a second, one item per block.  The launch
+// boundary is the gate_up -> down hand-off, so nothing waits, the partials go
+// through plain stores and loads, and the hardware dispatcher balances the
+// items over the CUs.
+
+// The dispatcher places consecutive workgroups on the 8 XCDs in turn.  Block
+// b runs logical item xcd_item(b, n), so each XCD gets one contiguous item
+// range: the gate_up items of a row, and later the down items that re-read
+// that row's partials (8 column pairs x the same h-blocks), share an L2.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_item(int b, int n) {
+  return n % kXcds ? b : (b % kXcds) * (n / kXcds) + b / kXcds;
+}
+
 template <int KG, int KTA>
 __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_gate_up_items(FusedMoe p) {
   __shared__ float s_red[4][64][4];
   __shared__ uint32_t s_x[256];
-  const int l = blockIdx.x / p.nA, a = blockIdx.x % p.nA;
+  const int g = xcd_item(blockIdx.x, gridDim.x);
+  const int l = g / p.nA, a = g % p.nA;
   const auto code = load_gate_up<KG, KTA>(p, l, a);
-  run_gate_up<KG, KTA, false>(p, l, a, code, s_x, s_red);
+  run_gate_up<KG, KTA, false, false>(p, l, a, code, s_x, s_red);
 }
 
 template <int KG, int KD, int KTB>
@@ -422,11 +447,12 @@ __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_down_items(FusedMoe p)
   __shared__ int s_flag;
   constexpr int kHB = KTB >= 8 ? KTB / 8 : 1;
   const int tid = threadIdx.x;
-  const int l = blockIdx.x / p.nB, bi = blockIdx.x % p.nB;
+  const int g = xcd_item(blockIdx.x, gridDim.x);
+  const int l = g / p.nB, bi = g % p.nB;
   const int kb = bi % p.NKB, rc = bi / p.NKB, cp = rc % p.NCP, r = rc / p.NCP;
   const int t = r / p.top_k, hb0 = (KTB * kb) / 8;
   const auto code = load_down<KD, KTB>(p, l, bi);
-  if ((tid >> 6) < kHB) down_inputs(p, l, r, hb0 + (tid >> 6), s_x + 64 * (tid >> 6));
+  if ((tid >> 6) < kHB) down_inputs<false>(p, l, r, hb0 + (tid >> 6), s_x + 64 * (tid >> 6));
   __syncthreads();
   compute_item<KD, KTB>(code, s_x + ((KTB * kb) % 8) * 8, s_red,
                         p.partB + ((size_t)l * p.nB + bi) * 256);
