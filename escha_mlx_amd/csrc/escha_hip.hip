@@ -11,6 +11,7 @@
 
 #include "../../include/escha_hip.h"
 #include "fused.hpp"
+#include "mfma.hpp"
 
 namespace {
 
@@ -282,6 +283,25 @@ int esc_dense_gemm_rows_out(const uint16_t* xh, const uint32_t* code, const floa
                    : ExactOutF<2, false>::run(R, xh, code, rout, M, TK, TN, rs, out, s);
   return use_lut ? ExactOutF<3, true>::run(R, xh, code, rout, M, TK, TN, rs, out, s)
                  : ExactOutF<3, false>::run(R, xh, code, rout, M, TK, TN, rs, out, s);
+}
+
+int esc_gemm_mfma(const uint16_t* xh, const uint32_t* code, int M, int K, int IC, int OC,
+                  int use_lut, float* mid, void* stream) {
+  if (int rc = check_proj(K, IC, OC)) return rc;
+  ESC_REQUIRE(xh && code && mid, "null pointer");
+  ESC_REQUIRE(M >= 0, "negative row count");
+  (void)use_lut;  // the table holds the hash's own values: both decodes give the same bits
+  if (M == 0) return ESC_OK;
+  const int TK = IC / 16, TN = OC / 16;
+  const int blocks = ((M + esc::kMmaRows - 1) / esc::kMmaRows) * (TN / 8);
+  hipStream_t s = S(stream);
+  if (K == 2)
+    hipLaunchKernelGGL(esc::k_gemm_mfma<2>, dim3(blocks), dim3(esc::kMmaThreads), 0, s, xh, code,
+                       M, TK, TN, mid);
+  else
+    hipLaunchKernelGGL(esc::k_gemm_mfma<3>, dim3(blocks), dim3(esc::kMmaThreads), 0, s, xh, code,
+                       M, TK, TN, mid);
+  return launched("k_gemm_mfma");
 }
 
 int esc_build_groups(const int32_t* row_expert, int m, int E, int R, int n_groups,

@@ -25,6 +25,10 @@ SUPPORTED_K = frozenset({2, 3})
 _CONFIG_LEN = 6
 _PRODUCTION_CODEBOOK = 1
 DENSE_R_MAX = 16
+# Row count at which the module switches to the matrix-core GEMM: the size
+# policy's R = 16 (the reference gates its matrix kernel the same way,
+# escha_mlx/dense.py:316-322).
+DENSE_MAT_R = 16
 
 
 def _check_scale(name: str, vec, expect: int) -> None:
@@ -131,6 +135,7 @@ class EschaLinear(torch.nn.Module):
         self._lut = envs.use_lut()
         self._exact = envs.use_exact()
         self._block_r_pin = envs.dense_block_r_pin()
+        self._mat = envs.dense_mat()
 
     @property
     def K(self) -> int:
@@ -143,7 +148,9 @@ class EschaLinear(torch.nn.Module):
         m = rows.shape[0]
         xh = ops.scaled_had(rows, w.rin, None)
         r = dense_block_r(m, self._block_r_pin)
-        if m > 1 and r <= 8:
+        if self._mat and r == DENSE_MAT_R:
+            y = ops.scaled_had_out(ops.dense_gemm_mat(xh, w.code, w.K, w.IC, w.OC), w.rout, None)
+        elif m > 1 and r <= 8:
             y = ops.dense_gemm_rows_direct_out(xh, w.code, w.rout, w.K, w.IC, w.OC, r,
                                                lut=self._lut)
         elif r > 1:

@@ -9,6 +9,11 @@ ValueError naming the variable (escha_mlx/envs.py:73-82).
                                 the split-K tolerance path)
   ESCHA_MLX_BLOCK_R        int  pin MoE rows per group (default: size policy)
   ESCHA_MLX_DENSE_BLOCK_R  int  pin dense rows per group (default: size policy)
+  ESCHA_MLX_DENSE_MAT      0/1  matrix-core GEMM for dense projections of >= 16
+                                rows.  Unset = on: the reference ships it off
+                                (escha_mlx/msl.py:1729-1759) because the sum is
+                                reassociated; on MI355X the matrix cores are the
+                                prefill path, so it is on unless set to 0
 
 Dropped on purpose (Apple-measured negatives with no MI355X analogue, see
 escha_mlx/msl.py:1145-1287): FETCH=shuffle, SPLITK, SORTX, PREFETCH,
@@ -47,6 +52,10 @@ def use_lut() -> bool:
 
 def use_exact() -> bool:
     return _flag("ESCHA_HIP_EXACT", False)
+
+
+def dense_mat() -> bool:
+    return _flag("ESCHA_MLX_DENSE_MAT", True)
 
 
 def block_r_pin() -> int | None:

@@ -201,6 +201,18 @@ def dense_gemm_rows_direct_out(xh: torch.Tensor, code_u32: torch.Tensor, rout: t
     return out
 
 
+def dense_gemm_mat(xh: torch.Tensor, code_u32: torch.Tensor, K: int, IC: int, OC: int,
+                   lut: bool | None = None) -> torch.Tensor:
+    """Matrix-core dense GEMM -> mid f32 [m, OC] (msl.py:1762-1782).  Deterministic,
+    reassociated float32 sum (tolerance contract); decoded weights bit-exact."""
+    _dev(xh, code_u32)
+    m = xh.shape[0]
+    mid = torch.empty((m, OC), dtype=torch.float32, device=xh.device)
+    _lib.call("esc_gemm_mfma", _ptr(xh), _ptr(_as_u32(code_u32)), m, K, IC, OC, _lut_flag(lut),
+              _ptr(mid), _stream())
+    return mid
+
+
 def build_groups(row_expert: torch.Tensor, E: int, R: int, n_groups: int):
     """Device sort-and-pack of rows into R-row expert groups (moe.py:30-78)."""
     _dev(row_expert)

@@ -97,6 +97,15 @@ int esc_dense_gemm_rows_out(const uint16_t* xh, const uint32_t* code, const floa
                             int R, int K, int IC, int OC, int use_lut, float rs, uint16_t* out,
                             void* stream);
 
+/* mid f32 [M][OC] = xh f16 [M][IC] @ decode(code [TK][TN][8K]) on the matrix
+ * cores (v_mfma_f32_32x32x16_f16, 256 rows x 128 columns per workgroup).
+ * Decoded weights are bit-exact; the float32 sum is reassociated
+ * (deterministic; tolerance contract).  use_lut is accepted for the call
+ * surface: table and hash decode give identical weights.
+ * Mirrors msl.dense_gemm_mat (escha_mlx/msl.py:1762-1782, source 1608-1708). */
+int esc_gemm_mfma(const uint16_t* xh, const uint32_t* code, int M, int K, int IC, int OC,
+                  int use_lut, float* mid, void* stream);
+
 /* Sort rows by expert into R-row groups (integer only, on device).
  * rows_idx [n_groups*R], group_expert [n_groups].
  * Mirrors moe.build_groups (escha_mlx/moe.py:30-78). */
