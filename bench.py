@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--only", choices=["both", "sustained", "chained"], default="both")
     ap.add_argument("--probe", action="store_true",
                     help="run the calibration copy and two sustained calls, untimed (for PMC)")
+    ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5], default=3,
+                    help="BASELINE config; 3 (the headline metric) by default")
     return ap.parse_args()
 
 
@@ -222,12 +224,178 @@ def probe(torch, args):
           flush=True)
 
 
+# ---------------------------------------------------------------- other configs
+# (secondary lines: `python bench.py --config N`; the headline is config 3)
+
+def _sgn(torch, n, g, dev):
+    return torch.where(torch.rand(n, generator=g, device=dev) < 0.5, -1.0, 1.0)
+
+
+def _dense_proj(torch, ic, oc, K, copies, g, dev):
+    """`copies` independent coded streams of one projection (cold rotation),
+    rin = +-1, rout = +-U[0.5,1.5]*1e-2 (f32)."""
+    code = [torch.randint(-2**31, 2**31 - 1, (ic // 16, oc // 16, 8 * K), generator=g, device=dev,
+                          dtype=torch.int32) for _ in range(copies)]
+    rin = _sgn(torch, ic, g, dev).float()
+    rout = (_sgn(torch, oc, g, dev) * (0.5 + torch.rand(oc, generator=g, device=dev)) * 1e-2).float()
+    return dict(ic=ic, oc=oc, K=K, code=code, rin=rin, rout=rout)
+
+
+def _linear(ops, P, x, i, lut, mat=True):
+    """One EschaLinear forward (escha_mlx/dense.py:337-362) on copy i of P."""
+    from escha_mlx_amd.dense import DENSE_MAT_R, dense_block_r
+    code = P["code"][i % len(P["code"])]
+    m = x.shape[0]
+    xh = ops.scaled_had(x, P["rin"], None)
+    r = dense_block_r(m)
+    if mat and r == DENSE_MAT_R:
+        return ops.scaled_had_out(ops.dense_gemm_mat(xh, code, P["K"], P["ic"], P["oc"]),
+                                  P["rout"], None)
+    if m > 1 and r <= 8:
+        return ops.dense_gemm_rows_direct_out(xh, code, P["rout"], P["K"], P["ic"], P["oc"], r,
+                                              lut=lut)
+    if r > 1:
+        return ops.scaled_had_out(ops.dense_gemm_rows(xh, code, P["K"], P["ic"], P["oc"], r,
+                                                      lut=lut), P["rout"], None)
+    return ops.gemv_fast_out(xh, code, None, P["rout"], P["K"], P["ic"], P["oc"], lut=lut)
+
+
+def bench_dense(args, torch, ops, cfg):
+    dev = "cuda:0"
+    g = torch.Generator(device=dev)
+    stream = torch.cuda.current_stream()
+    res = {"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "data": "synthetic: uniform-random code "
+           "streams, +-1 rin, +-U[0.5,1.5]e-2 rout, x ~ N(0,1) f16"}
+    if cfg == 1:
+        g.manual_seed(0)
+        P = _dense_proj(torch, 2048, 2048, 2, 1024, g, dev)   # 1 GiB of code, rotated
+        x = torch.randn(1, 2048, generator=g, device=dev).half()
+        ms = timed(torch, lambda i: _linear(ops, P, x, i, False), args.steps * 50,
+                   args.warmup, stream)
+        b = 2048 * 2048 * 2 // 8
+        res.update(metric="coded-weight GB/s, one 2048x2048 K2 projection at batch 1",
+                   value=round(b / (ms * 1e-3) / 1e9, 2), unit="GB/s", ms_per_step=round(ms, 5),
+                   dtype="u32 codes -> f16 weights (hash), f32 accumulate",
+                   config={"workload": "config 1: EschaLinear 2048x2048 K2 hash, M=1, 1024 "
+                                       "code copies rotated (1 GiB, cold)"},
+                   us_per_call=round(ms * 1e3, 3))
+        return res
+    if cfg == 2:
+        g.manual_seed(1)
+        L = 8   # 8 layer copies x 93 MB = 745 MB rotated
+        projs = [("q", 5120, 5120, 2, True), ("k", 5120, 5120, 2, True), ("v", 5120, 5120, 2, True),
+                 ("o", 5120, 5120, 2, True), ("up", 5120, 17408, 3, False),
+                 ("down", 17408, 5120, 3, False)]
+        P = {n: (_dense_proj(torch, ic, oc, K, L, g, dev), lut) for n, ic, oc, K, lut in projs}
+        per = {}
+        total_b = sum(ic * oc * K // 8 for _, ic, oc, K, _ in projs)
+        for M in (1, 4):
+            xs = {n: torch.randn(M, P[n][0]["ic"], generator=g, device=dev).half() for n in P}
+            t_layer = 0.0
+            for n, (pp, lut) in P.items():
+                ms = timed(torch, lambda i, pp=pp, lut=lut, n=n: _linear(ops, pp, xs[n], i, lut),
+                           args.steps * 5, args.warmup, stream)
+                b = pp["ic"] * pp["oc"] * pp["K"] // 8
+                per[f"M{M}_{n}_us"] = round(ms * 1e3, 2)
+                per[f"M{M}_{n}_gbs"] = round(b / (ms * 1e-3) / 1e9, 1)
+                t_layer += ms
+            per[f"M{M}_layer_us"] = round(t_layer * 1e3, 2)
+            per[f"M{M}_layer_gbs"] = round(total_b / (t_layer * 1e-3) / 1e9, 1)
+            per[f"M{M}_tok_s_per_layer"] = round(M / (t_layer * 1e-3), 1)
+        res.update(metric="coded-weight GB/s of one dense decoder layer (q,k,v,o K2 LUT, up/down "
+                          "K3) at batch 1", value=per["M1_layer_gbs"], unit="GB/s",
+                   ms_per_step=round(per["M1_layer_us"] / 1e3, 5),
+                   dtype="u32 codes -> f16 weights (LUT q/k/v/o, hash up/down), f32 accumulate",
+                   config={"workload": "config 2: 27B-class dense layer, 5120 hidden, M=1 and "
+                                       "M=4, 8 layer copies rotated (745 MB, cold)"},
+                   bytes_per_layer=total_b, **per)
+        return res
+    if cfg == 5:
+        g.manual_seed(4)
+        M = 2048
+        up = _dense_proj(torch, 5120, 17408, 3, 1, g, dev)
+        o = _dense_proj(torch, 5120, 5120, 2, 1, g, dev)
+        x = torch.randn(M, 5120, generator=g, device=dev).half()
+        flop = 2 * M * 5120 * (17408 + 5120)
+        xh_up = ops.scaled_had(x, up["rin"], None)
+        xh_o = ops.scaled_had(x, o["rin"], None)
+        ms_gu = timed(torch, lambda i: ops.dense_gemm_mat(xh_up, up["code"][0], 3, 5120, 17408),
+                      args.steps, args.warmup, stream)
+        ms_go = timed(torch, lambda i: ops.dense_gemm_mat(xh_o, o["code"][0], 2, 5120, 5120),
+                      args.steps, args.warmup, stream)
+        ms_mod = timed(torch, lambda i: (_linear(ops, up, x, i, False), _linear(ops, o, x, i, False)),
+                       args.steps, args.warmup, stream)
+        tf_k = flop / ((ms_gu + ms_go) * 1e-3) / 1e12
+        res.update(metric="prefill TFLOP/s, 2048 tokens through coded up (K3) + o (K2)",
+                   value=round(flop / (ms_mod * 1e-3) / 1e12, 2), unit="TFLOP/s",
+                   ms_per_step=round(ms_mod, 4), dtype="f16 x f16 -> f32 (MFMA), K2/K3 codes",
+                   config={"workload": "config 5: M=2048, up 5120->17408 K3 + o 5120x5120 K2, "
+                                       "EschaLinear (input transform, MFMA GEMM, output "
+                                       "transform)"},
+                   tok_s=round(M / (ms_mod * 1e-3), 1),
+                   gemm_up_us=round(ms_gu * 1e3, 1), gemm_o_us=round(ms_go * 1e3, 1),
+                   roofline={"bound": "mfma", "achieved": round(tf_k, 1), "peak": 2500.0,
+                             "unit": "TFLOP/s", "frac": round(tf_k / 2500.0, 4), "traffic": None,
+                             "kernel": "k_gemm_mfma<3> + k_gemm_mfma<2>",
+                             "flop_per_launch_pair": flop})
+        return res
+    raise SystemExit(f"config {cfg}: not measured by this bench")
+
+
+def bench_c4(args, torch, ops):
+    """Config 4: the MoE layer at 32 tokens (m = 256 routed rows)."""
+    from escha_mlx_amd import moe
+    dev = "cuda:0"
+    T, L = 32, 8
+    layers = make_layers(torch, L, dev, seed=3)
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    recs = []
+    for Ld in layers:
+        logits = torch.randn(T, E, generator=g, device=dev)
+        ids, scores = moe.route(logits, TOP_K)
+        x = torch.randn(T, H, generator=g, device=dev).half()
+        recs.append(dict(Ld, ids=ids, scores=scores, x=x,
+                         y=torch.empty(T, H, dtype=torch.float16, device=dev),
+                         distinct=int(torch.unique(ids).numel())))
+    ws = torch.zeros(ops.moe_expert_path_workspace(T, TOP_K, E, H, I), dtype=torch.uint8, device=dev)
+
+    def step(i):
+        R_ = recs[i % L]
+        ops.moe_expert_path(R_["x"], R_["ids"], R_["scores"], R_["gu_code"], R_["gu_rin"],
+                            R_["gu_rout"], K, R_["dn_code"], R_["dn_rin"], R_["dn_rout"], K,
+                            ws=ws, out=R_["y"])
+    ms = timed(torch, step, args.steps * L, args.warmup, stream)
+    distinct = sum(r["distinct"] for r in recs) / L
+    b = distinct * (BYTES_GU + BYTES_DN)
+    return {"metric": "coded-weight GB/s (distinct experts) + tok/s, MoE layer at batch 32",
+            "value": round(b / (ms * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "u32 codes -> f16 weights (hash), f32 accumulate",
+            "data": "synthetic, seeded logits [32,256] per layer, 8 layer stacks rotated",
+            "config": {"workload": "config 4: E=256, H=2048, I=512, top-8, T=32 (m=256 rows)"},
+            "distinct_experts_per_layer": distinct, "tok_s_per_layer": round(T / (ms * 1e-3), 1)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus N>1 is not supported "
                                    "(the sharding design is described, not built)"}))
         sys.exit(2)
+    if args.config != 3:
+        import torch
+
+        from escha_mlx_amd import ops
+        torch.cuda.set_device(0)
+        ops.init()
+        res = bench_c4(args, torch, ops) if args.config == 4 else bench_dense(args, torch, ops,
+                                                                              args.config)
+        print(json.dumps(res))
+        return
     traffic, traffic_detail = None, "not measured (--no-traffic)"
     if not args.probe and not args.no_traffic and args.only != "chained":
         traffic, traffic_detail = measure_traffic(args.layers)

@@ -37,6 +37,16 @@ __device__ __forceinline__ half_t to_f16(float x) {
   return (half_t)x;
 }
 
+// Workgroup barrier for LDS hand-offs only.  __syncthreads() also waits for
+// every outstanding global load of the wave (one vmcnt counter on gfx9),
+// which would stall on register prefetches issued just before it; this waits
+// for the wave's LDS operations only.
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
 // ---------------------------------------------------------------- lane map
 // Row / column of trellis step t inside its 16x16 tile.
 __host__ __device__ constexpr int step_row(int t) {

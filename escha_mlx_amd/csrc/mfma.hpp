@@ -9,9 +9,8 @@
 // Block = 256 threads (4 waves), tile 256 rows x 128 columns (8 code tiles),
 // K walked in stages of 2 kt (32 inputs), double-buffered through LDS:
 //   * decode: per kt each thread decodes 8 weights, rows 8h..8h+7 of one
-//     column, straight into the f16 B operand layout in LDS.  Wave w decodes
-//     half h = w & 1 of the columns with jhi = w >> 1 (steps with j >= 4), so
-//     every lane of a wave has the same window offset inside its words.
+//     column, straight into the f16 B operand layout in LDS (wave w decodes
+//     half h = w & 1 of the columns with jhi = w >> 1).
 //   * X: the block's 256 rows x 32 inputs are staged to LDS once per stage.
 //   * MFMA: wave (wm, wn) owns rows 128wm.. and columns 64wn..; per kt it runs
 //     4 x 2 v_mfma_f32_32x32x16_f16 (A: lane l holds row l%32, inputs
@@ -70,20 +69,26 @@ __device__ __forceinline__ uint4 mma_decode8<2>(const uint32_t (&w)[3], uint32_t
   return r;
 }
 
-// K=3: windows 3 bits apart; each state is one shift or funnel shift into the
-// low half (the u16 hash ignores the bits above).  O is the wave-uniform offset.
-template <int O>
-__device__ __forceinline__ uint4 mma_decode8_k3(const uint32_t (&w)[4]) {
+// K=3: windows 3 bits apart.  The lane's words are first re-aligned so the
+// stream starts at step t0's first bit (three funnel shifts by the lane's
+// offset o); every state is then one shift or funnel shift at a compile-time
+// position into the low half (the u16 hash ignores the bits above), so the
+// decode has no branches.
+template <>
+__device__ __forceinline__ uint4 mma_decode8<3>(const uint32_t (&w)[4], uint32_t o) {
   const uint32_t clo = kClo, chi = kChi;
+  uint32_t a3w[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) a3w[k] = __builtin_amdgcn_alignbit(w[k], w[k + 1], 32u - o);
   uint32_t r[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     const int i = q >> 1, e = q & 1;
-    const int pos = O + 3 * (8 * i + e);
+    const int pos = 3 * (8 * i + e);
     const int a = pos >> 5, off = pos & 31;
-    const uint32_t s = off <= 16 ? w[a] >> (16 - off)
-                                 : __builtin_amdgcn_alignbit(w[a], w[a + 1], 48 - off);
-    r[q] = mask_xor(hash_x<false>(s, clo, chi));
+    const uint32_t st = off <= 16 ? a3w[a] >> (16 - off)
+                                  : __builtin_amdgcn_alignbit(a3w[a], a3w[a + 1], 48 - off);
+    r[q] = mask_xor(hash_x<false>(st, clo, chi));
   }
   uint4 v;
   v.x = halves_sum2(r[0], r[1]);
@@ -91,17 +96,6 @@ __device__ __forceinline__ uint4 mma_decode8_k3(const uint32_t (&w)[4]) {
   v.z = halves_sum2(r[4], r[5]);
   v.w = halves_sum2(r[6], r[7]);
   return v;
-}
-
-template <>
-__device__ __forceinline__ uint4 mma_decode8<3>(const uint32_t (&w)[4], uint32_t o) {
-  // o = (12 jhi + 6 h - 13) mod 32, uniform across the wave
-  switch (o) {
-    case 19: return mma_decode8_k3<19>(w);
-    case 25: return mma_decode8_k3<25>(w);
-    case 31: return mma_decode8_k3<31>(w);
-    default: return mma_decode8_k3<5>(w);
-  }
 }
 
 template <int K>
@@ -137,7 +131,7 @@ __global__ __launch_bounds__(kMmaThreads, 2) void k_gemm_mfma(const uint16_t* __
   const int n = 16 * ti + 2 * (a3 + 4 * jhi) + bq;
   int st0 = K * (64 * a3 + 32 * bq + 4 * jhi + 2 * h) - (16 - K);
   if (st0 < 0) st0 += 256 * K;
-  const uint32_t o = __builtin_amdgcn_readfirstlane((uint32_t)(st0 & 31));
+  const uint32_t o = (uint32_t)(st0 & 31);  // 1..31: never 0 (K=2: 18..30, K=3: 5..31)
   int woff[NW];
 #pragma unroll
   for (int k = 0; k < NW; ++k) woff[k] = ((st0 >> 5) + k) % WPT;
@@ -153,27 +147,32 @@ __global__ __launch_bounds__(kMmaThreads, 2) void k_gemm_mfma(const uint16_t* __
     xrow[i] = xh + (size_t)r * IC + 8 * xchunk;
   }
 
-  uint32_t cw[2][NW];
-  uint4 xv[4];
-  auto load_stage = [&](int s) {
+  // global -> register staging of one stage, two sets in flight: the loads
+  // of stage s+2 are issued two MFMA phases before their data is needed
+  struct Regs {
+    uint32_t cw[2][NW];
+    uint4 xv[4];
+  };
+  auto load_stage = [&](Regs& r, int s) {
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
       const uint32_t* tp = ctile + (size_t)(2 * s + k2) * kstride;
 #pragma unroll
-      for (int k = 0; k < NW; ++k) cw[k2][k] = tp[woff[k]];
+      for (int k = 0; k < NW; ++k) r.cw[k2][k] = tp[woff[k]];
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xv[i] = *reinterpret_cast<const uint4*>(xrow[i] + 32 * s);
+    for (int i = 0; i < 4; ++i) r.xv[i] = *reinterpret_cast<const uint4*>(xrow[i] + 32 * s);
   };
-  auto store_stage = [&](int buf) {
+  auto store_stage = [&](const Regs& r, int buf) {
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
-      const uint4 v = mma_decode8<K>(cw[k2], o);
+      const uint4 v = mma_decode8<K>(r.cw[k2], o);
       *reinterpret_cast<uint4*>(&s_b[buf][n * kMmaPitch + 16 * k2 + 8 * h]) = v;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<uint4*>(&s_x[buf][(64 * i + (tid >> 2)) * kMmaPitch + 8 * xchunk]) = xv[i];
+      *reinterpret_cast<uint4*>(&s_x[buf][(64 * i + (tid >> 2)) * kMmaPitch + 8 * xchunk]) =
+          r.xv[i];
   };
 
   // ---- MFMA role
@@ -185,15 +184,7 @@ __global__ __launch_bounds__(kMmaThreads, 2) void k_gemm_mfma(const uint16_t* __
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  const int NS = TK / 2;
-  load_stage(0);
-  store_stage(0);
-  __syncthreads();
-  for (int s = 0; s < NS; ++s) {
-    const int buf = s & 1;
-    const bool more = s + 1 < NS;
-    if (more) load_stage(s + 1);
+  auto mma_stage = [&](int buf) {
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
       half8_t a[4], b[2];
@@ -211,8 +202,48 @@ __global__ __launch_bounds__(kMmaThreads, 2) void k_gemm_mfma(const uint16_t* __
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
-    if (more) store_stage(buf ^ 1);
-    __syncthreads();
+  };
+
+  // Interleave one stage's 16 MFMAs with the decode of the next stage (VALU)
+  // and its LDS traffic: each 32-cycle MFMA hides about six VALU issues.
+  auto interleave = [] {
+    __builtin_amdgcn_sched_group_barrier(0x020, 16, 0);  // global loads first
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);   // k2 = 0 fragments
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);   // k2 = 1 fragments
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+  };
+
+  // stage s lives in LDS buffer s & 1; register set r_even carries the even
+  // stages, r_odd the odd ones (NS = TK / 2 is a multiple of 4).  Loads past
+  // the last stage re-read the last stage (in bounds, never stored to a
+  // buffer that is read again), which keeps each half straight-line code.
+  const int NS = TK / 2;
+  Regs r_even, r_odd;
+  load_stage(r_even, 0);
+  load_stage(r_odd, 1);
+  store_stage(r_even, 0);
+  load_stage(r_even, 2);
+  lds_barrier();
+  for (int s = 0; s < NS; s += 2) {
+    mma_stage(0);  // stage s
+    store_stage(r_odd, 1);
+    load_stage(r_odd, min(s + 3, NS - 1));
+    interleave();
+    lds_barrier();
+    mma_stage(1);  // stage s + 1
+    store_stage(r_even, 0);
+    load_stage(r_even, min(s + 4, NS - 1));
+    interleave();
+    lds_barrier();
   }
 
   // ---- epilogue: D register r of lane l -> row 8(r/4) + 4(l/32) + r%4, col l%32
