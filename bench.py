@@ -252,12 +252,41 @@ def _linear(ops, P, x, i, lut, mat=True):
         return ops.scaled_had_out(ops.dense_gemm_mat(xh, code, P["K"], P["ic"], P["oc"]),
                                   P["rout"], None)
     if m > 1 and r <= 8:
-        return ops.dense_gemm_rows_direct_out(xh, code, P["rout"], P["K"], P["ic"], P["oc"], r,
-                                              lut=lut)
+        return ops.dense_gemm_rows_fast_out(xh, code, P["rout"], P["K"], P["ic"], P["oc"],
+                                            max(r, 2), lut=lut)
     if r > 1:
         return ops.scaled_had_out(ops.dense_gemm_rows(xh, code, P["K"], P["ic"], P["oc"], r,
                                                       lut=lut), P["rout"], None)
     return ops.gemv_fast_out(xh, code, None, P["rout"], P["K"], P["ic"], P["oc"], lut=lut)
+
+
+def graph_time(torch, fns, steps: int, warmup: int, stream):
+    """Capture each fn of `fns` in its own HIP graph (one per cold copy), check
+    one replay against the eager result, then time `steps` replays in rotation
+    (ms per replay).  Graphs hold the launch sequence the host would otherwise
+    re-issue call by call."""
+    graphs, outs = [], []
+    eager = fns[0]()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns:   # warm the allocator outside capture
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for f in fns:
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            outs.append(f())
+        graphs.append(gr)
+    for rep in range(2):
+        graphs[0].replay()
+        torch.cuda.synchronize()
+        for a, b in zip(eager, outs[0]):
+            if not torch.equal(a, b):
+                raise SystemExit("graph replay differs from the eager result")
+    return timed(torch, lambda i: graphs[i % len(graphs)].replay(), steps, warmup, stream)
 
 
 def bench_dense(args, torch, ops, cfg):
@@ -271,15 +300,17 @@ def bench_dense(args, torch, ops, cfg):
         g.manual_seed(0)
         P = _dense_proj(torch, 2048, 2048, 2, 1024, g, dev)   # 1 GiB of code, rotated
         x = torch.randn(1, 2048, generator=g, device=dev).half()
-        ms = timed(torch, lambda i: _linear(ops, P, x, i, False), args.steps * 50,
-                   args.warmup, stream)
+        ms_eager = timed(torch, lambda i: _linear(ops, P, x, i, False), args.steps * 50,
+                         args.warmup, stream)
+        fns = [lambda i=i: (_linear(ops, P, x, i, False),) for i in range(512)]
+        ms = graph_time(torch, fns, args.steps * 50, args.warmup, stream)
         b = 2048 * 2048 * 2 // 8
         res.update(metric="coded-weight GB/s, one 2048x2048 K2 projection at batch 1",
                    value=round(b / (ms * 1e-3) / 1e9, 2), unit="GB/s", ms_per_step=round(ms, 5),
                    dtype="u32 codes -> f16 weights (hash), f32 accumulate",
-                   config={"workload": "config 1: EschaLinear 2048x2048 K2 hash, M=1, 1024 "
-                                       "code copies rotated (1 GiB, cold)"},
-                   us_per_call=round(ms * 1e3, 3))
+                   config={"workload": "config 1: EschaLinear 2048x2048 K2 hash, M=1, HIP "
+                                       "graph per call, 512 code copies rotated (512 MiB, cold)"},
+                   us_per_call=round(ms * 1e3, 3), eager_us_per_call=round(ms_eager * 1e3, 3))
         return res
     if cfg == 2:
         g.manual_seed(1)
@@ -294,12 +325,17 @@ def bench_dense(args, torch, ops, cfg):
             xs = {n: torch.randn(M, P[n][0]["ic"], generator=g, device=dev).half() for n in P}
             t_layer = 0.0
             for n, (pp, lut) in P.items():
-                ms = timed(torch, lambda i, pp=pp, lut=lut, n=n: _linear(ops, pp, xs[n], i, lut),
-                           args.steps * 5, args.warmup, stream)
+                fns = [lambda i=i, pp=pp, lut=lut, n=n: (_linear(ops, pp, xs[n], i, lut),)
+                       for i in range(L)]
+                ms = graph_time(torch, fns, args.steps * 5, args.warmup, stream)
                 b = pp["ic"] * pp["oc"] * pp["K"] // 8
                 per[f"M{M}_{n}_us"] = round(ms * 1e3, 2)
                 per[f"M{M}_{n}_gbs"] = round(b / (ms * 1e-3) / 1e9, 1)
                 t_layer += ms
+            fl = [lambda i=i: tuple(_linear(ops, pp, xs[n], i, lut) for n, (pp, lut) in P.items())
+                  for i in range(L)]
+            per[f"M{M}_layer_graph_us"] = round(graph_time(torch, fl, args.steps, args.warmup,
+                                                           stream) * 1e3, 2)
             per[f"M{M}_layer_us"] = round(t_layer * 1e3, 2)
             per[f"M{M}_layer_gbs"] = round(total_b / (t_layer * 1e-3) / 1e9, 1)
             per[f"M{M}_tok_s_per_layer"] = round(M / (t_layer * 1e-3), 1)
@@ -308,7 +344,8 @@ def bench_dense(args, torch, ops, cfg):
                    ms_per_step=round(per["M1_layer_us"] / 1e3, 5),
                    dtype="u32 codes -> f16 weights (LUT q/k/v/o, hash up/down), f32 accumulate",
                    config={"workload": "config 2: 27B-class dense layer, 5120 hidden, M=1 and "
-                                       "M=4, 8 layer copies rotated (745 MB, cold)"},
+                                       "M=4, HIP graph per projection, 8 layer copies rotated "
+                                       "(745 MB, cold)"},
                    bytes_per_layer=total_b, **per)
         return res
     if cfg == 5:
@@ -449,7 +486,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                          "traffic_detail": traffic_detail,
-                         "kernel": "k_moe_gate_up_items<2,16> + k_moe_down_items<2,2,16> "
+                         "kernel": "k_moe_gate_up_items<2,16,true> + k_moe_down_items<2,2,16,true> "
                                    "(one esc_moe_expert_path_layers call)",
                          "bytes_per_launch": bytes_call,
                          "avg_launch_us": round(ms * 1e3, 2)},

@@ -160,6 +160,27 @@ struct FastF {
   }
 };
 
+template <int K, bool LUT>
+struct FastRowsF {
+  template <int R>
+  static int go(const uint16_t* xh, const uint32_t* code, int M, int TK, int TN, int S,
+                float* part, hipStream_t s) {
+    const int tpw = K == 2 ? 16 : 8;
+    hipLaunchKernelGGL((esc::k_gemv_fast_rows<K, LUT, R>), dim3((TN + tpw - 1) / tpw, (M + R - 1) / R, S),
+                       dim3(256), 0, s, xh, code, M, TK, TN, TK / S, part);
+    return launched("k_gemv_fast_rows");
+  }
+  static int run(int R, const uint16_t* xh, const uint32_t* code, int M, int TK, int TN, int S,
+                 float* part, hipStream_t s) {
+    switch (R) {
+      case 2: return go<2>(xh, code, M, TK, TN, S, part, s);
+      case 4: return go<4>(xh, code, M, TK, TN, S, part, s);
+      case 8: return go<8>(xh, code, M, TK, TN, S, part, s);
+    }
+    return fail(ESC_EINVAL, "rows per block R=%d not in {2,4,8}", R);
+  }
+};
+
 }  // namespace
 
 extern "C" {
@@ -238,6 +259,41 @@ int esc_gemv_fast_out(const uint16_t* xh, const uint32_t* code, const int32_t* r
     return rc;
   hipLaunchKernelGGL(esc::k_splitk_out, dim3(OC / 128, M), dim3(64), 0, S(stream), part, Sp, M,
                      OC, rout, row_expert, rs, out);
+  return launched("k_splitk_out");
+}
+
+size_t esc_gemm_rows_fast_workspace(int M, int R, int K, int IC, int OC) {
+  if (check_proj(K, IC, OC) || M <= 0 || R <= 0) return 0;
+  return (size_t)fast_splits(K, (M + R - 1) / R, IC / 16, OC / 16) * M * OC * sizeof(float);
+}
+
+int esc_gemm_rows_fast_out(const uint16_t* xh, const uint32_t* code, const float* rout, int M,
+                           int R, int K, int IC, int OC, int use_lut, float rs, uint16_t* out,
+                           void* ws, size_t ws_bytes, void* stream) {
+  if (int rc = check_proj(K, IC, OC)) return rc;
+  ESC_REQUIRE(xh && code && rout && out, "null pointer");
+  ESC_REQUIRE(M >= 0, "negative row count");
+  ESC_REQUIRE(R == 2 || R == 4 || R == 8, "rows per block R=%d not in {2,4,8}", R);
+  if (M == 0) return ESC_OK;
+  const int TK = IC / 16, TN = OC / 16;
+  const int Sp = fast_splits(K, (M + R - 1) / R, TK, TN);
+  const size_t need = (size_t)Sp * M * OC * sizeof(float);
+  if (!ws || ws_bytes < need)
+    return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, need);
+  if (use_lut)
+    if (int rc = ensure_lut()) return rc;
+  float* part = static_cast<float*>(ws);
+  hipStream_t s = S(stream);
+  int rc;
+  if (K == 2)
+    rc = use_lut ? FastRowsF<2, true>::run(R, xh, code, M, TK, TN, Sp, part, s)
+                 : FastRowsF<2, false>::run(R, xh, code, M, TK, TN, Sp, part, s);
+  else
+    rc = use_lut ? FastRowsF<3, true>::run(R, xh, code, M, TK, TN, Sp, part, s)
+                 : FastRowsF<3, false>::run(R, xh, code, M, TK, TN, Sp, part, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(esc::k_splitk_out, dim3(OC / 128, M), dim3(64), 0, s, part, Sp, M, OC, rout,
+                     nullptr, rs, out);
   return launched("k_splitk_out");
 }
 
@@ -374,7 +430,7 @@ constexpr int kFusedMaxRows = 64;
 
 struct FusedPlan {
   int L, M, NB, NKC, NKB, NCP, nA, nB, grid;
-  size_t off_pa, off_pb, off_int, total;
+  size_t off_pa, off_pb, off_xh2, off_int, total;
   int n_int;
 };
 
@@ -406,7 +462,8 @@ FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput) {
   auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
   f.off_pa = 0;
   f.off_pb = al((size_t)L * f.nA * 256 * 4);
-  f.off_int = f.off_pb + al((size_t)L * f.nB * 256 * 4);
+  f.off_xh2 = f.off_pb + al((size_t)L * f.nB * 256 * 4);
+  f.off_int = f.off_xh2 + al((size_t)L * f.M * I * 2);
   f.n_int = L * (f.M * f.NB + f.nA + T * f.NCP) + 2;
   f.total = f.off_int + al((size_t)f.n_int * 4);
   return f;
@@ -421,6 +478,7 @@ esc::FusedMoe fused_args(const FusedPlan& f, void* ws, int T, int top_k, int H, 
   esc::FusedMoe p{};
   p.partA = reinterpret_cast<float*>(w + f.off_pa);
   p.partB = reinterpret_cast<float*>(w + f.off_pb);
+  p.xh2 = reinterpret_cast<uint16_t*>(w + f.off_xh2);
   p.cntA = ints;
   p.claimA = p.cntA + (size_t)f.L * f.M * f.NB;
   p.cntB = p.claimA + (size_t)f.L * f.nA;
@@ -444,21 +502,25 @@ template <int KG, int KD, bool TP>
 int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
   if constexpr (TP) {
     // two launches: every gate_up item, then every down item (grid unused);
-    // small items when there are few layers, large ones otherwise
+    // small items when there are few layers, large ones otherwise; the down
+    // inputs are precomputed once per (row, h-block) for multi-layer calls
     (void)grid;
+    const dim3 ga(p.L * p.nA), gb(p.L * p.nB), blk(esc::kFusedThreads);
     if (p.NKC == p.H / 128) {
-      hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 8>), dim3(p.L * p.nA),
-                         dim3(esc::kFusedThreads), 0, s, p);
+      hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 8, false>), ga, blk, 0, s, p);
       if (int rc = launched("k_moe_gate_up_items")) return rc;
-      hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, 4>), dim3(p.L * p.nB),
-                         dim3(esc::kFusedThreads), 0, s, p);
+      hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, 4, false>), gb, blk, 0, s, p);
       return launched("k_moe_down_items");
     }
-    hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 16>), dim3(p.L * p.nA),
-                       dim3(esc::kFusedThreads), 0, s, p);
+    if (p.L > 1) {
+      hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 16, true>), ga, blk, 0, s, p);
+      if (int rc = launched("k_moe_gate_up_items")) return rc;
+      hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, 16, true>), gb, blk, 0, s, p);
+      return launched("k_moe_down_items");
+    }
+    hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 16, false>), ga, blk, 0, s, p);
     if (int rc = launched("k_moe_gate_up_items")) return rc;
-    hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, 16>), dim3(p.L * p.nB),
-                       dim3(esc::kFusedThreads), 0, s, p);
+    hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, 16, false>), gb, blk, 0, s, p);
     return launched("k_moe_down_items");
   } else {
     hipLaunchKernelGGL((esc::k_moe_fused<KG, KD, 8, 4, true>), dim3(grid),

@@ -199,6 +199,120 @@ __device__ __forceinline__ void fast_tile_packed(const LaneWords<K>& lw, uint32_
   }
 }
 
+// R-row variant of fast_tile_packed: every state pair is decoded once (hash,
+// or two table reads from LDS into the two halves) and multiplied into R
+// rows' accumulators.  xp[r] are row r's input pairs (x_pairs).
+template <int K, bool LUT, int R>
+__device__ __forceinline__ void fast_tile_rows(const LaneWords<K>& lw, uint32_t wprev,
+                                               const uint32_t (*xp)[8], const uint16_t* lut,
+                                               float (*acc)[Geo<K>::NCOL]) {
+  using G = Geo<K>;
+  const uint32_t clo = kClo, chi = kChi;
+#pragma unroll
+  for (int u = 0; u < G::SPL; ++u) {
+    if ((u >> 3) & 1) continue;  // u+8 handled with u
+    uint32_t w2;
+    if constexpr (K == 2) {
+      const int rel = 2 * (u + 1) - 16;
+      const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
+      const uint32_t hi = a < 0 ? wprev : lw.w[a];
+      const uint32_t p = off == 0 ? hi : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 32 - off);
+      if constexpr (LUT)
+        w2 = (uint32_t)lut[p & 0xFFFFu] | ((uint32_t)lut[p >> 16] << 16);
+      else
+        w2 = halves_sum2(mask_xor(hash_x<false>(p, clo, chi)), mask_xor(hash_x<true>(p, clo, chi)));
+    } else {
+      uint32_t s2[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int uu = u + 8 * (1 - h);  // low half: step u+8, high half: step u
+        const int rel = 3 * (uu + 1) - 16;
+        const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
+        const uint32_t hi = a < 0 ? wprev : lw.w[a];
+        s2[h] = off <= 16 ? hi >> (16 - off)
+                          : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 48 - off);
+      }
+      if constexpr (LUT)
+        w2 = (uint32_t)lut[s2[0] & 0xFFFFu] | ((uint32_t)lut[s2[1] & 0xFFFFu] << 16);
+      else
+        w2 = halves_sum2(mask_xor(hash_x<false>(s2[0], clo, chi)),
+                         mask_xor(hash_x<false>(s2[1], clo, chi)));
+    }
+    const int ci = G::col_slot(u), xi = xpair_index(fast_row(u));
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r][ci] = dot2(xp[r][xi], w2, acc[r][ci]);
+  }
+}
+
+// Dense split-K GEMM for a few rows (2..8): part[z][row][OC] as k_gemv_fast,
+// with R rows per block sharing every decoded weight.  grid (ceil(TN/TPW),
+// ceil(M/R), S), block 256; rows past M read row M-1 and are not stored.
+template <int K, bool LUT, int R>
+__global__ __launch_bounds__(256) void k_gemv_fast_rows(const uint16_t* __restrict__ xh,
+                                                        const uint32_t* __restrict__ code, int M,
+                                                        int TK, int TN, int KS,
+                                                        float* __restrict__ part) {
+  using G = Geo<K>;
+  __shared__ uint16_t s_lut[LUT ? 65536 : 1];
+  __shared__ float s_red[4][64][G::NCOL];
+  stage_lut<LUT>(s_lut);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int ntg = blockIdx.x, row0 = blockIdx.y * R, z = blockIdx.z;
+  const int IC = TK * 16, OC = TN * 16;
+  const int q = lane % G::LPT, tile = lane / G::LPT;
+  const int src = tile * G::LPT + (q + G::LPT - 1) % G::LPT;
+  const bool valid = ntg * G::TPW + tile < TN;
+  const int KW = KS / 4;
+  const int kt0 = z * KS + wave * KW;
+  const uint32_t* xrow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    xrow[r] = reinterpret_cast<const uint32_t*>(xh + (size_t)min(row0 + r, M - 1) * IC);
+  float acc[R][G::NCOL];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int i = 0; i < G::NCOL; ++i) acc[r][i] = 0.f;
+  const size_t lane_off = (size_t)ntg * G::TPW * (8 * K) + (size_t)lane * G::WPL;
+  LaneWords<K> zero{};
+  LaneWords<K> cur = valid ? load_lane_words<K>(code + (size_t)kt0 * TN * (8 * K) + lane_off) : zero;
+  for (int k = 0; k < KW; ++k) {
+    const int kt = kt0 + k;
+    LaneWords<K> nxt = cur;
+    if (valid && k + 1 < KW)
+      nxt = load_lane_words<K>(code + (size_t)(kt + 1) * TN * (8 * K) + lane_off);
+    uint32_t xp[R][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      uint32_t xw[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xw[i] = xrow[r][8 * kt + i];
+      x_pairs(xw, xp[r]);
+    }
+    const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
+    fast_tile_rows<K, LUT, R>(cur, wprev, xp, s_lut, acc);
+    cur = nxt;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int i = 0; i < G::NCOL; ++i) s_red[wave][lane][i] = acc[r][i];
+    __syncthreads();
+    if (wave == 0 && valid && row0 + r < M) {
+      float* pr = part + ((size_t)z * M + row0 + r) * OC + (size_t)(ntg * G::TPW + tile) * 16;
+#pragma unroll
+      for (int i = 0; i < G::NCOL; ++i) {
+        float v = s_red[0][lane][i];
+        v = v + s_red[1][lane][i];
+        v = v + s_red[2][lane][i];
+        v = v + s_red[3][lane][i];
+        pr[G::col(q, i)] = v;
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // Partial GEMV: part[z][row][OC] = sum over the block's kt range.
 // grid (TN/TPW, M, S), block 256; KS = TK/S kt per block, KS % 4 == 0.
 // row_expert null -> dense (single stream).

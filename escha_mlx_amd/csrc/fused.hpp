@@ -87,6 +87,7 @@ struct FusedMoe {
   const MoeLayer* layers;   // [L] device array for multi-layer launches
   float* partA;  // [L][nA][256]
   float* partB;  // [L][nB][256]
+  uint16_t* xh2; // [L][M][I]   down inputs (two-launch path)
   int* cntA;     // [L][M*NB]  published gate_up items per (row, h-block)
   int* claimA;   // [L][nA]
   int* cntB;     // [L][T*NCP] finished down items per (token, column pair)
@@ -249,11 +250,13 @@ __device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, K
   if (PUBLISH && threadIdx.x == 0) publish_gate_up(p, l, a);
 }
 
-// h-block kb of row r (layer l) -> its 128 down inputs (f16 pairs) in s_x[0..63].
-// COH: the gate_up partials were published in this launch (device-coherent
-// loads); otherwise by an earlier launch (plain loads, which may hit L2).
+// h-block kb of row r (layer l) -> this lane's pair of its 128 down inputs
+// (f16 pair, columns 128kb + 2lane, +1): the gate_up partials summed in fixed
+// kc order, the gate_up output transform, SwiGLU and the down input transform.
+// COH: the partials were published in this launch (device-coherent loads);
+// otherwise by an earlier launch (plain loads, which may hit L2).
 template <bool COH = true>
-__device__ void down_inputs(const FusedMoe& p, int l, int r, int kb, uint32_t* s_x) {
+__device__ uint32_t h_pair(const FusedMoe& p, int l, int r, int kb) {
   const int lane = threadIdx.x & 63;
   const MoeLayer& L = p.layer(l);
   const int e = L.ids[r];
@@ -292,7 +295,13 @@ __device__ void down_inputs(const FusedMoe& p, int l, int r, int kb, uint32_t* s
   float v0 = (float)h0 * ri[0];
   float v1 = (float)h1 * ri[1];
   h128_wave(v0, v1);
-  s_x[lane] = pack2(to_f16(v0 * kRS), to_f16(v1 * kRS));
+  return pack2(to_f16(v0 * kRS), to_f16(v1 * kRS));
+}
+
+// h-block kb of row r (layer l) -> its 128 down inputs (f16 pairs) in s_x[0..63].
+template <bool COH = true>
+__device__ void down_inputs(const FusedMoe& p, int l, int r, int kb, uint32_t* s_x) {
+  s_x[threadIdx.x & 63] = h_pair<COH>(p, l, r, kb);
 }
 
 // Last down item of (layer l, token t, column pair cp): every slot's 256
@@ -429,17 +438,43 @@ __device__ __forceinline__ int xcd_item(int b, int n) {
   return n % kXcds ? b : (b % kXcds) * (n / kXcds) + b / kXcds;
 }
 
-template <int KG, int KTA>
+// gate_up item a of layer l.  PREH (many token-layers per launch): the last
+// of the NKC items of its (row, h-block) to finish turns the h-block's
+// partials into the 128 down inputs (xh2), so every down item reads them
+// ready-made instead of redoing the transforms.  Without PREH (one
+// token-layer, latency-bound) the partials go out with plain stores and each
+// down item derives its own inputs, which keeps the counter round trip off
+// the critical path.
+template <int KG, int KTA, bool PREH>
 __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_gate_up_items(FusedMoe p) {
   __shared__ float s_red[4][64][4];
   __shared__ uint32_t s_x[256];
+  __shared__ int s_last;
+  const int tid = threadIdx.x;
   const int g = xcd_item(blockIdx.x, gridDim.x);
   const int l = g / p.nA, a = g % p.nA;
   const auto code = load_gate_up<KG, KTA>(p, l, a);
-  run_gate_up<KG, KTA, false, false>(p, l, a, code, s_x, s_red);
+  run_gate_up<KG, KTA, false, PREH>(p, l, a, code, s_x, s_red);
+  if constexpr (PREH) {
+    wait_vm();  // this wave's partial stores have completed
+    __syncthreads();
+    const int rb = a / p.NKC, b = rb % p.NB, r = rb / p.NB;
+    const int M = p.T * p.top_k;
+    if (tid == 0) {
+      int* c = &p.cntA[((size_t)l * M + r) * p.NB + b];
+      const bool last = add_relaxed(c, 1) == p.NKC - 1;
+      if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (s_last && tid < 64) {
+      const uint32_t v = h_pair<true>(p, l, r, b);
+      reinterpret_cast<uint32_t*>(p.xh2 + ((size_t)l * M + r) * p.I + 128 * b)[tid] = v;
+    }
+  }
 }
 
-template <int KG, int KD, int KTB>
+template <int KG, int KD, int KTB, bool PREH>
 __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_down_items(FusedMoe p) {
   __shared__ float s_red[4][64][4];
   __shared__ uint32_t s_x[256];
@@ -452,7 +487,14 @@ __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_down_items(FusedMoe p)
   const int kb = bi % p.NKB, rc = bi / p.NKB, cp = rc % p.NCP, r = rc / p.NCP;
   const int t = r / p.top_k, hb0 = (KTB * kb) / 8;
   const auto code = load_down<KD, KTB>(p, l, bi);
-  if ((tid >> 6) < kHB) down_inputs<false>(p, l, r, hb0 + (tid >> 6), s_x + 64 * (tid >> 6));
+  if ((tid >> 6) < kHB) {
+    const int w = tid >> 6;
+    if constexpr (PREH)
+      s_x[64 * w + (tid & 63)] = reinterpret_cast<const uint32_t*>(
+          p.xh2 + ((size_t)l * p.T * p.top_k + r) * p.I + 128 * (hb0 + w))[tid & 63];
+    else
+      down_inputs<false>(p, l, r, hb0 + w, s_x + 64 * w);
+  }
   __syncthreads();
   compute_item<KD, KTB>(code, s_x + ((KTB * kb) % 8) * 8, s_red,
                         p.partB + ((size_t)l * p.nB + bi) * 256);

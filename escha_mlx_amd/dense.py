@@ -150,6 +150,9 @@ class EschaLinear(torch.nn.Module):
         r = dense_block_r(m, self._block_r_pin)
         if self._mat and r == DENSE_MAT_R:
             y = ops.scaled_had_out(ops.dense_gemm_mat(xh, w.code, w.K, w.IC, w.OC), w.rout, None)
+        elif m > 1 and r <= 8 and not self._exact:
+            y = ops.dense_gemm_rows_fast_out(xh, w.code, w.rout, w.K, w.IC, w.OC, max(r, 2),
+                                             lut=self._lut)
         elif m > 1 and r <= 8:
             y = ops.dense_gemm_rows_direct_out(xh, w.code, w.rout, w.K, w.IC, w.OC, r,
                                                lut=self._lut)

@@ -201,6 +201,21 @@ def dense_gemm_rows_direct_out(xh: torch.Tensor, code_u32: torch.Tensor, rout: t
     return out
 
 
+def dense_gemm_rows_fast_out(xh: torch.Tensor, code_u32: torch.Tensor, rout: torch.Tensor,
+                             K: int, IC: int, OC: int, R: int, rs: float = RS,
+                             lut: bool | None = None) -> torch.Tensor:
+    """Dense rows, split-K with R rows per decode + fused output transform ->
+    f16 [m, OC] (tolerance contract; msl.py:1844-1870 policy)."""
+    _dev(xh, code_u32, rout)
+    m = xh.shape[0]
+    out = torch.empty((m, OC), dtype=torch.float16, device=xh.device)
+    nbytes = _lib.load().esc_gemm_rows_fast_workspace(m, R, K, IC, OC) if m else 0
+    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=xh.device)
+    _lib.call("esc_gemm_rows_fast_out", _ptr(xh), _ptr(_as_u32(code_u32)), _ptr(rout), m, R, K,
+              IC, OC, _lut_flag(lut), rs, _ptr(out), _ptr(ws), nbytes, _stream())
+    return out
+
+
 def dense_gemm_mat(xh: torch.Tensor, code_u32: torch.Tensor, K: int, IC: int, OC: int,
                    lut: bool | None = None) -> torch.Tensor:
     """Matrix-core dense GEMM -> mid f32 [m, OC] (msl.py:1762-1782).  Deterministic,

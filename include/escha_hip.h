@@ -106,6 +106,18 @@ int esc_dense_gemm_rows_out(const uint16_t* xh, const uint32_t* code, const floa
 int esc_gemm_mfma(const uint16_t* xh, const uint32_t* code, int M, int K, int IC, int OC,
                   int use_lut, float* mid, void* stream);
 
+/* Dense GEMM for a few rows, tolerance contract: y f16 [M][OC] =
+ * f16((H128(xh @ decode(code)) * rs) * rout), R rows (2, 4 or 8) per
+ * workgroup share every decoded weight; split-K partials in ws
+ * (esc_gemm_rows_fast_workspace bytes), summed in fixed order.  Deterministic;
+ * reassociated float32 sum.  The decode-once-per-R-rows policy of
+ * msl.dense_gemm_rows_direct_out (escha_mlx/msl.py:1844-1870, used by
+ * EschaLinear at 1 < M, R <= 8: escha_mlx/dense.py:346-355), split along K. */
+size_t esc_gemm_rows_fast_workspace(int M, int R, int K, int IC, int OC);
+int esc_gemm_rows_fast_out(const uint16_t* xh, const uint32_t* code, const float* rout, int M,
+                           int R, int K, int IC, int OC, int use_lut, float rs, uint16_t* out,
+                           void* ws, size_t ws_bytes, void* stream);
+
 /* Sort rows by expert into R-row groups (integer only, on device).
  * rows_idx [n_groups*R], group_expert [n_groups].
  * Mirrors moe.build_groups (escha_mlx/moe.py:30-78). */

@@ -256,6 +256,44 @@ def test_fast_gemv_deterministic():
         assert np.array_equal(bits16(ops().gemv_fast_out(*args)), first)
 
 
+@pytest.mark.parametrize("lut", [False, True], ids=["hash", "lut"])
+@pytest.mark.parametrize("K,IC,OC,m,R_", [(2, 2048, 1024, 5, 4), (3, 512, 2048, 8, 8),
+                                          (2, 1024, 384, 3, 2), (3, 1024, 640, 13, 8)])
+def test_fast_rows_one_hot_bit_exact(K, IC, OC, m, R_, lut):
+    """R rows per decode: one non-zero input per row keeps every sum exact."""
+    rng = np.random.default_rng(7 * K + m + R_)
+    code = _expert_stack(rng, K, IC, OC, 1)[0]
+    rout = (rng.choice([-1.0, 1.0], OC) * rng.uniform(0.5, 1.5, OC) * 1e-2).astype(np.float32)
+    xh = np.zeros((m, IC), np.float16)
+    hot = rng.integers(0, IC, size=m)
+    for r in range(m):
+        xh[r, hot[r]] = np.float16(rng.choice([1.0, -2.0, 0.5]))
+    out = ops().dense_gemm_rows_fast_out(torch.from_numpy(xh).to(DEV), dcode(code),
+                                         torch.from_numpy(rout).to(DEV), K, IC, OC, R_, lut=lut)
+    w = R.reconstruct(code, IC, OC, K)
+    for r in range(m):
+        mid = xh[r, hot[r]].astype(np.float32) * w[hot[r]].astype(np.float32)
+        want = R.output_transform(mid[None], rout)[0]
+        assert np.array_equal(bits16(out)[r], want.view(np.uint16)), r
+
+
+@pytest.mark.parametrize("K,IC,OC,m,R_", [(2, 5120, 1024, 4, 4), (3, 1024, 2048, 7, 8),
+                                          (3, 2048, 512, 2, 2)])
+def test_fast_rows_tolerance_vs_f64_and_deterministic(K, IC, OC, m, R_):
+    rng = np.random.default_rng(K * 17 + m)
+    code = _expert_stack(rng, K, IC, OC, 1)[0]
+    rout = (rng.choice([-1.0, 1.0], OC) * rng.uniform(0.5, 1.5, OC) * 1e-2).astype(np.float32)
+    xh = rng.standard_normal((m, IC)).astype(np.float16)
+    args = (torch.from_numpy(xh).to(DEV), dcode(code), torch.from_numpy(rout).to(DEV), K, IC, OC, R_)
+    out = ops().dense_gemm_rows_fast_out(*args)
+    w = R.reconstruct(code, IC, OC, K)
+    exact = R.h128(R.gemv_f64(xh, w).astype(np.float32)) * R.RS * rout
+    got = out.cpu().numpy().astype(np.float32)
+    err = (np.abs(got - exact).max(axis=1) / np.abs(exact).max(axis=1)).max()
+    assert err < 2e-3, err
+    assert np.array_equal(bits16(ops().dense_gemm_rows_fast_out(*args)), bits16(out))
+
+
 # ---------------------------------------------------------------- routing / MoE
 
 def test_route_topk_matches_oracle(ref_vectors):
@@ -460,10 +498,19 @@ def test_dense_linear_module_vs_deploy_and_oracle(dense_linear_golden, monkeypat
     g = dense_linear_golden
     lin = dense.build({"escha_code": g["code"], "escha_rin": g["rin"], "escha_rout": g["rout"],
                        "escha_s_in": g["s_in"], "escha_s_out": g["s_out"], "bias": g["bias"]}, device=DEV)
+    y_fast = lin(torch.from_numpy(g["x"]).to(DEV)).cpu().numpy()   # M=8 -> split-K rows (default)
+    monkeypatch.setenv("ESCHA_HIP_EXACT", "1")
+    lin = dense.build({"escha_code": g["code"], "escha_rin": g["rin"], "escha_rout": g["rout"],
+                       "escha_s_in": g["s_in"], "escha_s_out": g["s_out"], "bias": g["bias"]}, device=DEV)
     y = lin(torch.from_numpy(g["x"]).to(DEV)).cpu().numpy()   # M=8 -> fused rows-out, exact order
     rin, rout = R.fold_scales(g["rin"], g["rout"], g["s_in"], g["s_out"])
     want = R.dense_linear(g["x"], g["code"], rin, rout, g["K"], bias=g["bias"], ordered=True)
     assert np.array_equal(y.view(np.uint16), want.view(np.uint16))
+    wf = want.astype(np.float32)
+    assert np.abs(y_fast.astype(np.float32) - wf).max() <= 2e-3 * np.abs(wf).max()
+    monkeypatch.delenv("ESCHA_HIP_EXACT")
+    lin = dense.build({"escha_code": g["code"], "escha_rin": g["rin"], "escha_rout": g["rout"],
+                       "escha_s_in": g["s_in"], "escha_s_out": g["s_out"], "bias": g["bias"]}, device=DEV)
     dep = g["deploy"].astype(np.float32)
     rel = np.abs(y.astype(np.float32) - dep).mean() / np.abs(dep).mean()
     assert rel < 3e-3
