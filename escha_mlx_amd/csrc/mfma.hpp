@@ -9,16 +9,15 @@
 // Block = 256 threads (4 waves), tile 256 rows x 128 columns (8 code tiles),
 // K walked in stages of 2 kt (32 inputs), double-buffered through LDS:
 //   * decode: per kt each thread decodes 8 weights, rows 8h..8h+7 of one
-//     column, straight into the f16 B operand layout in LDS (wave w decodes
-//     half h = w & 1 of the columns with jhi = w >> 1).
+//     column, straight into the f16 B operand layout in LDS.
 //   * X: the block's 256 rows x 32 inputs are staged to LDS once per stage.
 //   * MFMA: wave (wm, wn) owns rows 128wm.. and columns 64wn..; per kt it runs
 //     4 x 2 v_mfma_f32_32x32x16_f16 (A: lane l holds row l%32, inputs
 //     8(l/32)..+7; B: inputs 8(l/32)..+7 of column l%32; D register r of lane
 //     l is row 8(r/4) + 4(l/32) + r%4, column l%32).
 // The decode of stage s+1 is issued between the MFMAs of stage s, so the
-// VALU (decode) and the matrix pipe overlap.  LDS rows are padded to 80 B so
-// the 16-byte fragment reads of 16 consecutive rows hit distinct banks.
+// VALU (decode) and the matrix pipe overlap.  LDS chunks are XOR-swizzled so
+// the 16-byte fragment reads and writes hit distinct banks.
 #pragma once
 
 #include "fast.hpp"
@@ -30,8 +29,24 @@ typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kMmaRows = 256;           // rows per block
 constexpr int kMmaCols = 128;           // columns per block (8 tiles)
-constexpr int kMmaPitch = 40;           // halves per LDS row: 2 kt x 16 + 8 pad
+constexpr int kMmaPitch = 32;           // halves per LDS row: 2 kt x 16 inputs
+
+// LDS row r holds one stage (2 kt) of one input row (s_x) or one column
+// (s_b) as four 16-byte chunks c = 2*kt + half; chunk c is stored at
+// position c ^ swz(r).  Every access pattern of the kernel (16 consecutive
+// rows at one chunk; 4 rows x 4 chunks) then touches distinct bank groups,
+// for 8- and 16-lane phases alike.
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+__device__ __forceinline__ int lds_off(int r, int c) { return r * kMmaPitch + 8 * (c ^ swz(r)); }
 constexpr int kMmaThreads = 256;
+
+// Raw buffer resource over [p, p + bytes) (gfx9 descriptor word 3); loads
+// through it take a scalar base and a 32-bit lane offset, and read zero past
+// the end instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, size_t bytes) {
+  const int n = bytes > 0xFFFFFFF0u ? (int)0xFFFFFFF0u : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, n, 0x00020000);
+}
 
 // Code words one decode lane reads per kt: K=2 -> 3 (a 66-bit span),
 // K=3 -> 4 (a 91-bit span).
@@ -125,27 +140,32 @@ __global__ __launch_bounds__(kMmaThreads, 2) void k_gemm_mfma(const uint16_t* __
   }
   const int row0 = rb * kMmaRows;
 
-  // ---- decode role: (column n, half h) of each kt
-  const int jhi = wave >> 1, h = wave & 1;
-  const int ti = lane >> 3, a3 = (lane >> 1) & 3, bq = lane & 1;
-  const int n = 16 * ti + 2 * (a3 + 4 * jhi) + bq;
+  // ---- decode role: (column n, half h) of each kt; wave w decodes half
+  // h = w & 1 of tiles 4(w >> 1)..+3, 16 consecutive columns per 16 lanes
+  const int h = wave & 1;
+  const int ti = 4 * (wave >> 1) + (lane >> 4), c16 = lane & 15;
+  const int n = 16 * ti + c16;
+  const int jhi = c16 >> 3, a3 = (c16 >> 1) & 3, bq = c16 & 1;  // c16 = 2(a3 + 4jhi) + bq
   int st0 = K * (64 * a3 + 32 * bq + 4 * jhi + 2 * h) - (16 - K);
   if (st0 < 0) st0 += 256 * K;
   const uint32_t o = (uint32_t)(st0 & 31);  // 1..31: never 0 (K=2: 18..30, K=3: 5..31)
-  int woff[NW];
+  // loads go through buffer resources: a scalar base, a scalar per-stage
+  // offset and a constant 32-bit lane offset, so the loop spends no VALU on
+  // addresses
+  uint32_t loff[NW];  // byte offsets of the lane's words within a kt row of the block
 #pragma unroll
-  for (int k = 0; k < NW; ++k) woff[k] = ((st0 >> 5) + k) % WPT;
-  const uint32_t* ctile = code + (size_t)(8 * cb + ti) * WPT;  // kt = 0
-  const size_t kstride = (size_t)TN * WPT;
+  for (int k = 0; k < NW; ++k) loff[k] = 4u * (ti * WPT + ((st0 >> 5) + k) % WPT);
+  const uint32_t kstride = 4u * TN * WPT;  // bytes per kt row
+  const __amdgpu_buffer_rsrc_t crs =
+      buf_rsrc(code + (size_t)(8 * cb) * WPT, (size_t)TK * kstride - (size_t)(8 * cb) * WPT * 4);
 
   // ---- X role: rows 64i + tid/4, 16-byte chunk tid%4 of the stage's 64 bytes
   const int xchunk = tid & 3;
-  const uint16_t* xrow[4];
+  uint32_t xoff[4];  // byte offsets (M * IC * 2 < 2^32)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = min(row0 + 64 * i + (tid >> 2), M - 1);
-    xrow[i] = xh + (size_t)r * IC + 8 * xchunk;
-  }
+  for (int i = 0; i < 4; ++i)
+    xoff[i] = 2u * ((uint32_t)min(row0 + 64 * i + (tid >> 2), M - 1) * IC + 8 * xchunk);
+  const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(xh, (size_t)M * IC * 2);
 
   // global -> register staging of one stage, two sets in flight: the loads
   // of stage s+2 are issued two MFMA phases before their data is needed
@@ -156,22 +176,26 @@ __global__ __launch_bounds__(kMmaThreads, 2) void k_gemm_mfma(const uint16_t* __
   auto load_stage = [&](Regs& r, int s) {
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
-      const uint32_t* tp = ctile + (size_t)(2 * s + k2) * kstride;
+      const uint32_t so = (uint32_t)(2 * s + k2) * kstride;
 #pragma unroll
-      for (int k = 0; k < NW; ++k) r.cw[k2][k] = tp[woff[k]];
+      for (int k = 0; k < NW; ++k)
+        r.cw[k2][k] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(crs, loff[k], so, 0);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.xv[i] = *reinterpret_cast<const uint4*>(xrow[i] + 32 * s);
+    for (int i = 0; i < 4; ++i) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[i], 64u * s, 0);
+      r.xv[i] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
   };
   auto store_stage = [&](const Regs& r, int buf) {
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
       const uint4 v = mma_decode8<K>(r.cw[k2], o);
-      *reinterpret_cast<uint4*>(&s_b[buf][n * kMmaPitch + 16 * k2 + 8 * h]) = v;
+      *reinterpret_cast<uint4*>(&s_b[buf][lds_off(n, 2 * k2 + h)]) = v;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<uint4*>(&s_x[buf][(64 * i + (tid >> 2)) * kMmaPitch + 8 * xchunk]) =
+      *reinterpret_cast<uint4*>(&s_x[buf][lds_off(64 * i + (tid >> 2), xchunk)]) =
           r.xv[i];
   };
 
@@ -191,11 +215,11 @@ __global__ __launch_bounds__(kMmaThreads, 2) void k_gemm_mfma(const uint16_t* __
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         a[i] = *reinterpret_cast<const half8_t*>(
-            &s_x[buf][(128 * wm + 32 * i + (lane & 31)) * kMmaPitch + 16 * k2 + 8 * (lane >> 5)]);
+            &s_x[buf][lds_off(128 * wm + 32 * i + (lane & 31), 2 * k2 + (lane >> 5))]);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         b[j] = *reinterpret_cast<const half8_t*>(
-            &s_b[buf][(64 * wn + 32 * j + (lane & 31)) * kMmaPitch + 16 * k2 + 8 * (lane >> 5)]);
+            &s_b[buf][lds_off(64 * wn + 32 * j + (lane & 31), 2 * k2 + (lane >> 5))]);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
