@@ -12,6 +12,7 @@
 #include "../../include/escha_hip.h"
 #include "fused.hpp"
 #include "mfma.hpp"
+#include "linear.hpp"
 
 namespace {
 
@@ -181,6 +182,70 @@ struct FastRowsF {
   }
 };
 
+// ---- one-launch linear for M < 16 (linear.hpp)
+constexpr int kLinearSmallRows = 16;
+
+struct LinearPlan {
+  int R, S, KS, groups, row_groups;
+  size_t off_part, off_cnt, off_xh, off_mid, total;
+};
+
+// Fewest splits that reach the workgroup target: more splits mean more
+// float32 partials through the device-coherent path and a longer last-arriver
+// sum; the table path also stages 128 KiB of LDS per workgroup.
+LinearPlan linear_plan(int M, int K, int IC, int OC, bool lut) {
+  LinearPlan p{};
+  const int TK = IC / 16, TN = OC / 16, tpw = K == 2 ? 16 : 8;
+  auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
+  if (M < kLinearSmallRows) {
+    p.R = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    p.groups = (TN + tpw - 1) / tpw;
+    p.row_groups = (M + p.R - 1) / p.R;
+    const int nb = TK / 8;  // 128-input blocks
+    // fewest splits (largest KS <= 64) that still fill the GPU
+    const int target = lut ? 128 : 256;  // measured best on MI355X for 2048..17408 shapes
+    p.S = nb;
+    for (int S = 1; S <= std::min(nb, 64); ++S) {
+      if (nb % S || 8 * (nb / S) > 64) continue;
+      p.S = S;
+      if (p.groups * p.row_groups * S >= target) break;
+    }
+    p.KS = 8 * (nb / p.S);
+    // counters first, at an offset that does not depend on the split count:
+    // one zero-filled workspace serves the table and the hash plan alike
+    p.off_cnt = 0;
+    p.off_part = al((size_t)p.groups * p.row_groups * 4);
+    p.total = p.off_part + al((size_t)p.S * M * OC * 4);
+  } else {
+    p.off_xh = 0;
+    p.off_mid = al((size_t)M * IC * 2);
+    p.total = p.off_mid + al((size_t)M * OC * 4);
+  }
+  return p;
+}
+
+template <int K, bool LUT>
+struct LinearSmallF {
+  template <int R>
+  static int go(const uint16_t* x, const float* rin, const uint32_t* code, const float* rout,
+                const uint16_t* bias, int M, int TK, int TN, const LinearPlan& lp, float rs,
+                float* part, int* cnt, uint16_t* y, hipStream_t s) {
+    hipLaunchKernelGGL((esc::k_linear_small<K, LUT, R>), dim3(lp.groups, lp.row_groups, lp.S),
+                       dim3(256), 0, s, x, rin, code, rout, bias, M, TK, TN, lp.KS, rs, part, cnt, y);
+    return launched("k_linear_small");
+  }
+  static int run(const uint16_t* x, const float* rin, const uint32_t* code, const float* rout,
+                 const uint16_t* bias, int M, int TK, int TN, const LinearPlan& lp, float rs,
+                 float* part, int* cnt, uint16_t* y, hipStream_t s) {
+    switch (lp.R) {
+      case 1: return go<1>(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
+      case 2: return go<2>(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
+      case 4: return go<4>(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
+      default: return go<8>(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
+    }
+  }
+};
+
 }  // namespace
 
 extern "C" {
@@ -260,6 +325,43 @@ int esc_gemv_fast_out(const uint16_t* xh, const uint32_t* code, const int32_t* r
   hipLaunchKernelGGL(esc::k_splitk_out, dim3(OC / 128, M), dim3(64), 0, S(stream), part, Sp, M,
                      OC, rout, row_expert, rs, out);
   return launched("k_splitk_out");
+}
+
+size_t esc_linear_workspace(int M, int K, int IC, int OC) {
+  if (check_proj(K, IC, OC) || M <= 0) return 0;
+  return std::max(linear_plan(M, K, IC, OC, false).total, linear_plan(M, K, IC, OC, true).total);
+}
+
+int esc_linear(const uint16_t* x, const float* rin, const uint32_t* code, const float* rout,
+               const uint16_t* bias, int M, int K, int IC, int OC, int use_lut, float rs,
+               uint16_t* y, void* ws, size_t ws_bytes, void* stream) {
+  if (int rc = check_proj(K, IC, OC)) return rc;
+  ESC_REQUIRE(x && rin && code && rout && y, "null pointer");
+  ESC_REQUIRE(M >= 0, "negative row count");
+  if (M == 0) return ESC_OK;
+  const LinearPlan lp = linear_plan(M, K, IC, OC, use_lut != 0);
+  if (!ws || ws_bytes < lp.total)
+    return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, lp.total);
+  const int TK = IC / 16, TN = OC / 16;
+  hipStream_t s = S(stream);
+  char* w = static_cast<char*>(ws);
+  if (M < kLinearSmallRows) {
+    if (use_lut)
+      if (int rc = ensure_lut()) return rc;
+    float* part = reinterpret_cast<float*>(w + lp.off_part);
+    int* cnt = reinterpret_cast<int*>(w + lp.off_cnt);
+    if (K == 2)
+      return use_lut ? LinearSmallF<2, true>::run(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s)
+                     : LinearSmallF<2, false>::run(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
+    return use_lut ? LinearSmallF<3, true>::run(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s)
+                   : LinearSmallF<3, false>::run(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
+  }
+  // many rows: input transform, matrix-core GEMM, output transform
+  uint16_t* xh = reinterpret_cast<uint16_t*>(w + lp.off_xh);
+  float* mid = reinterpret_cast<float*>(w + lp.off_mid);
+  if (int rc = esc_input_transform(x, rin, nullptr, M, IC, rs, xh, stream)) return rc;
+  if (int rc = esc_gemm_mfma(xh, code, M, K, IC, OC, use_lut, mid, stream)) return rc;
+  return esc_output_transform(mid, rout, nullptr, bias, M, OC, rs, y, stream);
 }
 
 size_t esc_gemm_rows_fast_workspace(int M, int R, int K, int IC, int OC) {

@@ -136,16 +136,32 @@ class EschaLinear(torch.nn.Module):
         self._exact = envs.use_exact()
         self._block_r_pin = envs.dense_block_r_pin()
         self._mat = envs.dense_mat()
+        self._ws = {}  # zero-filled one-launch workspaces per (rows, device)
 
     @property
     def K(self) -> int:
         return self._w.K
+
+    def _linear_ws(self, m: int, device) -> torch.Tensor | None:
+        if m >= ops.LINEAR_SMALL_ROWS:
+            return None  # no counters: a fresh workspace per call
+        key = (m, device)
+        if key not in self._ws:
+            need = ops.linear_workspace(m, self._w.K, self._w.IC, self._w.OC)
+            self._ws[key] = torch.zeros(max(need, 4), dtype=torch.uint8, device=device)
+        return self._ws[key]
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         w = self._w
         shape = x.shape
         rows = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
         m = rows.shape[0]
+        if (not self._exact and self._block_r_pin is None
+                and (m < ops.LINEAR_SMALL_ROWS or self._mat)):
+            # the whole linear in esc_linear (one launch below 16 rows)
+            y = ops.linear(rows, w.code, w.rin, w.rout, w.K, w.IC, w.OC, bias=self.bias,
+                           lut=self._lut, ws=self._linear_ws(m, rows.device))
+            return y.reshape(*shape[:-1], w.OC).to(x.dtype)
         xh = ops.scaled_had(rows, w.rin, None)
         r = dense_block_r(m, self._block_r_pin)
         if self._mat and r == DENSE_MAT_R:

@@ -201,6 +201,36 @@ def dense_gemm_rows_direct_out(xh: torch.Tensor, code_u32: torch.Tensor, rout: t
     return out
 
 
+LINEAR_SMALL_ROWS = 16
+
+
+def linear_workspace(m: int, K: int, IC: int, OC: int) -> int:
+    return int(_lib.load().esc_linear_workspace(m, K, IC, OC))
+
+
+def linear(x: torch.Tensor, code_u32: torch.Tensor, rin: torch.Tensor, rout: torch.Tensor, K: int,
+           IC: int, OC: int, bias: torch.Tensor | None = None, lut: bool | None = None,
+           rs: float = RS, ws: torch.Tensor | None = None) -> torch.Tensor:
+    """The whole coded linear (input transform, GEMV/GEMM, output transform,
+    optional f16 bias) -> y f16 [m, OC]; one launch below 16 rows
+    (dense.py:337-362).  ws must be zero-filled before its first use (the
+    one-launch path keeps self-resetting counters there)."""
+    _dev(x, code_u32, rin, rout, bias)
+    m = x.shape[0]
+    if x.dtype != torch.float16 or tuple(x.shape) != (m, IC):
+        raise ValueError(f"x must be f16 [m, {IC}]")
+    y = torch.empty((m, OC), dtype=torch.float16, device=x.device)
+    if m == 0:
+        return y
+    need = linear_workspace(m, K, IC, OC)
+    if ws is None:  # counters (one-launch path) must start at zero; the rest is scratch
+        alloc = torch.zeros if m < LINEAR_SMALL_ROWS else torch.empty
+        ws = alloc(max(need, 4), dtype=torch.uint8, device=x.device)
+    _lib.call("esc_linear", _ptr(x), _ptr(rin), _ptr(_as_u32(code_u32)), _ptr(rout), _ptr(bias), m,
+              K, IC, OC, _lut_flag(lut), rs, _ptr(y), _ptr(ws), ws.numel(), _stream())
+    return y
+
+
 def dense_gemm_rows_fast_out(xh: torch.Tensor, code_u32: torch.Tensor, rout: torch.Tensor,
                              K: int, IC: int, OC: int, R: int, rs: float = RS,
                              lut: bool | None = None) -> torch.Tensor:

@@ -106,6 +106,22 @@ int esc_dense_gemm_rows_out(const uint16_t* xh, const uint32_t* code, const floa
 int esc_gemm_mfma(const uint16_t* xh, const uint32_t* code, int M, int K, int IC, int OC,
                   int use_lut, float* mid, void* stream);
 
+/* The whole coded linear, y f16 [M][OC] = (bias +) f16((H128(xh @ W) * rs) *
+ * rout) with xh = f16(H128(f32(x) * rin) * rs), x f16 [M][IC], rin f32 [IC],
+ * rout f32 [OC], bias f16 [OC] or NULL (added in f32 after the f16 round).
+ * M < 16: one launch (in-block input transform, split-K GEMV with R rows per
+ * decode, the last split of each column group sums the partials in fixed
+ * order and output-transforms); M >= 16: input transform, matrix-core GEMM,
+ * output transform.  ws: esc_linear_workspace bytes, zero-filled before its
+ * first use (its counters are left zero after every call); calls sharing one
+ * ws must not overlap.  Tolerance contract (reassociated float32 sum);
+ * decoded weights bit-exact.
+ * Replaces EschaLinear.__call__ (escha_mlx/dense.py:337-362). */
+size_t esc_linear_workspace(int M, int K, int IC, int OC);
+int esc_linear(const uint16_t* x, const float* rin, const uint32_t* code, const float* rout,
+               const uint16_t* bias, int M, int K, int IC, int OC, int use_lut, float rs,
+               uint16_t* y, void* ws, size_t ws_bytes, void* stream);
+
 /* Dense GEMM for a few rows, tolerance contract: y f16 [M][OC] =
  * f16((H128(xh @ decode(code)) * rs) * rout), R rows (2, 4 or 8) per
  * workgroup share every decoded weight; split-K partials in ws
