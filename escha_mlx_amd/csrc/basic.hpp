@@ -163,8 +163,9 @@ __global__ __launch_bounds__(1024) void k_build_groups(const int* __restrict__ r
                                                        int E, int R, int n_groups,
                                                        int* __restrict__ rows_idx,
                                                        int* __restrict__ group_expert) {
-  __shared__ int s_cnt[4096];
-  __shared__ int s_start[4096];
+  __shared__ int s_cnt[4096];    // rows per expert, then rows placed so far
+  __shared__ int s_start[4096];  // first padded slot of each expert
+  __shared__ int s_e[1024];      // one chunk of row_expert
   const int tid = threadIdx.x, nt = blockDim.x;
   for (int e = tid; e < E; e += nt) s_cnt[e] = 0;
   for (int i = tid; i < n_groups * R; i += nt) rows_idx[i] = m;
@@ -172,24 +173,55 @@ __global__ __launch_bounds__(1024) void k_build_groups(const int* __restrict__ r
   __syncthreads();
   for (int r = tid; r < m; r += nt) atomicAdd(&s_cnt[row_expert[r]], 1);
   __syncthreads();
-  if (tid == 0) {
-    int acc = 0;
-    for (int e = 0; e < E; ++e) {
-      s_start[e] = acc;
-      acc += (s_cnt[e] + R - 1) / R * R;
+  // exclusive prefix of the padded counts: each thread sums 4 experts, then a
+  // block-wide scan of the 1024 partial sums (Hillis-Steele in LDS)
+  {
+    int loc[4], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * tid + j;
+      loc[j] = e < E ? (s_cnt[e] + R - 1) / R * R : 0;
+      sum += loc[j];
+    }
+    s_e[tid] = sum;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int v = tid >= off ? s_e[tid - off] : 0;
+      __syncthreads();
+      s_e[tid] += v;
+      __syncthreads();
+    }
+    int acc = s_e[tid] - sum;  // exclusive
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * tid + j;
+      if (e < E) s_start[e] = acc;
+      acc += loc[j];
     }
   }
   __syncthreads();
   // group_expert: every padded group of expert e
   for (int e = tid; e < E; e += nt) {
-    int ng = (s_cnt[e] + R - 1) / R;
+    const int ng = (s_cnt[e] + R - 1) / R;
     for (int g = 0; g < ng; ++g) group_expert[s_start[e] / R + g] = e;
+    s_cnt[e] = 0;
   }
-  // stable placement: rank of row r among earlier rows with the same expert
-  for (int r = tid; r < m; r += nt) {
-    int e = row_expert[r], rank = 0;
-    for (int q = 0; q < r; ++q) rank += (row_expert[q] == e);
-    rows_idx[s_start[e] + rank] = r;
+  __syncthreads();
+  // stable placement, one chunk of nt rows at a time: a row's rank is the
+  // number of earlier rows of its expert (earlier chunks counted in s_cnt)
+  for (int c0 = 0; c0 < m; c0 += nt) {
+    const int r = c0 + tid;
+    const int e = r < m ? row_expert[r] : -1;
+    s_e[tid] = e;
+    __syncthreads();
+    if (r < m) {
+      int rank = s_cnt[e];
+      for (int q = 0; q < tid; ++q) rank += (s_e[q] == e);
+      rows_idx[s_start[e] + rank] = r;
+    }
+    __syncthreads();
+    if (r < m) atomicAdd(&s_cnt[e], 1);
+    __syncthreads();
   }
 }
 

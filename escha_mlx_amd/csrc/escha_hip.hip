@@ -168,7 +168,7 @@ struct FastRowsF {
                 float* part, hipStream_t s) {
     const int tpw = K == 2 ? 16 : 8;
     hipLaunchKernelGGL((esc::k_gemv_fast_rows<K, LUT, R>), dim3((TN + tpw - 1) / tpw, (M + R - 1) / R, S),
-                       dim3(256), 0, s, xh, code, M, TK, TN, TK / S, part);
+                       dim3(256), 0, s, xh, code, nullptr, nullptr, M, TK, TN, TK / S, part);
     return launched("k_gemv_fast_rows");
   }
   static int run(int R, const uint16_t* xh, const uint32_t* code, int M, int TK, int TN, int S,
@@ -508,22 +508,59 @@ int esc_moe_combine(const uint16_t* d16, const float* scores, int T, int top_k, 
 
 // ---- routed experts: input transform -> gate_up -> swiglu/transform -> down -> combine
 namespace {
+// Rows per expert group of the split-K chain: once there are as many routed
+// rows as experts, rows of one expert share each decoded weight (groups laid
+// out by moe.build_groups); below that almost every expert has one row.
+int moe_group_rows(int M, int E) { return M >= 4 * E ? 4 : M >= E ? 2 : 0; }
+
 struct MoePlan {
-  int M, S1, S2;
-  size_t off_xh, off_p1, off_xh2, off_p2, total;
+  int M, S1, S2, R, n_groups;
+  size_t off_xh, off_p1, off_xh2, off_p2, off_rows, off_gexp, total;
 };
-MoePlan moe_plan(int T, int top_k, int H, int I, int K_gu, int K_dn) {
+MoePlan moe_plan(int T, int top_k, int E, int H, int I, int K_gu, int K_dn) {
   MoePlan p;
   p.M = T * top_k;
-  p.S1 = fast_splits(K_gu, p.M, H / 16, 2 * I / 16);
-  p.S2 = fast_splits(K_dn, p.M, I / 16, H / 16);
+  p.R = E <= 4096 ? moe_group_rows(p.M, E) : 0;
+  p.n_groups = p.R ? (p.M + E * (p.R - 1) + p.R - 1) / p.R : 0;
+  const int eff = p.R ? (p.M + p.R - 1) / p.R : p.M;  // non-empty groups, about
+  p.S1 = fast_splits(K_gu, eff, H / 16, 2 * I / 16);
+  p.S2 = fast_splits(K_dn, eff, I / 16, H / 16);
   auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
   p.off_xh = 0;
   p.off_p1 = al(p.off_xh + (size_t)p.M * H * 2);
   p.off_xh2 = al(p.off_p1 + (size_t)p.S1 * p.M * 2 * I * 4);
   p.off_p2 = al(p.off_xh2 + (size_t)p.M * I * 2);
-  p.total = al(p.off_p2 + (size_t)p.S2 * p.M * H * 4);
+  p.off_rows = al(p.off_p2 + (size_t)p.S2 * p.M * H * 4);
+  p.off_gexp = al(p.off_rows + (size_t)p.n_groups * p.R * 4);
+  p.total = al(p.off_gexp + (size_t)p.n_groups * 4);
   return p;
+}
+
+template <int K, bool LUT>
+struct GroupRowsF {
+  template <int R>
+  static int go(const uint16_t* xh, const uint32_t* code, const int* rows, const int* gexp,
+                int n_groups, int M, int TK, int TN, int S, float* part, hipStream_t s) {
+    const int tpw = K == 2 ? 16 : 8;
+    hipLaunchKernelGGL((esc::k_gemv_fast_rows<K, LUT, R>), dim3((TN + tpw - 1) / tpw, n_groups, S),
+                       dim3(256), 0, s, xh, code, rows, gexp, M, TK, TN, TK / S, part);
+    return launched("k_gemv_fast_rows");
+  }
+  static int run(int R, const uint16_t* xh, const uint32_t* code, const int* rows, const int* gexp,
+                 int n_groups, int M, int TK, int TN, int S, float* part, hipStream_t s) {
+    return R == 4 ? go<4>(xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s)
+                  : go<2>(xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s);
+  }
+};
+
+int group_rows(int K, int lut, int R, const uint16_t* xh, const uint32_t* code, const int* rows,
+               const int* gexp, int n_groups, int M, int TK, int TN, int S, float* part,
+               hipStream_t s) {
+  if (K == 2)
+    return lut ? GroupRowsF<2, true>::run(R, xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s)
+               : GroupRowsF<2, false>::run(R, xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s);
+  return lut ? GroupRowsF<3, true>::run(R, xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s)
+             : GroupRowsF<3, false>::run(R, xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s);
 }
 
 // One-launch path (fused.hpp).  Latency mode: small items over the whole GPU
@@ -641,11 +678,10 @@ int launch_fused(const esc::FusedMoe& p, int K_gu, int K_dn, int grid, hipStream
 
 extern "C" {
 size_t esc_moe_expert_path_workspace(int T, int top_k, int E, int H, int I) {
-  (void)E;
   if (T <= 0 || top_k <= 0 || H <= 0 || I <= 0) return 0;
   // the plan's sizes depend on K only through the split counts; take the max
-  size_t a = moe_plan(T, top_k, H, I, 2, 2).total, b = moe_plan(T, top_k, H, I, 3, 3).total;
-  size_t c = moe_plan(T, top_k, H, I, 2, 3).total, d = moe_plan(T, top_k, H, I, 3, 2).total;
+  size_t a = moe_plan(T, top_k, E, H, I, 2, 2).total, b = moe_plan(T, top_k, E, H, I, 3, 3).total;
+  size_t c = moe_plan(T, top_k, E, H, I, 2, 3).total, d = moe_plan(T, top_k, E, H, I, 3, 2).total;
   size_t m = std::max(std::max(a, b), std::max(c, d));
   if (fused_eligible(T, top_k, H, I)) {
     m = std::max(m, fused_plan(1, T, top_k, H, I, false).total);
@@ -704,7 +740,7 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
     p.layers = nullptr;
     return launch_fused<false>(p, K_gu, K_dn, f.grid, S(stream));
   }
-  const MoePlan p = moe_plan(T, top_k, H, I, K_gu, K_dn);
+  const MoePlan p = moe_plan(T, top_k, E, H, I, K_gu, K_dn);
   if (!ws || ws_bytes < p.total)
     return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, p.total);
   if (use_lut)
@@ -719,15 +755,30 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
   hipLaunchKernelGGL(esc::k_moe_input, dim3(H / 128, p.M), dim3(64), 0, s, x, ids, top_k, gu_rin,
                      H, rs, xh);
   if (int rc = launched("k_moe_input")) return rc;
-  if (int rc = by_k_lut<FastF>(K_gu, use_lut, xh, gu_code, ids, p.M, H / 16, 2 * I / 16, p.S1,
-                               p1, s))
+  int* rows = reinterpret_cast<int*>(w + p.off_rows);
+  int* gexp = reinterpret_cast<int*>(w + p.off_gexp);
+  if (p.R) {
+    hipLaunchKernelGGL(esc::k_build_groups, dim3(1), dim3(1024), 0, s, ids, p.M, E, p.R,
+                       p.n_groups, rows, gexp);
+    if (int rc = launched("k_build_groups")) return rc;
+    if (int rc = group_rows(K_gu, use_lut, p.R, xh, gu_code, rows, gexp, p.n_groups, p.M, H / 16,
+                            2 * I / 16, p.S1, p1, s))
+      return rc;
+  } else if (int rc = by_k_lut<FastF>(K_gu, use_lut, xh, gu_code, ids, p.M, H / 16, 2 * I / 16,
+                                      p.S1, p1, s)) {
     return rc;
+  }
   hipLaunchKernelGGL(esc::k_moe_mid, dim3(I / 128, p.M), dim3(64), 0, s, p1, p.S1, p.M, I, ids,
                      gu_rout, dn_rin, rs, xh2);
   if (int rc = launched("k_moe_mid")) return rc;
-  if (int rc = by_k_lut<FastF>(K_dn, use_lut, xh2, dn_code, ids, p.M, I / 16, H / 16, p.S2, p2,
-                               s))
+  if (p.R) {
+    if (int rc = group_rows(K_dn, use_lut, p.R, xh2, dn_code, rows, gexp, p.n_groups, p.M, I / 16,
+                            H / 16, p.S2, p2, s))
+      return rc;
+  } else if (int rc = by_k_lut<FastF>(K_dn, use_lut, xh2, dn_code, ids, p.M, I / 16, H / 16, p.S2,
+                                      p2, s)) {
     return rc;
+  }
   hipLaunchKernelGGL(esc::k_moe_combine, dim3(H / 128, T), dim3(64), 0, s, p2, p.S2, p.M, H, ids,
                      scores, top_k, dn_rout, rs, y);
   return launched("k_moe_combine");

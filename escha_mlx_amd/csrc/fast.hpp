@@ -244,21 +244,35 @@ __device__ __forceinline__ void fast_tile_rows(const LaneWords<K>& lw, uint32_t 
   }
 }
 
-// Dense split-K GEMM for a few rows (2..8): part[z][row][OC] as k_gemv_fast,
-// with R rows per block sharing every decoded weight.  grid (ceil(TN/TPW),
-// ceil(M/R), S), block 256; rows past M read row M-1 and are not stored.
+// Split-K GEMM for a few rows (2..8) sharing every decoded weight:
+// part[z][row][OC] as k_gemv_fast.  grid (ceil(TN/TPW), n_groups, S), block
+// 256.  Dense (rows_idx null): group g is rows gR..gR+R-1 of one stream,
+// rows past M read row M-1 and are not stored.  Grouped (moe.build_groups
+// layout, escha_mlx/moe.py:30-78): group g holds rows rows_idx[gR..gR+R) of
+// expert group_expert[g] (code stacked [E][TK][TN][8K]); padding rows (== M)
+// compute on row 0 and are not stored, groups of expert -1 do nothing.
 template <int K, bool LUT, int R>
 __global__ __launch_bounds__(256) void k_gemv_fast_rows(const uint16_t* __restrict__ xh,
-                                                        const uint32_t* __restrict__ code, int M,
-                                                        int TK, int TN, int KS,
+                                                        const uint32_t* __restrict__ code,
+                                                        const int* __restrict__ rows_idx,
+                                                        const int* __restrict__ group_expert,
+                                                        int M, int TK, int TN, int KS,
                                                         float* __restrict__ part) {
   using G = Geo<K>;
+  const int grp = blockIdx.y;
+  const int e = group_expert ? group_expert[grp] : 0;
+  if (e < 0) return;  // whole block: no barrier reached
   __shared__ uint16_t s_lut[LUT ? 65536 : 1];
   __shared__ float s_red[4][64][G::NCOL];
   stage_lut<LUT>(s_lut);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int ntg = blockIdx.x, row0 = blockIdx.y * R, z = blockIdx.z;
+  const int ntg = blockIdx.x, z = blockIdx.z;
   const int IC = TK * 16, OC = TN * 16;
+  const uint32_t* base = code + (size_t)e * TK * TN * (8 * K);
+  int rows[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    rows[r] = rows_idx ? rows_idx[grp * R + r] : (grp * R + r < M ? grp * R + r : M);
   const int q = lane % G::LPT, tile = lane / G::LPT;
   const int src = tile * G::LPT + (q + G::LPT - 1) % G::LPT;
   const bool valid = ntg * G::TPW + tile < TN;
@@ -267,7 +281,8 @@ __global__ __launch_bounds__(256) void k_gemv_fast_rows(const uint16_t* __restri
   const uint32_t* xrow[R];
 #pragma unroll
   for (int r = 0; r < R; ++r)
-    xrow[r] = reinterpret_cast<const uint32_t*>(xh + (size_t)min(row0 + r, M - 1) * IC);
+    xrow[r] = reinterpret_cast<const uint32_t*>(
+        xh + (size_t)(rows[r] < M ? rows[r] : (rows_idx ? 0 : M - 1)) * IC);
   float acc[R][G::NCOL];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -275,12 +290,12 @@ __global__ __launch_bounds__(256) void k_gemv_fast_rows(const uint16_t* __restri
     for (int i = 0; i < G::NCOL; ++i) acc[r][i] = 0.f;
   const size_t lane_off = (size_t)ntg * G::TPW * (8 * K) + (size_t)lane * G::WPL;
   LaneWords<K> zero{};
-  LaneWords<K> cur = valid ? load_lane_words<K>(code + (size_t)kt0 * TN * (8 * K) + lane_off) : zero;
+  LaneWords<K> cur = valid ? load_lane_words<K>(base + (size_t)kt0 * TN * (8 * K) + lane_off) : zero;
   for (int k = 0; k < KW; ++k) {
     const int kt = kt0 + k;
     LaneWords<K> nxt = cur;
     if (valid && k + 1 < KW)
-      nxt = load_lane_words<K>(code + (size_t)(kt + 1) * TN * (8 * K) + lane_off);
+      nxt = load_lane_words<K>(base + (size_t)(kt + 1) * TN * (8 * K) + lane_off);
     uint32_t xp[R][8];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -298,8 +313,8 @@ __global__ __launch_bounds__(256) void k_gemv_fast_rows(const uint16_t* __restri
 #pragma unroll
     for (int i = 0; i < G::NCOL; ++i) s_red[wave][lane][i] = acc[r][i];
     __syncthreads();
-    if (wave == 0 && valid && row0 + r < M) {
-      float* pr = part + ((size_t)z * M + row0 + r) * OC + (size_t)(ntg * G::TPW + tile) * 16;
+    if (wave == 0 && valid && rows[r] < M) {
+      float* pr = part + ((size_t)z * M + rows[r]) * OC + (size_t)(ntg * G::TPW + tile) * 16;
 #pragma unroll
       for (int i = 0; i < G::NCOL; ++i) {
         float v = s_red[0][lane][i];

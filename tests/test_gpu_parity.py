@@ -408,16 +408,23 @@ def test_moe_exact_chain_stagewise_bit_exact(K_gu, K_dn):
     assert np.array_equal(bits16(y), y_ref.astype(np.float16).view(np.uint16))
 
 
-def test_moe_multi_launch_path_vs_oracle(monkeypatch):
-    """More rows than the one-launch path takes (T*k > 64): split-K chain."""
-    E, H, I, K_gu, K_dn, T, k = 64, 256, 128, 2, 3, 9, 8
-    c = _moe_case(E, H, I, K_gu, K_dn, T, k, 5)
+@pytest.mark.parametrize("E,T,K_gu,K_dn", [(64, 9, 2, 3), (16, 12, 3, 2), (256, 9, 2, 2)],
+                         ids=["groups_of_2", "groups_of_4", "per_row"])
+def test_moe_multi_launch_path_vs_oracle(E, T, K_gu, K_dn, monkeypatch):
+    """More rows than the one-launch path takes (T*k > 64): split-K chain, with
+    rows of one expert sharing each decoded weight once rows >= experts
+    (groups in the moe.build_groups layout), per row otherwise; deterministic."""
+    H, I, k = 256, 128, 8
+    c = _moe_case(E, H, I, K_gu, K_dn, T, k, 5 + E)
     blk = _block(c, E, k, K_gu, K_dn, monkeypatch, exact=False)
     ids, sc = ops().route_topk(torch.from_numpy(c["logits"]).to(DEV), k)
-    y = blk(torch.from_numpy(c["x"]).to(DEV), ids, sc).cpu().numpy().astype(np.float32)
+    x = torch.from_numpy(c["x"]).to(DEV)
+    y = blk(x, ids, sc)
     ids_np, sc_np = ids.cpu().numpy(), sc.cpu().numpy()
     want = _oracle_moe(c, ids_np, sc_np, E, H, I, K_gu, K_dn, np.unique(ids_np)).astype(np.float32)
-    assert np.abs(y - want).max() / np.abs(want).max() < 5e-3
+    got = y.cpu().numpy().astype(np.float32)
+    assert np.abs(got - want).max() / np.abs(want).max() < 5e-3
+    assert torch.equal(blk(x, ids, sc), y)
 
 
 def test_moe_one_launch_status_and_reuse(monkeypatch):
