@@ -184,6 +184,7 @@ struct FastRowsF {
 
 // ---- one-launch linear for M < 16 (linear.hpp)
 constexpr int kLinearSmallRows = 16;
+constexpr int kLinearSmallRowsLut = 8;
 
 struct LinearPlan {
   int R, S, KS, groups, row_groups;
@@ -198,7 +199,9 @@ LinearPlan linear_plan(int M, int K, int IC, int OC, bool lut) {
   const int TK = IC / 16, TN = OC / 16, tpw = K == 2 ? 16 : 8;
   auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
   if (M < kLinearSmallRows) {
-    p.R = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    // every row of the group shares each decoded weight (one B column of
+    // the matrix-core multiply each); the table path's LDS holds 8 rows
+    p.R = std::min(M, lut ? kLinearSmallRowsLut : kLinearSmallRows - 1);
     p.groups = (TN + tpw - 1) / tpw;
     p.row_groups = (M + p.R - 1) / p.R;
     const int nb = TK / 8;  // 128-input blocks
@@ -226,23 +229,20 @@ LinearPlan linear_plan(int M, int K, int IC, int OC, bool lut) {
 
 template <int K, bool LUT>
 struct LinearSmallF {
-  template <int R>
-  static int go(const uint16_t* x, const float* rin, const uint32_t* code, const float* rout,
-                const uint16_t* bias, int M, int TK, int TN, const LinearPlan& lp, float rs,
-                float* part, int* cnt, uint16_t* y, hipStream_t s) {
-    hipLaunchKernelGGL((esc::k_linear_small<K, LUT, R>), dim3(lp.groups, lp.row_groups, lp.S),
-                       dim3(256), 0, s, x, rin, code, rout, bias, M, TK, TN, lp.KS, rs, part, cnt, y);
-    return launched("k_linear_small");
-  }
   static int run(const uint16_t* x, const float* rin, const uint32_t* code, const float* rout,
                  const uint16_t* bias, int M, int TK, int TN, const LinearPlan& lp, float rs,
                  float* part, int* cnt, uint16_t* y, hipStream_t s) {
-    switch (lp.R) {
-      case 1: return go<1>(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
-      case 2: return go<2>(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
-      case 4: return go<4>(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
-      default: return go<8>(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
-    }
+    // one row: VALU GEMV; several rows: matrix-core row-blocked GEMM
+    constexpr int RMAX = LUT ? kLinearSmallRowsLut : kLinearSmallRows;
+    if (lp.R < 1 || lp.R > RMAX) return fail(ESC_EINVAL, "rows per group %d > %d", lp.R, RMAX);
+    const dim3 grid(lp.groups, lp.row_groups, lp.S);
+    if (lp.R == 1)
+      hipLaunchKernelGGL((esc::k_linear_small<K, LUT, 1>), grid, dim3(256), 0, s, x, rin, code,
+                         rout, bias, M, TK, TN, lp.KS, 1, rs, part, cnt, y);
+    else
+      hipLaunchKernelGGL((esc::k_linear_small<K, LUT, RMAX>), grid, dim3(256), 0, s, x, rin, code,
+                         rout, bias, M, TK, TN, lp.KS, lp.R, rs, part, cnt, y);
+    return launched("k_linear_small");
   }
 };
 

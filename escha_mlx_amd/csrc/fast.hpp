@@ -244,13 +244,153 @@ __device__ __forceinline__ void fast_tile_rows(const LaneWords<K>& lw, uint32_t 
   }
 }
 
-// Split-K GEMM for a few rows (2..8) sharing every decoded weight:
-// part[z][row][OC] as k_gemv_fast.  grid (ceil(TN/TPW), n_groups, S), block
-// 256.  Dense (rows_idx null): group g is rows gR..gR+R-1 of one stream,
-// rows past M read row M-1 and are not stored.  Grouped (moe.build_groups
-// layout, escha_mlx/moe.py:30-78): group g holds rows rows_idx[gR..gR+R) of
-// expert group_expert[g] (code stacked [E][TK][TN][8K]); padding rows (== M)
-// compute on row 0 and are not stored, groups of expert -1 do nothing.
+// ---------------------------------------------------------------- MFMA accumulate
+// The multiply-add of a decoded tile moved off the VALU onto the matrix core:
+// v_mfma_f32_16x16x32_f16 with the decoded weights as the A operand and the
+// inputs as B, one token per B column.
+//
+// Wave-step geometry: lane l works on kt offset g = l / 16 and on tile-lane
+// i = l % 16 = LPT * tc + q (tile tc of the step's 16 / LPT tiles, lane q of
+// the tile), so a wave-step covers 16 / LPT tiles x 4 kt.  A row i is then one
+// output column (tile tc, column Geo::col(q, ci)) for every k of the operand,
+// and k = 8g + j runs over 8 inputs of kt g: the MFMA sums the four kt of the
+// step.  The lane's pair leaders u (steps u, u+8 sharing a column, rows
+// fast_row(u) and +2) with column slot ci and m = (u >> 3) & 3 in {0, 2} fill
+// A operand (ci, m / 2) in register v = u & 3.  Those rows do not depend on ci,
+// so one kt needs two B operands, 8 words of input pairs in "B order".
+//
+// D (16x16 f32, 4 registers): lane l holds rows 4(l / 16) + r, i.e. the
+// output columns of tile-lanes i = 4(l / 16) + r, for token l % 16.
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// B order of one kt's 16 inputs (f16 slots of its 8 words): input row r sits
+// in word 4((r>>2)&1) + 2((r>>3)&1) + (r&1), low half for rows with bit 1 set
+// (the "+2" row of a pair), high half otherwise.  Words 0..3 are the B operand
+// of pair group m = 0, words 4..7 that of m = 2.
+__device__ constexpr int xb_slot(int r) {
+  return 2 * (4 * ((r >> 2) & 1) + 2 * ((r >> 3) & 1) + (r & 1)) + 1 - ((r >> 1) & 1);
+}
+// store inputs c, c+1 (c even, counted from the first input of s) in B order
+__device__ __forceinline__ void put_xb(uint16_t* s, int c, uint32_t pair) {
+  const int kt = c >> 4, r = c & 15;
+  s[16 * kt + xb_slot(r)] = (uint16_t)pair;
+  s[16 * kt + xb_slot(r + 1)] = (uint16_t)(pair >> 16);
+}
+
+// The packed weight pair [w(u+8) | w(u) << 16] of pair leader u: hash decode,
+// or two reads of the 65,536-entry table (LUT) into the two halves.
+template <int K, bool LUT = false>
+__device__ __forceinline__ uint32_t decode_pair(const LaneWords<K>& lw, uint32_t wprev, int u,
+                                                const uint16_t* lut = nullptr) {
+  const uint32_t clo = kClo, chi = kChi;
+  if constexpr (K == 2) {
+    const int rel = 2 * (u + 1) - 16;
+    const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
+    const uint32_t hi = a < 0 ? wprev : lw.w[a];
+    const uint32_t p = off == 0 ? hi : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 32 - off);
+    if constexpr (LUT) return (uint32_t)lut[p & 0xFFFFu] | ((uint32_t)lut[p >> 16] << 16);
+    return halves_sum2(mask_xor(hash_x<false>(p, clo, chi)), mask_xor(hash_x<true>(p, clo, chi)));
+  } else {
+    uint32_t s2[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int uu = u + 8 * (1 - h);
+      const int rel = 3 * (uu + 1) - 16;
+      const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
+      const uint32_t hi = a < 0 ? wprev : lw.w[a];
+      s2[h] = off <= 16 ? hi >> (16 - off) : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 48 - off);
+    }
+    if constexpr (LUT)
+      return (uint32_t)lut[s2[0] & 0xFFFFu] | ((uint32_t)lut[s2[1] & 0xFFFFu] << 16);
+    return halves_sum2(mask_xor(hash_x<false>(s2[0], clo, chi)),
+                       mask_xor(hash_x<false>(s2[1], clo, chi)));
+  }
+}
+
+// Decode the lane's tile of one wave-step and accumulate it into acc[ci]
+// (NCOL accumulators) with 2 * NCOL MFMAs; b0 / b2: the lane's B operands
+// (pair groups m = 0 and m = 2 of its kt).
+template <int K, bool LUT = false>
+__device__ __forceinline__ void mma_tile(const LaneWords<K>& lw, uint32_t wprev, u32x4_t b0,
+                                         u32x4_t b2, f32x4_t* acc, const uint16_t* lut = nullptr) {
+  using G = Geo<K>;
+  u32x4_t a[G::NCOL][2];
+#pragma unroll
+  for (int u = 0; u < G::SPL; ++u) {
+    if ((u >> 3) & 1) continue;
+    const int ci = G::col_slot(u), P = (u >> 4) & 1, v = u & 3;
+    a[ci][P][v] = decode_pair<K, LUT>(lw, wprev, u, lut);
+    if (v == 3)
+      acc[ci] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a[ci][P]),
+                                                      __builtin_bit_cast(half8_t, P ? b2 : b0),
+                                                      acc[ci], 0, 0, 0);
+  }
+}
+
+// The two B operands of one kt from its 8 input words in row order
+// (word k = inputs 2k, 2k+1).
+__device__ __forceinline__ void b_operands(uint4 lo, uint4 hi, u32x4_t& b0, u32x4_t& b2) {
+  const uint32_t xw[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  uint32_t xp[8];
+  x_pairs(xw, xp);
+  b0 = u32x4_t{xp[0], xp[1], xp[4], xp[5]};
+  b2 = u32x4_t{xp[2], xp[3], xp[6], xp[7]};
+}
+
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent2(float* p, float a, float b) {
+  const uint64_t v = (uint64_t)__builtin_bit_cast(uint32_t, a) |
+                     ((uint64_t)__builtin_bit_cast(uint32_t, b) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// two consecutive floats; COH: device-coherent (for a consumer in the same launch)
+template <bool COH>
+__device__ __forceinline__ void st_pair(float* p, float a, float b) {
+  if constexpr (COH)
+    st_coherent2(p, a, b);
+  else
+    *reinterpret_cast<float2*>(p) = make_float2(a, b);
+}
+
+// Store one token's D values of a wave-step's tile-lane group: lane 16g + c
+// holds tile-lanes i = 4g + r (r = 0..3).  dst: column 0 of the step's first
+// tile in the token's output row.
+template <int K, bool COH = false>
+__device__ __forceinline__ void mma_store(const f32x4_t* acc, int g, float* dst) {
+  if constexpr (K == 2) {
+    // tile g, lane q = r: columns 2r + {0,1} (slots 0,1), 8 + 2r + {0,1} (slots 2,3)
+    float* d = dst + 16 * g;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      st_pair<COH>(d + 2 * r, acc[0][r], acc[1][r]);
+      st_pair<COH>(d + 8 + 2 * r, acc[2][r], acc[3][r]);
+    }
+  } else {
+    // tile g/2, lanes q = 4(g&1) + r: columns q (slot 0) and q + 8 (slot 1)
+    float* d = dst + 16 * (g >> 1) + 4 * (g & 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      st_pair<COH>(d + 8 * h, acc[h][0], acc[h][1]);
+      st_pair<COH>(d + 8 * h + 2, acc[h][2], acc[h][3]);
+    }
+  }
+}
+
+// Split-K GEMM for up to 16 rows sharing every decoded weight, on the matrix
+// core (mma_tile; B column c = row c of the group): part[z][row][OC] as
+// k_gemv_fast.  grid (ceil(TN/TPW), n_groups, S), block 256; wave w owns tiles
+// [TPW*x + (16/LPT)*w, +16/LPT) over the block's KS kt (KS % 4 == 0), so no
+// cross-wave reduction.  Dense (rows_idx null): group g is rows gR..gR+R-1 of
+// one stream; rows past M read row M-1 and are not stored.  Grouped
+// (moe.build_groups layout, escha_mlx/moe.py:30-78): group g holds rows
+// rows_idx[gR..gR+R) of expert group_expert[g] (code stacked [E][TK][TN][8K]);
+// padding rows (== M) compute on row 0 and are not stored, groups of expert -1
+// do nothing.
 template <int K, bool LUT, int R>
 __global__ __launch_bounds__(256) void k_gemv_fast_rows(const uint16_t* __restrict__ xh,
                                                         const uint32_t* __restrict__ code,
@@ -258,74 +398,53 @@ __global__ __launch_bounds__(256) void k_gemv_fast_rows(const uint16_t* __restri
                                                         const int* __restrict__ group_expert,
                                                         int M, int TK, int TN, int KS,
                                                         float* __restrict__ part) {
+  static_assert(R >= 1 && R <= 16, "");
   using G = Geo<K>;
+  constexpr int TPS = 16 / G::LPT;
   const int grp = blockIdx.y;
   const int e = group_expert ? group_expert[grp] : 0;
   if (e < 0) return;  // whole block: no barrier reached
   __shared__ uint16_t s_lut[LUT ? 65536 : 1];
-  __shared__ float s_red[4][64][G::NCOL];
   stage_lut<LUT>(s_lut);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int ntg = blockIdx.x, z = blockIdx.z;
+  const int z = blockIdx.z;
   const int IC = TK * 16, OC = TN * 16;
-  const uint32_t* base = code + (size_t)e * TK * TN * (8 * K);
-  int rows[R];
+  const int tile0 = blockIdx.x * G::TPW + TPS * wave;
+  if (tile0 >= TN) return;  // whole wave (TN is a multiple of TPS)
+  const int gk = lane >> 4, c = lane & 15, tc = c / G::LPT, q = lane % G::LPT;
+  const int src = (lane & ~(G::LPT - 1)) | ((lane + G::LPT - 1) & (G::LPT - 1));
+  // the lane's B column: row min(c, R-1) of the group
+  const int rc = c < R ? c : R - 1;
+  const int row = rows_idx ? rows_idx[grp * R + rc] : min(grp * R + rc, M);
+  const int xr = row < M ? row : (rows_idx ? 0 : M - 1);
+  const uint4* xq = reinterpret_cast<const uint4*>(xh + (size_t)xr * IC);
+  const size_t kstride = (size_t)TN * (8 * K);
+  const uint32_t* lp = code + (size_t)e * TK * kstride + (size_t)(tile0 + tc) * (8 * K) +
+                       q * G::WPL;
+  const int kt0 = z * KS + gk, nsteps = KS / 4;
+  f32x4_t acc[G::NCOL];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-    rows[r] = rows_idx ? rows_idx[grp * R + r] : (grp * R + r < M ? grp * R + r : M);
-  const int q = lane % G::LPT, tile = lane / G::LPT;
-  const int src = tile * G::LPT + (q + G::LPT - 1) % G::LPT;
-  const bool valid = ntg * G::TPW + tile < TN;
-  const int KW = KS / 4;
-  const int kt0 = z * KS + wave * KW;
-  const uint32_t* xrow[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-    xrow[r] = reinterpret_cast<const uint32_t*>(
-        xh + (size_t)(rows[r] < M ? rows[r] : (rows_idx ? 0 : M - 1)) * IC);
-  float acc[R][G::NCOL];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int i = 0; i < G::NCOL; ++i) acc[r][i] = 0.f;
-  const size_t lane_off = (size_t)ntg * G::TPW * (8 * K) + (size_t)lane * G::WPL;
-  LaneWords<K> zero{};
-  LaneWords<K> cur = valid ? load_lane_words<K>(base + (size_t)kt0 * TN * (8 * K) + lane_off) : zero;
-  for (int k = 0; k < KW; ++k) {
-    const int kt = kt0 + k;
+  for (int i = 0; i < G::NCOL; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  LaneWords<K> cur = load_lane_words<K>(lp + (size_t)kt0 * kstride);
+  uint4 xa = xq[2 * kt0], xb = xq[2 * kt0 + 1];
+  for (int k = 0; k < nsteps; ++k) {
     LaneWords<K> nxt = cur;
-    if (valid && k + 1 < KW)
-      nxt = load_lane_words<K>(base + (size_t)(kt + 1) * TN * (8 * K) + lane_off);
-    uint32_t xp[R][8];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      uint32_t xw[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xw[i] = xrow[r][8 * kt + i];
-      x_pairs(xw, xp[r]);
+    uint4 na = xa, nb = xb;
+    if (k + 1 < nsteps) {
+      const int kt = kt0 + 4 * (k + 1);
+      nxt = load_lane_words<K>(lp + (size_t)kt * kstride);
+      na = xq[2 * kt];
+      nb = xq[2 * kt + 1];
     }
+    u32x4_t b0, b2;
+    b_operands(xa, xb, b0, b2);
     const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
-    fast_tile_rows<K, LUT, R>(cur, wprev, xp, s_lut, acc);
+    mma_tile<K, LUT>(cur, wprev, b0, b2, acc, s_lut);
     cur = nxt;
+    xa = na;
+    xb = nb;
   }
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-#pragma unroll
-    for (int i = 0; i < G::NCOL; ++i) s_red[wave][lane][i] = acc[r][i];
-    __syncthreads();
-    if (wave == 0 && valid && rows[r] < M) {
-      float* pr = part + ((size_t)z * M + rows[r]) * OC + (size_t)(ntg * G::TPW + tile) * 16;
-#pragma unroll
-      for (int i = 0; i < G::NCOL; ++i) {
-        float v = s_red[0][lane][i];
-        v = v + s_red[1][lane][i];
-        v = v + s_red[2][lane][i];
-        v = v + s_red[3][lane][i];
-        pr[G::col(q, i)] = v;
-      }
-    }
-    __syncthreads();
-  }
+  if (c < R && row < M) mma_store<K>(acc, gk, part + ((size_t)z * M + row) * OC + 16 * tile0);
 }
 
 // Partial GEMV: part[z][row][OC] = sum over the block's kt range.

@@ -55,10 +55,6 @@ __device__ __forceinline__ bool claim(int* p) {
   return __hip_atomic_compare_exchange_strong(p, &expected, 1, __ATOMIC_RELAXED,
                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_coherent(float* p, float v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ float2 ld_coherent2(const float* p) {
   const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
@@ -263,10 +259,10 @@ __device__ uint32_t h_pair(const FusedMoe& p, int l, int r, int kb) {
   const float* base =
       p.partA + ((size_t)l * p.nA + (size_t)(r * p.NB + kb) * p.NKC) * 256 + 2 * lane;
   float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
-  for (int kc0 = 0; kc0 < p.NKC; kc0 += 16) {
-    float2 gv[16], uv[16];
+  for (int kc0 = 0; kc0 < p.NKC; kc0 += 8) {
+    float2 gv[8], uv[8];
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
+    for (int j = 0; j < 8; ++j)
       if (kc0 + j < p.NKC) {
         if constexpr (COH) {
           gv[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256);
@@ -277,7 +273,7 @@ __device__ uint32_t h_pair(const FusedMoe& p, int l, int r, int kb) {
         }
       }
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
+    for (int j = 0; j < 8; ++j)
       if (kc0 + j < p.NKC) {
         g0 = g0 + gv[j].x;
         g1 = g1 + gv[j].y;
@@ -313,8 +309,8 @@ __device__ void combine_tile(const FusedMoe& p, int l, int t, int cp, uint16_t (
   const MoeLayer& L = p.layer(l);
   for (int s0 = wave; s0 < p.top_k; s0 += 8) {
     float v[2][2][2] = {};
-    for (int kb0 = 0; kb0 < p.NKB; kb0 += 8) {
-      float2 pv[2][2][8];
+    for (int kb0 = 0; kb0 < p.NKB; kb0 += 4) {
+      float2 pv[2][2][4];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int s = s0 + 4 * u;
@@ -323,7 +319,7 @@ __device__ void combine_tile(const FusedMoe& p, int l, int t, int cp, uint16_t (
                           ((size_t)l * p.nB + (size_t)((t * p.top_k + s) * p.NCP + cp) * p.NKB) * 256 +
                           2 * lane;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 4; ++j)
           if (kb0 + j < p.NKB) {
             pv[u][0][j] = ld_coherent2(pb + (size_t)(kb0 + j) * 256);
             pv[u][1][j] = ld_coherent2(pb + (size_t)(kb0 + j) * 256 + 128);
@@ -332,7 +328,7 @@ __device__ void combine_tile(const FusedMoe& p, int l, int t, int cp, uint16_t (
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 4; ++j)
           if (s0 + 4 * u < p.top_k && kb0 + j < p.NKB) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {

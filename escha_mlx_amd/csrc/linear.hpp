@@ -6,9 +6,13 @@
 // [z*KS, (z+1)*KS) with KS a multiple of 8, i.e. whole 128-input blocks:
 //   1. the block input-transforms its own KS/8 blocks of x for its R rows
 //      (one wave per (row, block)) into LDS, so no xh tensor is written;
-//   2. decode + multiply as k_gemv_fast_rows (R rows share each decoded
-//      weight), reduce the 4 waves in LDS, publish float32 partials
-//      [S][M][OC] with device-coherent stores;
+//   2. one row (RMAX == 1, the GEMV): the 4 waves split the kt range, decode
+//      TPW tiles per kt step and multiply-add with packed dot2 on the VALU,
+//      then reduce in LDS.  Several rows (RMAX > 1, the row-blocked GEMM):
+//      wave w decodes its 16/LPT tiles over the block's kt and multiplies them
+//      on the matrix core (mma_tile, inputs staged in B order), B column c =
+//      row c of the group, so R <= RMAX rows share every decoded weight.  The
+//      block publishes float32 partials [S][M][OC] with device-coherent stores;
 //   3. the last of the S blocks of a (row group, column group) -- found with
 //      a device-scope counter that it resets to zero -- sums the S partials
 //      in z order (one thread per column, 32 loads in flight at a time),
@@ -21,73 +25,98 @@
 
 namespace esc {
 
-template <int K, bool LUT, int R>
+template <int K, bool LUT, int RMAX>
 __global__ __launch_bounds__(256) void k_linear_small(
     const uint16_t* __restrict__ x, const float* __restrict__ rin,
     const uint32_t* __restrict__ code, const float* __restrict__ rout,
-    const uint16_t* __restrict__ bias, int M, int TK, int TN, int KS, float rs,
+    const uint16_t* __restrict__ bias, int M, int TK, int TN, int KS, int R, float rs,
     float* __restrict__ part, int* __restrict__ cnt, uint16_t* __restrict__ y) {
   using G = Geo<K>;
+  constexpr int TPS = 16 / G::LPT;
+  constexpr int kCols = G::TPW * 16;  // columns per column group
+  constexpr int kBlocks = kCols / 128;  // 128-column blocks per group
+  constexpr bool kMma = RMAX > 1;
   __shared__ uint16_t s_lut[LUT ? 65536 : 1];
-  __shared__ float s_red[4][64][G::NCOL];
-  __shared__ uint32_t s_x[R][8 * 64];  // up to 64 kt of inputs per row
+  __shared__ __attribute__((aligned(16))) uint32_t s_x[RMAX][8 * 64];  // up to 64 kt per row
+  __shared__ float s_red[kMma ? 1 : 4][64][G::NCOL];
+  __shared__ float s_sum[2][kCols];
   __shared__ int s_last;
   stage_lut<LUT>(s_lut);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int ntg = blockIdx.x, row0 = blockIdx.y * R, z = blockIdx.z, S = gridDim.z;
   const int IC = TK * 16, OC = TN * 16;
   const int nb = KS / 8;  // 128-input blocks of the block's kt range
-  // the first kt step's code is requested before anything else, so its
-  // latency overlaps the input transform
-  const int q = lane % G::LPT, tile = lane / G::LPT;
-  const int src = tile * G::LPT + (q + G::LPT - 1) % G::LPT;
-  const bool valid = ntg * G::TPW + tile < TN;
-  const int KW = KS / 4;
-  const int kl0 = wave * KW, kt0 = z * KS + kl0;
-  const size_t lane_off = (size_t)ntg * G::TPW * (8 * K) + (size_t)lane * G::WPL;
-  LaneWords<K> zero{};
-  LaneWords<K> cur = valid ? load_lane_words<K>(code + (size_t)kt0 * TN * (8 * K) + lane_off) : zero;
+  const size_t kstride = (size_t)TN * (8 * K);
+  const int src = (lane & ~(G::LPT - 1)) | ((lane + G::LPT - 1) & (G::LPT - 1));
+  // matrix-core geometry: wave w owns tiles [tile0, tile0 + 16/LPT), lane
+  // kt offset gk, tile-lane c = LPT*tc + q, B column c
+  const int tile0 = ntg * G::TPW + TPS * wave;
+  const int gk = lane >> 4, c = lane & 15, tc = c / G::LPT, q = lane % G::LPT;
+  // VALU geometry: all waves on the group's TPW tiles, kt split 4 ways
+  const int vtile = lane / G::LPT, kl0 = wave * (KS / 4);
+  const bool valid = kMma ? tile0 < TN : ntg * G::TPW + vtile < TN;  // kMma: wave-uniform
+  const uint32_t* lp = kMma ? code + (size_t)(tile0 + tc) * (8 * K) + q * G::WPL
+                            : code + (size_t)(ntg * G::TPW) * (8 * K) + lane * G::WPL;
+  const int kt0 = kMma ? z * KS + gk : z * KS + kl0;
+  const int nsteps = KS / 4, kstep = kMma ? 4 : 1;
+  // the first step's code is requested before anything else, so its latency
+  // overlaps the input transform
+  LaneWords<K> cur{};
+  if (valid) cur = load_lane_words<K>(lp + (size_t)kt0 * kstride);
   // 1. input transform: xh = f16(H128(f32(x) * rin) * RS) per (row, block)
   for (int it = wave; it < R * nb; it += 4) {
     const int r = it / nb, b = it % nb;
     const int row = min(row0 + r, M - 1);
-    const int c = 16 * KS * z + 128 * b + 2 * lane;
-    float v0 = (float)__builtin_bit_cast(half_t, x[(size_t)row * IC + c]) * rin[c];
-    float v1 = (float)__builtin_bit_cast(half_t, x[(size_t)row * IC + c + 1]) * rin[c + 1];
+    const int cc = 16 * KS * z + 128 * b + 2 * lane;
+    float v0 = (float)__builtin_bit_cast(half_t, x[(size_t)row * IC + cc]) * rin[cc];
+    float v1 = (float)__builtin_bit_cast(half_t, x[(size_t)row * IC + cc + 1]) * rin[cc + 1];
     h128_wave(v0, v1);
-    s_x[r][64 * b + lane] = pack2(to_f16(v0 * rs), to_f16(v1 * rs));
+    const uint32_t pr = pack2(to_f16(v0 * rs), to_f16(v1 * rs));
+    if constexpr (kMma)
+      put_xb(reinterpret_cast<uint16_t*>(s_x[r]), 128 * b + 2 * lane, pr);
+    else
+      s_x[r][64 * b + lane] = pr;
   }
   __syncthreads();
-  // 2. decode + multiply the block's tiles over its kt range
-  float acc[R][G::NCOL];
+  // 2. decode + multiply over the block's kt range
+  if constexpr (kMma) {
+    if (valid) {
+      f32x4_t acc[G::NCOL];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int i = 0; i < G::NCOL; ++i) acc[r][i] = 0.f;
-  for (int k = 0; k < KW; ++k) {
-    LaneWords<K> nxt = cur;
-    if (valid && k + 1 < KW)
-      nxt = load_lane_words<K>(code + (size_t)(kt0 + k + 1) * TN * (8 * K) + lane_off);
-    uint32_t xp[R][8];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      uint32_t xw[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xw[i] = s_x[r][8 * (kl0 + k) + i];
-      x_pairs(xw, xp[r]);
+      for (int i = 0; i < G::NCOL; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const uint32_t* xs = s_x[c < R ? c : R - 1];
+      for (int k = 0; k < nsteps; ++k) {
+        LaneWords<K> nxt = cur;
+        if (k + 1 < nsteps) nxt = load_lane_words<K>(lp + (size_t)(kt0 + kstep * (k + 1)) * kstride);
+        const u32x4_t* xb = reinterpret_cast<const u32x4_t*>(xs + 8 * (4 * k + gk));
+        const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
+        mma_tile<K, LUT>(cur, wprev, xb[0], xb[1], acc, s_lut);
+        cur = nxt;
+      }
+      if (c < R && row0 + c < M)
+        mma_store<K, true>(acc, gk, part + ((size_t)z * M + row0 + c) * OC + 16 * tile0);
     }
-    const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
-    fast_tile_rows<K, LUT, R>(cur, wprev, xp, s_lut, acc);
-    cur = nxt;
-  }
-  // reduce the 4 waves (fixed order) and publish the partials
+  } else {
+    float acc[1][G::NCOL];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
+    for (int i = 0; i < G::NCOL; ++i) acc[0][i] = 0.f;
+    for (int k = 0; k < nsteps; ++k) {
+      LaneWords<K> nxt = cur;
+      if (valid && k + 1 < nsteps) nxt = load_lane_words<K>(lp + (size_t)(kt0 + k + 1) * kstride);
+      uint32_t xw[8], xp[1][8];
 #pragma unroll
-    for (int i = 0; i < G::NCOL; ++i) s_red[wave][lane][i] = acc[r][i];
+      for (int i = 0; i < 8; ++i) xw[i] = s_x[0][8 * (kl0 + k) + i];
+      x_pairs(xw, xp[0]);
+      const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
+      fast_tile_rows<K, LUT, 1>(cur, wprev, xp, s_lut, acc);
+      cur = nxt;
+    }
+    // reduce the 4 waves (fixed order) and publish the partials
+#pragma unroll
+    for (int i = 0; i < G::NCOL; ++i) s_red[wave][lane][i] = acc[0][i];
     __syncthreads();
-    if (wave == 0 && valid && row0 + r < M) {
-      float* pr = part + ((size_t)z * M + row0 + r) * OC + (size_t)(ntg * G::TPW + tile) * 16;
+    if (wave == 0 && valid) {
+      float* pr = part + ((size_t)z * M + row0) * OC + (size_t)(ntg * G::TPW + vtile) * 16;
 #pragma unroll
       for (int i = 0; i < G::NCOL; ++i) {
         float v = s_red[0][lane][i];
@@ -97,27 +126,22 @@ __global__ __launch_bounds__(256) void k_linear_small(
         st_coherent(pr + G::col(q, i), v);
       }
     }
-    __syncthreads();
   }
   wait_vm();
   __syncthreads();
   // 3. the last split of (row group, column group) finishes the columns
   if (threadIdx.x == 0) {
-    int* c = &cnt[(size_t)blockIdx.y * gridDim.x + ntg];
-    const bool last = add_relaxed(c, 1) == S - 1;
-    if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int* cn = &cnt[(size_t)blockIdx.y * gridDim.x + ntg];
+    const bool last = add_relaxed(cn, 1) == S - 1;
+    if (last) __hip_atomic_store(cn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = last;
   }
   __syncthreads();
   if (!s_last) return;
   // one thread per column: the splits' partials are requested 32 at a time,
   // summed in z order, and staged in LDS for the output transform
-  constexpr int kCols = G::TPW * 16;          // columns per column group
-  constexpr int kBlocks = kCols / 128;        // 128-column blocks per group
-  float* s_sum = &s_red[0][0][0];             // [R][kCols] floats (<= 8 KiB needed)
-  static_assert(sizeof(s_red) >= 2 * kCols * sizeof(float), "");
   const int col0 = ntg * kCols;
-  for (int r0 = 0; r0 < R; r0 += 2) {         // two rows per pass fit s_red
+  for (int r0 = 0; r0 < R; r0 += 2) {  // two rows per pass
     for (int rr = 0; rr < 2 && r0 + rr < R; ++rr) {
       const int row = min(row0 + r0 + rr, M - 1);
       const int j = threadIdx.x;
@@ -137,7 +161,7 @@ __global__ __launch_bounds__(256) void k_linear_small(
           for (int zz = 0; zz < 32; ++zz)
             if (z0 + zz < S) v = v + pv[zz];
         }
-        s_sum[rr * kCols + j] = v;
+        s_sum[rr][j] = v;
       }
     }
     __syncthreads();
@@ -145,8 +169,8 @@ __global__ __launch_bounds__(256) void k_linear_small(
       const int rr = it / kBlocks, b = it % kBlocks, r = r0 + rr;
       const int col = col0 + 128 * b + 2 * lane;
       if (r >= R || row0 + r >= M || col >= OC) continue;
-      float v0 = s_sum[rr * kCols + 128 * b + 2 * lane];
-      float v1 = s_sum[rr * kCols + 128 * b + 2 * lane + 1];
+      float v0 = s_sum[rr][128 * b + 2 * lane];
+      float v1 = s_sum[rr][128 * b + 2 * lane + 1];
       h128_wave(v0, v1);
       half_t y0 = to_f16((v0 * rs) * rout[col]);
       half_t y1 = to_f16((v1 * rs) * rout[col + 1]);

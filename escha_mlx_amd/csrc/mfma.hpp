@@ -24,7 +24,6 @@
 
 namespace esc {
 
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kMmaRows = 256;           // rows per block
