@@ -3,8 +3,10 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -246,6 +248,40 @@ struct LinearSmallF {
   }
 };
 
+// Compute units of the current device (queried once per device).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Row blocks of 16 per k_gemm_mma2 workgroup (NRB in {2,4,6,8}).  The kernel
+// is decode-bound, so a tile's time grows slowly with its rows (measured on
+// MI355X: 0.76 + 0.03 NRB, relative to NRB = 8), and a launch takes as many
+// tile-times as the busiest CU holds tiles: pick the NRB that minimises
+// ceil(tiles / CUs) * tile time.
+int mma2_row_blocks(int M, int TN) {
+  const int cus = device_cus();
+  int best = 8;
+  double best_cost = 1e30;
+  for (int nrb = 8; nrb >= 2; nrb -= 2) {
+    const long tiles = (long)((M + 16 * nrb - 1) / (16 * nrb)) * (TN / 16);
+    const double cost = (double)((tiles + cus - 1) / cus) * (0.76 + 0.03 * nrb);
+    if (cost < best_cost * 0.999) {
+      best_cost = cost;
+      best = nrb;
+    }
+  }
+  return best;
+}
+
 }  // namespace
 
 extern "C" {
@@ -451,8 +487,27 @@ int esc_gemm_mfma(const uint16_t* xh, const uint32_t* code, int M, int K, int IC
   (void)use_lut;  // the table holds the hash's own values: both decodes give the same bits
   if (M == 0) return ESC_OK;
   const int TK = IC / 16, TN = OC / 16;
-  const int blocks = ((M + esc::kMmaRows - 1) / esc::kMmaRows) * (TN / 8);
   hipStream_t s = S(stream);
+  if (TN % 16 == 0) {
+    const int nrb = mma2_row_blocks(M, TN);
+    const int blocks = ((M + 16 * nrb - 1) / (16 * nrb)) * (TN / 16);
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, xh, code, M, TK, TN, mid);
+    };
+    if (K == 2) {
+      if (nrb == 2) go(esc::k_gemm_mma2<2, 2>);
+      else if (nrb == 4) go(esc::k_gemm_mma2<2, 4>);
+      else if (nrb == 6) go(esc::k_gemm_mma2<2, 6>);
+      else go(esc::k_gemm_mma2<2, 8>);
+    } else {
+      if (nrb == 2) go(esc::k_gemm_mma2<3, 2>);
+      else if (nrb == 4) go(esc::k_gemm_mma2<3, 4>);
+      else if (nrb == 6) go(esc::k_gemm_mma2<3, 6>);
+      else go(esc::k_gemm_mma2<3, 8>);
+    }
+    return launched("k_gemm_mma2");
+  }
+  const int blocks = ((M + esc::kMmaRows - 1) / esc::kMmaRows) * (TN / 8);
   if (K == 2)
     hipLaunchKernelGGL(esc::k_gemm_mfma<2>, dim3(blocks), dim3(esc::kMmaThreads), 0, s, xh, code,
                        M, TK, TN, mid);
@@ -510,8 +565,11 @@ int esc_moe_combine(const uint16_t* d16, const float* scores, int T, int top_k, 
 namespace {
 // Rows per expert group of the split-K chain: once there are as many routed
 // rows as experts, rows of one expert share each decoded weight (groups laid
-// out by moe.build_groups); below that almost every expert has one row.
-int moe_group_rows(int M, int E) { return M >= 4 * E ? 4 : M >= E ? 2 : 0; }
+// out by moe.build_groups, one row per B column of the matrix-core multiply,
+// so a group costs one decode whatever its row count); below that almost
+// every expert has one row.
+constexpr int kMoeGroupRows = 8;
+int moe_group_rows(int M, int E) { return M >= E ? kMoeGroupRows : 0; }
 
 struct MoePlan {
   int M, S1, S2, R, n_groups;
@@ -522,7 +580,10 @@ MoePlan moe_plan(int T, int top_k, int E, int H, int I, int K_gu, int K_dn) {
   p.M = T * top_k;
   p.R = E <= 4096 ? moe_group_rows(p.M, E) : 0;
   p.n_groups = p.R ? (p.M + E * (p.R - 1) + p.R - 1) / p.R : 0;
-  const int eff = p.R ? (p.M + p.R - 1) / p.R : p.M;  // non-empty groups, about
+  // non-empty groups, about: the experts a uniform routing touches, or M/R
+  const int eff = p.R ? std::max((p.M + p.R - 1) / p.R,
+                                 (int)(E * (1.0 - std::pow(1.0 - 1.0 / E, (double)p.M))))
+                      : p.M;
   p.S1 = fast_splits(K_gu, eff, H / 16, 2 * I / 16);
   p.S2 = fast_splits(K_dn, eff, I / 16, H / 16);
   auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
@@ -548,8 +609,8 @@ struct GroupRowsF {
   }
   static int run(int R, const uint16_t* xh, const uint32_t* code, const int* rows, const int* gexp,
                  int n_groups, int M, int TK, int TN, int S, float* part, hipStream_t s) {
-    return R == 4 ? go<4>(xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s)
-                  : go<2>(xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s);
+    if (R != kMoeGroupRows) return fail(ESC_EINVAL, "rows per expert group %d", R);
+    return go<kMoeGroupRows>(xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s);
   }
 };
 

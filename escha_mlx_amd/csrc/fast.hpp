@@ -245,19 +245,21 @@ __device__ __forceinline__ void fast_tile_rows(const LaneWords<K>& lw, uint32_t 
 }
 
 // ---------------------------------------------------------------- MFMA accumulate
-// The multiply-add of a decoded tile moved off the VALU onto the matrix core:
+// The multiply-add of decoded tiles on the matrix core:
 // v_mfma_f32_16x16x32_f16 with the decoded weights as the A operand and the
-// inputs as B, one token per B column.
+// inputs as B, one input row (token) per B column.
 //
 // Wave-step geometry: lane l works on kt offset g = l / 16 and on tile-lane
 // i = l % 16 = LPT * tc + q (tile tc of the step's 16 / LPT tiles, lane q of
-// the tile), so a wave-step covers 16 / LPT tiles x 4 kt.  A row i is then one
-// output column (tile tc, column Geo::col(q, ci)) for every k of the operand,
-// and k = 8g + j runs over 8 inputs of kt g: the MFMA sums the four kt of the
-// step.  The lane's pair leaders u (steps u, u+8 sharing a column, rows
-// fast_row(u) and +2) with column slot ci and m = (u >> 3) & 3 in {0, 2} fill
-// A operand (ci, m / 2) in register v = u & 3.  Those rows do not depend on ci,
-// so one kt needs two B operands, 8 words of input pairs in "B order".
+// the tile), so a wave-step covers 16 / LPT tiles x 4 kt.  A row i is one
+// output column (tile tc, column Geo::col(q, ci)) for every k of an operand,
+// and k = 8g + j runs over 8 inputs of kt g: one MFMA sums four kt.
+//
+// The lane's steps of column slot ci are u = (m, v): tile row 2m + (v & 1) +
+// 8(v >> 1), m, v = 0..3.  A operand (ci, P) holds the 8 steps v in
+// {2P, 2P+1}: register m = [w(m, 2P) | w(m, 2P+1) << 16], tile rows 8P + 2m
+// and +1.  So the matching B operand is input words 4P..4P+3 of the kt in
+// plain row order (word k = inputs 2k, 2k+1): one 16-byte piece.
 //
 // D (16x16 f32, 4 registers): lane l holds rows 4(l / 16) + r, i.e. the
 // output columns of tile-lanes i = 4(l / 16) + r, for token l % 16.
@@ -265,78 +267,83 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-// B order of one kt's 16 inputs (f16 slots of its 8 words): input row r sits
-// in word 4((r>>2)&1) + 2((r>>3)&1) + (r&1), low half for rows with bit 1 set
-// (the "+2" row of a pair), high half otherwise.  Words 0..3 are the B operand
-// of pair group m = 0, words 4..7 that of m = 2.
-__device__ constexpr int xb_slot(int r) {
-  return 2 * (4 * ((r >> 2) & 1) + 2 * ((r >> 3) & 1) + (r & 1)) + 1 - ((r >> 1) & 1);
-}
-// store inputs c, c+1 (c even, counted from the first input of s) in B order
-__device__ __forceinline__ void put_xb(uint16_t* s, int c, uint32_t pair) {
-  const int kt = c >> 4, r = c & 15;
-  s[16 * kt + xb_slot(r)] = (uint16_t)pair;
-  s[16 * kt + xb_slot(r + 1)] = (uint16_t)(pair >> 16);
+// the lane's step index of (m, v) in column slot ci
+template <int K>
+__device__ constexpr int mma_step(int m, int v, int ci) {
+  return K == 2 ? 32 * (ci & 1) + 8 * m + 4 * (ci >> 1) + v : 8 * m + 4 * ci + v;
 }
 
-// The packed weight pair [w(u+8) | w(u) << 16] of pair leader u: hash decode,
-// or two reads of the 65,536-entry table (LUT) into the two halves.
+// 16-bit state of step u in the low half (K = 3; bits above ignored by the
+// u16 ops and masked for the table)
+__device__ __forceinline__ uint32_t state3(const LaneWords<3>& lw, uint32_t wprev, int u) {
+  const int rel = 3 * (u + 1) - 16;
+  const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
+  const uint32_t hi = a < 0 ? wprev : lw.w[a];
+  return off <= 16 ? hi >> (16 - off) : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 48 - off);
+}
+// 32-bit window [s_u | s_{u+8}] (K = 2: the two states are 16 bits apart)
+__device__ __forceinline__ uint32_t window2(const LaneWords<2>& lw, uint32_t wprev, int u) {
+  const int rel = 2 * (u + 1) - 16;
+  const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
+  const uint32_t hi = a < 0 ? wprev : lw.w[a];
+  return off == 0 ? hi : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 32 - off);
+}
+
+// A operand (ci, P) of the lane's tile: hash decode, or reads of the
+// 65,536-entry table (LUT) into the two halves of each register.
 template <int K, bool LUT = false>
-__device__ __forceinline__ uint32_t decode_pair(const LaneWords<K>& lw, uint32_t wprev, int u,
-                                                const uint16_t* lut = nullptr) {
+__device__ __forceinline__ u32x4_t mma_a_operand(const LaneWords<K>& lw, uint32_t wprev, int ci,
+                                                 int P, const uint16_t* lut = nullptr) {
   const uint32_t clo = kClo, chi = kChi;
-  if constexpr (K == 2) {
-    const int rel = 2 * (u + 1) - 16;
-    const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
-    const uint32_t hi = a < 0 ? wprev : lw.w[a];
-    const uint32_t p = off == 0 ? hi : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 32 - off);
-    if constexpr (LUT) return (uint32_t)lut[p & 0xFFFFu] | ((uint32_t)lut[p >> 16] << 16);
-    return halves_sum2(mask_xor(hash_x<false>(p, clo, chi)), mask_xor(hash_x<true>(p, clo, chi)));
-  } else {
-    uint32_t s2[2];
+  u32x4_t a;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int uu = u + 8 * (1 - h);
-      const int rel = 3 * (uu + 1) - 16;
-      const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
-      const uint32_t hi = a < 0 ? wprev : lw.w[a];
-      s2[h] = off <= 16 ? hi >> (16 - off) : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 48 - off);
+  for (int m = 0; m < 4; m += 2) {
+    const int ua = mma_step<K>(m, 2 * P, ci), ub = mma_step<K>(m, 2 * P + 1, ci);
+    if constexpr (K == 2) {
+      // one window per v gives the steps of m (high half) and m + 1 (low half)
+      const uint32_t pa = window2(lw, wprev, ua), pb = window2(lw, wprev, ub);
+      if constexpr (LUT) {
+        a[m] = (uint32_t)lut[pa >> 16] | ((uint32_t)lut[pb >> 16] << 16);
+        a[m + 1] = (uint32_t)lut[pa & 0xFFFFu] | ((uint32_t)lut[pb & 0xFFFFu] << 16);
+      } else {
+        a[m] = halves_sum2(mask_xor(hash_x<true>(pa, clo, chi)), mask_xor(hash_x<true>(pb, clo, chi)));
+        a[m + 1] =
+            halves_sum2(mask_xor(hash_x<false>(pa, clo, chi)), mask_xor(hash_x<false>(pb, clo, chi)));
+      }
+    } else {
+      const uint32_t sa0 = state3(lw, wprev, ua), sb0 = state3(lw, wprev, ub);
+      const uint32_t sa1 = state3(lw, wprev, ua + 8), sb1 = state3(lw, wprev, ub + 8);
+      if constexpr (LUT) {
+        a[m] = (uint32_t)lut[sa0 & 0xFFFFu] | ((uint32_t)lut[sb0 & 0xFFFFu] << 16);
+        a[m + 1] = (uint32_t)lut[sa1 & 0xFFFFu] | ((uint32_t)lut[sb1 & 0xFFFFu] << 16);
+      } else {
+        a[m] = halves_sum2(mask_xor(hash_x<false>(sa0, clo, chi)),
+                           mask_xor(hash_x<false>(sb0, clo, chi)));
+        a[m + 1] = halves_sum2(mask_xor(hash_x<false>(sa1, clo, chi)),
+                               mask_xor(hash_x<false>(sb1, clo, chi)));
+      }
     }
-    if constexpr (LUT)
-      return (uint32_t)lut[s2[0] & 0xFFFFu] | ((uint32_t)lut[s2[1] & 0xFFFFu] << 16);
-    return halves_sum2(mask_xor(hash_x<false>(s2[0], clo, chi)),
-                       mask_xor(hash_x<false>(s2[1], clo, chi)));
   }
+  return a;
+}
+
+__device__ __forceinline__ f32x4_t mma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                                __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
 }
 
 // Decode the lane's tile of one wave-step and accumulate it into acc[ci]
-// (NCOL accumulators) with 2 * NCOL MFMAs; b0 / b2: the lane's B operands
-// (pair groups m = 0 and m = 2 of its kt).
+// (NCOL accumulators) with 2 * NCOL MFMAs; b0 / b1: the lane's B operands
+// (input words 0..3 and 4..7 of its kt).
 template <int K, bool LUT = false>
 __device__ __forceinline__ void mma_tile(const LaneWords<K>& lw, uint32_t wprev, u32x4_t b0,
-                                         u32x4_t b2, f32x4_t* acc, const uint16_t* lut = nullptr) {
+                                         u32x4_t b1, f32x4_t* acc, const uint16_t* lut = nullptr) {
   using G = Geo<K>;
-  u32x4_t a[G::NCOL][2];
 #pragma unroll
-  for (int u = 0; u < G::SPL; ++u) {
-    if ((u >> 3) & 1) continue;
-    const int ci = G::col_slot(u), P = (u >> 4) & 1, v = u & 3;
-    a[ci][P][v] = decode_pair<K, LUT>(lw, wprev, u, lut);
-    if (v == 3)
-      acc[ci] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a[ci][P]),
-                                                      __builtin_bit_cast(half8_t, P ? b2 : b0),
-                                                      acc[ci], 0, 0, 0);
+  for (int ci = 0; ci < G::NCOL; ++ci) {
+    acc[ci] = mma16(mma_a_operand<K, LUT>(lw, wprev, ci, 0, lut), b0, acc[ci]);
+    acc[ci] = mma16(mma_a_operand<K, LUT>(lw, wprev, ci, 1, lut), b1, acc[ci]);
   }
-}
-
-// The two B operands of one kt from its 8 input words in row order
-// (word k = inputs 2k, 2k+1).
-__device__ __forceinline__ void b_operands(uint4 lo, uint4 hi, u32x4_t& b0, u32x4_t& b2) {
-  const uint32_t xw[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-  uint32_t xp[8];
-  x_pairs(xw, xp);
-  b0 = u32x4_t{xp[0], xp[1], xp[4], xp[5]};
-  b2 = u32x4_t{xp[2], xp[3], xp[6], xp[7]};
 }
 
 __device__ __forceinline__ void st_coherent(float* p, float v) {
@@ -436,10 +443,9 @@ __global__ __launch_bounds__(256) void k_gemv_fast_rows(const uint16_t* __restri
       na = xq[2 * kt];
       nb = xq[2 * kt + 1];
     }
-    u32x4_t b0, b2;
-    b_operands(xa, xb, b0, b2);
     const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
-    mma_tile<K, LUT>(cur, wprev, b0, b2, acc, s_lut);
+    mma_tile<K, LUT>(cur, wprev, __builtin_bit_cast(u32x4_t, xa), __builtin_bit_cast(u32x4_t, xb),
+                     acc, s_lut);
     cur = nxt;
     xa = na;
     xb = nb;

@@ -10,7 +10,7 @@
 //      TPW tiles per kt step and multiply-add with packed dot2 on the VALU,
 //      then reduce in LDS.  Several rows (RMAX > 1, the row-blocked GEMM):
 //      wave w decodes its 16/LPT tiles over the block's kt and multiplies them
-//      on the matrix core (mma_tile, inputs staged in B order), B column c =
+//      on the matrix core (mma_tile), B column c =
 //      row c of the group, so R <= RMAX rows share every decoded weight.  The
 //      block publishes float32 partials [S][M][OC] with device-coherent stores;
 //   3. the last of the S blocks of a (row group, column group) -- found with
@@ -72,10 +72,7 @@ __global__ __launch_bounds__(256) void k_linear_small(
     float v1 = (float)__builtin_bit_cast(half_t, x[(size_t)row * IC + cc + 1]) * rin[cc + 1];
     h128_wave(v0, v1);
     const uint32_t pr = pack2(to_f16(v0 * rs), to_f16(v1 * rs));
-    if constexpr (kMma)
-      put_xb(reinterpret_cast<uint16_t*>(s_x[r]), 128 * b + 2 * lane, pr);
-    else
-      s_x[r][64 * b + lane] = pr;
+    s_x[r][64 * b + lane] = pr;
   }
   __syncthreads();
   // 2. decode + multiply over the block's kt range

@@ -283,4 +283,152 @@ __global__ __launch_bounds__(kMmaThreads, 2) void k_gemm_mfma(const uint16_t* __
     }
 }
 
+// Coded GEMM with the weights decoded straight into MFMA A operands (no LDS
+// for weights): mid[M][OC] f32 = xh[M][IC] f16 @ decode(code), for OC a
+// multiple of 256.  Same tolerance contract as k_gemm_mfma.
+//
+// Block = 4 waves, tile 16*NRB rows x 256 columns (16 code tiles); wave w owns
+// tiles 4w..4w+3 (64 columns).  K is walked in steps of 4 kt (64 inputs):
+//   * each lane decodes its tile-lane of the wave-step (mma_a_operand: 4
+//     column groups x 2 input halves = 8 A operands, v_mfma_f32_16x16x32_f16
+//     layout, one kt per 16 lanes), so each weight is decoded once per block;
+//   * X: the block's rows x 64 inputs are staged through LDS (double
+//     buffered, 16-byte chunks XOR-swizzled by row); a B operand is one
+//     16-byte read (16 rows x 8 inputs of one kt per 16 lanes) and feeds the
+//     4 A operands of its input half;
+//   * each A operand meets NRB row blocks: 8 * NRB MFMAs per wave-step, in
+//     one straight-line body with the decode of the next wave-step, so the
+//     matrix pipe and the VALU overlap (two workgroups per CU).
+// The kernel is decode-bound: the host picks NRB for the shape.
+// D register r of lane l: output column of tile-lane 4(l/16) + r, row l%16 of
+// the row block.
+template <int K, int NRB>
+__global__ __launch_bounds__(256, 2) void k_gemm_mma2(
+    const uint16_t* __restrict__ xh, const uint32_t* __restrict__ code, int M, int TK, int TN,
+    float* __restrict__ mid) {
+  using G = Geo<K>;
+  constexpr int TPS = 16 / G::LPT, GPW = 4 / TPS, NA = GPW * G::NCOL;
+  static_assert(NA == 4, "four 16-column groups per wave");
+  static_assert(NRB % 2 == 0 && NRB >= 2 && NRB <= 8, "whole x chunks per thread, 2 waves/SIMD");
+  constexpr int BR = 16 * NRB;            // rows per block
+  constexpr int XCH = BR * 8 / 256;       // 16-byte x chunks per thread per stage
+  __shared__ uint4 s_x[2][BR * 8];        // [stage][row][chunk ^ (row & 7)]
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int IC = TK * 16, OC = TN * 16;
+  const int ncb = TN / 16;
+  int rb, cb;
+  if (ncb % 8 == 0) {
+    const int per = ncb / 8, qq = blockIdx.x / 8, x = blockIdx.x % 8;
+    rb = qq / per;
+    cb = 8 * (qq % per) + x;
+  } else {
+    rb = blockIdx.x / ncb;
+    cb = blockIdx.x % ncb;
+  }
+  const int row0 = rb * BR;
+  const int tile0 = cb * 16 + 4 * wave;
+  const int gk = lane >> 4, c = lane & 15, tc = c / G::LPT, q = lane % G::LPT;
+  const int src = (lane & ~(G::LPT - 1)) | ((lane + G::LPT - 1) & (G::LPT - 1));
+
+  // code: tile group tg of the wave, lane's kt = 4s + gk
+  const size_t kstride = (size_t)TN * (8 * K);
+  const uint32_t* cbase = code + (size_t)(tile0 + tc) * (8 * K) + q * G::WPL + gk * kstride;
+  auto load_code = [&](LaneWords<K>* cw, int s) {
+#pragma unroll
+    for (int tg = 0; tg < GPW; ++tg)
+      cw[tg] = load_lane_words<K>(cbase + (size_t)tg * TPS * (8 * K) + (size_t)(4 * s) * kstride);
+  };
+  // x: chunk e = tid + 256j of a stage is row e/8, logical chunk (e%8)^(row&7)
+  // = kt (lc/2) half (lc%2), 128 bytes per row per stage
+  uint32_t xoff[XCH];
+#pragma unroll
+  for (int j = 0; j < XCH; ++j) {
+    const int e = tid + 256 * j, r = e >> 3, lc = (e & 7) ^ (r & 7);
+    xoff[j] = 2u * ((uint32_t)min(row0 + r, M - 1) * IC) + 16u * lc;
+  }
+  const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(xh, (size_t)M * IC * 2);
+  auto load_x = [&](uint4* xr, int s) {
+#pragma unroll
+    for (int j = 0; j < XCH; ++j) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[j], 128u * s, 0);
+      xr[j] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+  };
+  auto store_x = [&](const uint4* xr, int buf) {
+#pragma unroll
+    for (int j = 0; j < XCH; ++j) s_x[buf][tid + 256 * j] = xr[j];
+  };
+
+  f32x4_t acc[NA][NRB];
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int r = 0; r < NRB; ++r) acc[a][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // software pipeline: the MFMAs of step s and the decode of step s+1 sit in
+  // one straight-line body (the matrix pipe and the VALU overlap); loads past
+  // the last step re-read it (in bounds, never used)
+  const int NS = TK / 4;
+  auto decode_step = [&](const LaneWords<K>* w, u32x4_t (*Ad)[2]) {
+#pragma unroll
+    for (int tg = 0; tg < GPW; ++tg) {
+      const uint32_t wprev = __shfl(w[tg].w[G::WPL - 1], src);
+#pragma unroll
+      for (int ci = 0; ci < G::NCOL; ++ci)
+#pragma unroll
+        for (int P = 0; P < 2; ++P) Ad[tg * G::NCOL + ci][P] = mma_a_operand<K>(w[tg], wprev, ci, P);
+    }
+  };
+  LaneWords<K> cw[GPW];
+  uint4 xr[XCH];
+  u32x4_t A[NA][2];
+  load_code(cw, 0);
+  load_x(xr, 0);
+  store_x(xr, 0);
+  decode_step(cw, A);
+  load_code(cw, min(1, NS - 1));
+  lds_barrier();
+  for (int s = 0; s < NS; ++s) {
+    const int buf = s & 1;
+    load_x(xr, min(s + 1, NS - 1));
+    LaneWords<K> cn[GPW];
+    load_code(cn, min(s + 2, NS - 1));
+    u32x4_t An[NA][2];
+#pragma unroll
+    for (int P = 0; P < 2; ++P)
+#pragma unroll
+      for (int r = 0; r < NRB; ++r) {
+        const uint4 bv = s_x[buf][(16 * r + c) * 8 + ((2 * gk + P) ^ (c & 7))];
+        const u32x4_t b = __builtin_bit_cast(u32x4_t, bv);
+#pragma unroll
+        for (int a = 0; a < NA; ++a) acc[a][r] = mma16(A[a][P], b, acc[a][r]);
+      }
+    decode_step(cw, An);
+    store_x(xr, buf ^ 1);
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+      A[a][0] = An[a][0];
+      A[a][1] = An[a][1];
+    }
+#pragma unroll
+    for (int tg = 0; tg < GPW; ++tg) cw[tg] = cn[tg];
+    lds_barrier();
+  }
+
+#pragma unroll
+  for (int r = 0; r < NRB; ++r) {
+    const int row = row0 + 16 * r + c;
+    if (row < M) {
+#pragma unroll
+      for (int tg = 0; tg < GPW; ++tg) {
+        f32x4_t t[G::NCOL];
+#pragma unroll
+        for (int ci = 0; ci < G::NCOL; ++ci) t[ci] = acc[tg * G::NCOL + ci][r];
+        mma_store<K>(t, gk, mid + (size_t)row * OC + 16 * (tile0 + TPS * tg));
+      }
+    }
+  }
+}
+
 }  // namespace esc

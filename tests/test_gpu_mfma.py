@@ -48,7 +48,11 @@ def _dev_ratio(ref: torch.Tensor, got: torch.Tensor) -> float:
 # plus a two-row-block case with an XCD-mapped column count (OC/128 = 8)
 @pytest.mark.parametrize("ic,oc,K,m", [(256, 384, 2, 16), (256, 384, 2, 17), (256, 384, 2, 33),
                                        (512, 640, 3, 16), (512, 640, 3, 17), (512, 640, 3, 33),
-                                       (1024, 1024, 2, 300), (1024, 1024, 3, 300)])
+                                       (1024, 1024, 2, 300), (1024, 1024, 3, 300),
+                                       # OC a multiple of 256 (the direct-A kernel) at shapes for
+                                       # which a 256-CU device picks 2, 4, 6 and 8 row blocks
+                                       (512, 2048, 3, 50), (256, 4096, 2, 600), (256, 4096, 2, 1025),
+                                       (256, 8192, 3, 900)])
 def test_gemm_mat_close_to_rows_and_deterministic(ic, oc, K, m):
     rng = np.random.default_rng(909 + m + K)
     _, code = _code(rng, ic, oc, K)
@@ -62,7 +66,8 @@ def test_gemm_mat_close_to_rows_and_deterministic(ic, oc, K, m):
     assert torch.equal(got.view(torch.int32), again.view(torch.int32)), "not reproducible"
 
 
-@pytest.mark.parametrize("K,ic,oc,m", [(2, 512, 1024, 300), (3, 512, 640, 70), (2, 2048, 128, 257)])
+@pytest.mark.parametrize("K,ic,oc,m", [(2, 512, 1024, 300), (3, 512, 640, 70), (2, 2048, 128, 257),
+                                       (3, 1024, 2048, 75), (2, 256, 4096, 600), (3, 256, 8192, 900)])
 def test_gemm_mat_one_hot_rows_are_decoded_weights(K, ic, oc, m):
     rng = np.random.default_rng(31 * K + m)
     u32, code = _code(rng, ic, oc, K)

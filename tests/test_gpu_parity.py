@@ -409,7 +409,7 @@ def test_moe_exact_chain_stagewise_bit_exact(K_gu, K_dn):
 
 
 @pytest.mark.parametrize("E,T,K_gu,K_dn", [(64, 9, 2, 3), (16, 12, 3, 2), (256, 9, 2, 2)],
-                         ids=["groups_of_2", "groups_of_4", "per_row"])
+                         ids=["grouped", "grouped_experts_over_8_rows", "per_row"])
 def test_moe_multi_launch_path_vs_oracle(E, T, K_gu, K_dn, monkeypatch):
     """More rows than the one-launch path takes (T*k > 64): split-K chain, with
     rows of one expert sharing each decoded weight once rows >= experts
