@@ -397,7 +397,8 @@ def bench_dense(args, torch, ops, cfg):
                    gemm_up_us=round(ms_gu * 1e3, 1), gemm_o_us=round(ms_go * 1e3, 1),
                    roofline={"bound": "mfma", "achieved": round(tf_k, 1), "peak": 2500.0,
                              "unit": "TFLOP/s", "frac": round(tf_k / 2500.0, 4), "traffic": None,
-                             "kernel": "k_gemm_mfma<3> + k_gemm_mfma<2>",
+                             "kernel": "k_gemm_mma2<3,8> + k_gemm_mma2<2,6> (row blocks per "
+                                       "workgroup chosen by the host for this shape)",
                              "flop_per_launch_pair": flop})
         return res
     raise SystemExit(f"config {cfg}: not measured by this bench")

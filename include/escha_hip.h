@@ -98,7 +98,10 @@ int esc_dense_gemm_rows_out(const uint16_t* xh, const uint32_t* code, const floa
                             void* stream);
 
 /* mid f32 [M][OC] = xh f16 [M][IC] @ decode(code [TK][TN][8K]) on the matrix
- * cores (v_mfma_f32_32x32x16_f16, 256 rows x 128 columns per workgroup).
+ * cores: for OC a multiple of 256, v_mfma_f32_16x16x32_f16 with the weights
+ * decoded straight into A operands (16*NRB rows x 256 columns per workgroup,
+ * NRB chosen per shape); otherwise v_mfma_f32_32x32x16_f16 on weights decoded
+ * into LDS (256 rows x 128 columns per workgroup).
  * Decoded weights are bit-exact; the float32 sum is reassociated
  * (deterministic; tolerance contract).  use_lut is accepted for the call
  * surface: table and hash decode give identical weights.
@@ -109,10 +112,11 @@ int esc_gemm_mfma(const uint16_t* xh, const uint32_t* code, int M, int K, int IC
 /* The whole coded linear, y f16 [M][OC] = (bias +) f16((H128(xh @ W) * rs) *
  * rout) with xh = f16(H128(f32(x) * rin) * rs), x f16 [M][IC], rin f32 [IC],
  * rout f32 [OC], bias f16 [OC] or NULL (added in f32 after the f16 round).
- * M < 16: one launch (in-block input transform, split-K GEMV with R rows per
- * decode, the last split of each column group sums the partials in fixed
- * order and output-transforms); M >= 16: input transform, matrix-core GEMM,
- * output transform.  ws: esc_linear_workspace bytes, zero-filled before its
+ * M < 16: one launch (in-block input transform; split-K GEMV, packed dot2 on
+ * the VALU for one row, for 2..15 rows the rows of a group share each decoded
+ * weight on the matrix core; the last split of each column group sums the
+ * partials in fixed order and output-transforms); M >= 16: input transform,
+ * matrix-core GEMM, output transform.  ws: esc_linear_workspace bytes, zero-filled before its
  * first use (its counters are left zero after every call); calls sharing one
  * ws must not overlap.  Tolerance contract (reassociated float32 sum);
  * decoded weights bit-exact.
@@ -124,7 +128,8 @@ int esc_linear(const uint16_t* x, const float* rin, const uint32_t* code, const 
 
 /* Dense GEMM for a few rows, tolerance contract: y f16 [M][OC] =
  * f16((H128(xh @ decode(code)) * rs) * rout), R rows (2, 4 or 8) per
- * workgroup share every decoded weight; split-K partials in ws
+ * workgroup share every decoded weight (one row per B column of
+ * v_mfma_f32_16x16x32_f16); split-K partials in ws
  * (esc_gemm_rows_fast_workspace bytes), summed in fixed order.  Deterministic;
  * reassociated float32 sum.  The decode-once-per-R-rows policy of
  * msl.dense_gemm_rows_direct_out (escha_mlx/msl.py:1844-1870, used by
