@@ -52,46 +52,73 @@ __device__ __forceinline__ void h128_wave(float& v0, float& v1) {
   }
 }
 
+// Transform kernels: one wave per (row, 128-block); a 256-thread workgroup
+// covers kTransformRows rows of one 128-block (kTransformRows / 4 per wave,
+// their loads issued together).  grid (dim/128, ceil(m / kTransformRows)).
+constexpr int kTransformRows = 16;
+
 // xh = f16(H128(f32(rows) * rin) * RS); rin is [E][IC] gathered by row_expert,
 // or [IC] when row_expert is null (escha_mlx/msl.py:875-916, 1029-1047).
-// grid (IC/128, m), block 64.
-__global__ __launch_bounds__(64) void k_input_transform(const uint16_t* __restrict__ rows,
-                                                        const float* __restrict__ rin,
-                                                        const int* __restrict__ row_expert,
-                                                        int IC, float rs,
-                                                        uint16_t* __restrict__ out) {
-  const int blk = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
-  const size_t off = (size_t)row * IC + blk * 128 + 2 * lane;
-  const float* r = rin + (row_expert ? (size_t)row_expert[row] * IC : 0) + blk * 128 + 2 * lane;
-  float v0 = (float)__builtin_bit_cast(half_t, rows[off]) * r[0];
-  float v1 = (float)__builtin_bit_cast(half_t, rows[off + 1]) * r[1];
-  h128_wave(v0, v1);
-  out[off] = __builtin_bit_cast(uint16_t, to_f16(v0 * rs));
-  out[off + 1] = __builtin_bit_cast(uint16_t, to_f16(v1 * rs));
+__global__ __launch_bounds__(256) void k_input_transform(const uint16_t* __restrict__ rows,
+                                                         const float* __restrict__ rin,
+                                                         const int* __restrict__ row_expert,
+                                                         int m, int IC, float rs,
+                                                         uint16_t* __restrict__ out) {
+  constexpr int RPW = kTransformRows / 4;
+  const int blk = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = blk * 128 + 2 * lane;
+  const int row0 = blockIdx.y * kTransformRows + RPW * wave;
+  float v[RPW][2];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) {
+    const int row = min(row0 + j, m - 1);
+    const uint32_t xv = *reinterpret_cast<const uint32_t*>(rows + (size_t)row * IC + c);
+    const float* r = rin + (row_expert ? (size_t)row_expert[row] * IC : 0) + c;
+    v[j][0] = (float)__builtin_bit_cast(half_t, (uint16_t)xv) * r[0];
+    v[j][1] = (float)__builtin_bit_cast(half_t, (uint16_t)(xv >> 16)) * r[1];
+  }
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) {
+    h128_wave(v[j][0], v[j][1]);
+    if (row0 + j < m)
+      *reinterpret_cast<uint32_t*>(out + (size_t)(row0 + j) * IC + c) =
+          (uint32_t)__builtin_bit_cast(uint16_t, to_f16(v[j][0] * rs)) |
+          ((uint32_t)__builtin_bit_cast(uint16_t, to_f16(v[j][1] * rs)) << 16);
+  }
 }
 
 // y = f16((H128(mid) * RS) * rout) [+ bias, added in f32 after the f16 round]
 // (escha_mlx/msl.py:919-949, 1050-1067; bias per dense.py:358-361).
-__global__ __launch_bounds__(64) void k_output_transform(const float* __restrict__ mid,
-                                                         const float* __restrict__ rout,
-                                                         const int* __restrict__ row_expert,
-                                                         const uint16_t* __restrict__ bias,
-                                                         int OC, float rs,
-                                                         uint16_t* __restrict__ out) {
-  const int blk = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
-  const size_t off = (size_t)row * OC + blk * 128 + 2 * lane;
+__global__ __launch_bounds__(256) void k_output_transform(const float* __restrict__ mid,
+                                                          const float* __restrict__ rout,
+                                                          const int* __restrict__ row_expert,
+                                                          const uint16_t* __restrict__ bias,
+                                                          int m, int OC, float rs,
+                                                          uint16_t* __restrict__ out) {
+  constexpr int RPW = kTransformRows / 4;
+  const int blk = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = blk * 128 + 2 * lane;
-  const float* r = rout + (row_expert ? (size_t)row_expert[row] * OC : 0) + c;
-  float v0 = mid[off], v1 = mid[off + 1];
-  h128_wave(v0, v1);
-  half_t y0 = to_f16((v0 * rs) * r[0]);
-  half_t y1 = to_f16((v1 * rs) * r[1]);
-  if (bias) {
-    y0 = to_f16((float)y0 + (float)__builtin_bit_cast(half_t, bias[c]));
-    y1 = to_f16((float)y1 + (float)__builtin_bit_cast(half_t, bias[c + 1]));
+  const int row0 = blockIdx.y * kTransformRows + RPW * wave;
+  float2 v[RPW];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j)
+    v[j] = *reinterpret_cast<const float2*>(mid + (size_t)min(row0 + j, m - 1) * OC + c);
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) {
+    const int row = row0 + j;
+    if (row >= m) continue;  // wave-uniform
+    float v0 = v[j].x, v1 = v[j].y;
+    h128_wave(v0, v1);
+    const float* r = rout + (row_expert ? (size_t)row_expert[row] * OC : 0) + c;
+    half_t y0 = to_f16((v0 * rs) * r[0]);
+    half_t y1 = to_f16((v1 * rs) * r[1]);
+    if (bias) {
+      y0 = to_f16((float)y0 + (float)__builtin_bit_cast(half_t, bias[c]));
+      y1 = to_f16((float)y1 + (float)__builtin_bit_cast(half_t, bias[c + 1]));
+    }
+    *reinterpret_cast<uint32_t*>(out + (size_t)row * OC + c) =
+        (uint32_t)__builtin_bit_cast(uint16_t, y0) | ((uint32_t)__builtin_bit_cast(uint16_t, y1) << 16);
   }
-  out[off] = __builtin_bit_cast(uint16_t, y0);
-  out[off + 1] = __builtin_bit_cast(uint16_t, y1);
 }
 
 // ---------------------------------------------------------------- router

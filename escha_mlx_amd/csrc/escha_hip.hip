@@ -282,6 +282,30 @@ int mma2_row_blocks(int M, int TN) {
   return best;
 }
 
+// k_gemm_mma2 launch (TN % 16 == 0); OUT: output transform fused, y written.
+template <bool OUT>
+int gemm_mma2(int K, const uint16_t* xh, const uint32_t* code, int M, int TK, int TN, float* mid,
+              const float* rout, const uint16_t* bias, float rs, uint16_t* y, hipStream_t s) {
+  const int nrb = mma2_row_blocks(M, TN);
+  const int blocks = ((M + 16 * nrb - 1) / (16 * nrb)) * (TN / 16);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, xh, code, M, TK, TN, mid, rout, bias,
+                       rs, y);
+  };
+  if (K == 2) {
+    if (nrb == 2) go(esc::k_gemm_mma2<2, 2, OUT>);
+    else if (nrb == 4) go(esc::k_gemm_mma2<2, 4, OUT>);
+    else if (nrb == 6) go(esc::k_gemm_mma2<2, 6, OUT>);
+    else go(esc::k_gemm_mma2<2, 8, OUT>);
+  } else {
+    if (nrb == 2) go(esc::k_gemm_mma2<3, 2, OUT>);
+    else if (nrb == 4) go(esc::k_gemm_mma2<3, 4, OUT>);
+    else if (nrb == 6) go(esc::k_gemm_mma2<3, 6, OUT>);
+    else go(esc::k_gemm_mma2<3, 8, OUT>);
+  }
+  return launched("k_gemm_mma2");
+}
+
 }  // namespace
 
 extern "C" {
@@ -307,8 +331,9 @@ int esc_input_transform(const uint16_t* rows, const float* rin, const int32_t* r
   ESC_REQUIRE(IC > 0 && IC % 128 == 0, "Hadamard dimension must be divisible by 128, got %d", IC);
   ESC_REQUIRE(m >= 0, "negative row count");
   if (m == 0) return ESC_OK;
-  hipLaunchKernelGGL(esc::k_input_transform, dim3(IC / 128, m), dim3(64), 0, S(stream), rows,
-                     rin, row_expert, IC, rs, out);
+  const int ry = (m + esc::kTransformRows - 1) / esc::kTransformRows;
+  hipLaunchKernelGGL(esc::k_input_transform, dim3(IC / 128, ry), dim3(256), 0, S(stream), rows,
+                     rin, row_expert, m, IC, rs, out);
   return launched("k_input_transform");
 }
 
@@ -319,8 +344,9 @@ int esc_output_transform(const float* mid, const float* rout, const int32_t* row
   ESC_REQUIRE(OC > 0 && OC % 128 == 0, "Hadamard dimension must be divisible by 128, got %d", OC);
   ESC_REQUIRE(m >= 0, "negative row count");
   if (m == 0) return ESC_OK;
-  hipLaunchKernelGGL(esc::k_output_transform, dim3(OC / 128, m), dim3(64), 0, S(stream), mid,
-                     rout, row_expert, bias, OC, rs, out);
+  const int ry = (m + esc::kTransformRows - 1) / esc::kTransformRows;
+  hipLaunchKernelGGL(esc::k_output_transform, dim3(OC / 128, ry), dim3(256), 0, S(stream), mid,
+                     rout, row_expert, bias, m, OC, rs, out);
   return launched("k_output_transform");
 }
 
@@ -392,10 +418,12 @@ int esc_linear(const uint16_t* x, const float* rin, const uint32_t* code, const 
     return use_lut ? LinearSmallF<3, true>::run(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s)
                    : LinearSmallF<3, false>::run(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
   }
-  // many rows: input transform, matrix-core GEMM, output transform
+  // many rows: input transform, then the matrix-core GEMM with the output
+  // transform in its epilogue (or GEMM + output transform for OC % 256 != 0)
   uint16_t* xh = reinterpret_cast<uint16_t*>(w + lp.off_xh);
-  float* mid = reinterpret_cast<float*>(w + lp.off_mid);
   if (int rc = esc_input_transform(x, rin, nullptr, M, IC, rs, xh, stream)) return rc;
+  if (TN % 16 == 0) return gemm_mma2<true>(K, xh, code, M, TK, TN, nullptr, rout, bias, rs, y, s);
+  float* mid = reinterpret_cast<float*>(w + lp.off_mid);
   if (int rc = esc_gemm_mfma(xh, code, M, K, IC, OC, use_lut, mid, stream)) return rc;
   return esc_output_transform(mid, rout, nullptr, bias, M, OC, rs, y, stream);
 }
@@ -488,25 +516,8 @@ int esc_gemm_mfma(const uint16_t* xh, const uint32_t* code, int M, int K, int IC
   if (M == 0) return ESC_OK;
   const int TK = IC / 16, TN = OC / 16;
   hipStream_t s = S(stream);
-  if (TN % 16 == 0) {
-    const int nrb = mma2_row_blocks(M, TN);
-    const int blocks = ((M + 16 * nrb - 1) / (16 * nrb)) * (TN / 16);
-    auto go = [&](auto kern) {
-      hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, xh, code, M, TK, TN, mid);
-    };
-    if (K == 2) {
-      if (nrb == 2) go(esc::k_gemm_mma2<2, 2>);
-      else if (nrb == 4) go(esc::k_gemm_mma2<2, 4>);
-      else if (nrb == 6) go(esc::k_gemm_mma2<2, 6>);
-      else go(esc::k_gemm_mma2<2, 8>);
-    } else {
-      if (nrb == 2) go(esc::k_gemm_mma2<3, 2>);
-      else if (nrb == 4) go(esc::k_gemm_mma2<3, 4>);
-      else if (nrb == 6) go(esc::k_gemm_mma2<3, 6>);
-      else go(esc::k_gemm_mma2<3, 8>);
-    }
-    return launched("k_gemm_mma2");
-  }
+  if (TN % 16 == 0)
+    return gemm_mma2<false>(K, xh, code, M, TK, TN, mid, nullptr, nullptr, 0.f, nullptr, s);
   const int blocks = ((M + esc::kMmaRows - 1) / esc::kMmaRows) * (TN / 8);
   if (K == 2)
     hipLaunchKernelGGL(esc::k_gemm_mfma<2>, dim3(blocks), dim3(esc::kMmaThreads), 0, s, xh, code,

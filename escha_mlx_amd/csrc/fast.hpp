@@ -346,6 +346,9 @@ __device__ __forceinline__ void mma_tile(const LaneWords<K>& lw, uint32_t wprev,
   }
 }
 
+__device__ __forceinline__ uint32_t pack2(half_t a, half_t b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
 __device__ __forceinline__ void st_coherent(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v),
                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

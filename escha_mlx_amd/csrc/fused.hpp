@@ -195,9 +195,6 @@ __device__ __forceinline__ void compute_item(const ItemCode<K, NKT>& code, const
   }
 }
 
-__device__ __forceinline__ uint32_t pack2(half_t a, half_t b) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-}
 
 template <int K, int KTA>
 __device__ __forceinline__ ItemCode<K, KTA> load_gate_up(const FusedMoe& p, int l, int a) {

@@ -302,10 +302,15 @@ __global__ __launch_bounds__(kMmaThreads, 2) void k_gemm_mfma(const uint16_t* __
 // The kernel is decode-bound: the host picks NRB for the shape.
 // D register r of lane l: output column of tile-lane 4(l/16) + r, row l%16 of
 // the row block.
-template <int K, int NRB>
+// OUT: the output transform is fused into the epilogue (y f16 = (bias +)
+// f16((H128(row) * rs) * rout), the formula of k_output_transform): per 16-row
+// block the two waves of each 128-column block exchange their 64 columns
+// through LDS and each transforms 8 rows; mid is not written.
+template <int K, int NRB, bool OUT = false>
 __global__ __launch_bounds__(256, 2) void k_gemm_mma2(
     const uint16_t* __restrict__ xh, const uint32_t* __restrict__ code, int M, int TK, int TN,
-    float* __restrict__ mid) {
+    float* __restrict__ mid, const float* __restrict__ rout = nullptr,
+    const uint16_t* __restrict__ bias = nullptr, float rs = 0.f, uint16_t* __restrict__ y = nullptr) {
   using G = Geo<K>;
   constexpr int TPS = 16 / G::LPT, GPW = 4 / TPS, NA = GPW * G::NCOL;
   static_assert(NA == 4, "four 16-column groups per wave");
@@ -416,17 +421,58 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mma2(
     lds_barrier();
   }
 
+  if constexpr (!OUT) {
 #pragma unroll
-  for (int r = 0; r < NRB; ++r) {
-    const int row = row0 + 16 * r + c;
-    if (row < M) {
+    for (int r = 0; r < NRB; ++r) {
+      const int row = row0 + 16 * r + c;
+      if (row < M) {
 #pragma unroll
-      for (int tg = 0; tg < GPW; ++tg) {
-        f32x4_t t[G::NCOL];
+        for (int tg = 0; tg < GPW; ++tg) {
+          f32x4_t t[G::NCOL];
 #pragma unroll
-        for (int ci = 0; ci < G::NCOL; ++ci) t[ci] = acc[tg * G::NCOL + ci][r];
-        mma_store<K>(t, gk, mid + (size_t)row * OC + 16 * (tile0 + TPS * tg));
+          for (int ci = 0; ci < G::NCOL; ++ci) t[ci] = acc[tg * G::NCOL + ci][r];
+          mma_store<K>(t, gk, mid + (size_t)row * OC + 16 * (tile0 + TPS * tg));
+        }
       }
+    }
+  } else {
+    constexpr int kPitch = 128 + 4;  // floats per staged row
+    static_assert(sizeof(s_x) >= 2 * 16 * kPitch * sizeof(float) || NRB < 6, "");
+    __shared__ float s_o[NRB < 6 ? 2 * 16 * kPitch : 1];
+    float* so = NRB < 6 ? s_o : reinterpret_cast<float*>(&s_x[0][0]);
+    const int pair = wave >> 1, hw = wave & 1;
+    float* sp = so + pair * 16 * kPitch;
+    const int col0 = 256 * cb + 128 * pair;  // the pair's 128-column block
+#pragma unroll
+    for (int r = 0; r < NRB; ++r) {
+      // this wave's 64 columns of rows 16r..16r+15 into the pair's LDS block
+#pragma unroll
+      for (int tg = 0; tg < GPW; ++tg)
+#pragma unroll
+        for (int ci = 0; ci < G::NCOL; ++ci)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int i = 4 * gk + rr, tc = i / G::LPT, q = i % G::LPT;
+            sp[c * kPitch + 64 * hw + 16 * (TPS * tg + tc) + G::col(q, ci)] =
+                acc[tg * G::NCOL + ci][r][rr];
+          }
+      __syncthreads();
+#pragma unroll 2
+      for (int j = 0; j < 8; ++j) {
+        const int rl = 8 * hw + j, row = row0 + 16 * r + rl;
+        float v0 = sp[rl * kPitch + 2 * lane], v1 = sp[rl * kPitch + 2 * lane + 1];
+        h128_wave(v0, v1);
+        const int col = col0 + 2 * lane;
+        half_t y0 = to_f16((v0 * rs) * rout[col]);
+        half_t y1 = to_f16((v1 * rs) * rout[col + 1]);
+        if (bias) {
+          y0 = to_f16((float)y0 + (float)__builtin_bit_cast(half_t, bias[col]));
+          y1 = to_f16((float)y1 + (float)__builtin_bit_cast(half_t, bias[col + 1]));
+        }
+        if (row < M)
+          *reinterpret_cast<uint32_t*>(y + (size_t)row * OC + col) = pack2(y0, y1);
+      }
+      __syncthreads();
     }
   }
 }

@@ -139,3 +139,22 @@ def test_module_default_uses_one_launch_linear(monkeypatch):
         monkeypatch.setenv("ESCHA_HIP_EXACT", "1")
         y_exact = EschaLinear(w, bias=bias)(x).float()
         assert float((y_fast - y_exact).abs().max() / y_exact.abs().max()) < 2e-3
+
+
+@pytest.mark.parametrize("K,ic,oc,m", [(2, 1024, 1024, 40), (3, 512, 2048, 300), (2, 256, 4096, 600),
+                                       (3, 1024, 768, 33), (2, 512, 640, 50)])
+def test_linear_many_rows_fused_epilogue_equals_three_launches(K, ic, oc, m):
+    """From 16 rows esc_linear runs the input transform and the matrix-core GEMM
+    with the output transform in its epilogue (OC a multiple of 256; otherwise
+    GEMM + output transform): bit-identical to the three separate C-ABI calls."""
+    rng = np.random.default_rng(3 * K + m)
+    u32, rin, rout = _proj(rng, ic, oc, K)
+    bias = _dev((rng.standard_normal(oc) * 0.05).astype(np.float16))
+    x = _dev(rng.standard_normal((m, ic)).astype(np.float16))
+    code, rin_d, rout_d = _code(u32), _dev(rin), _dev(rout)
+    for b in (None, bias):
+        y = ops().linear(x, code, rin_d, rout_d, K, ic, oc, bias=b)
+        xh = ops().scaled_had(x, rin_d, None)
+        mid = ops().dense_gemm_mat(xh, code, K, ic, oc)
+        want = ops().scaled_had_out(mid, rout_d, None, bias=b)
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16))
