@@ -30,6 +30,29 @@ __global__ __launch_bounds__(256) void k_decode_tiles(const uint32_t* __restrict
 // One wave owns one 128-block of one row; lane l holds elements 2l and 2l+1.
 // Stage s pairs i with i ^ (1 << s), bit 0 first, (a + b, a - b) in float32
 // (escha_mlx/ref.py:204-218, msl.py:905-913).  Built with -ffp-contract=off.
+// The lane exchanges stay on the VALU: DPP quad permutes for lane ^ 1 and
+// ^ 2, two bank-masked DPP row shifts for ^ 4 and ^ 8, and the gfx950 row /
+// half-wave swaps (v_permlane16_swap, v_permlane32_swap) for ^ 16 and ^ 32.
+
+// value of lane ^ M (M in {1, 2, 4, 8}: within a row of 16 lanes)
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  int r;
+  if constexpr (M == 1) {
+    r = __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (M == 2) {
+    r = __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else {
+    // lanes with bit M clear read lane + M (row_shl), the others lane - M
+    // (row_shr); each shift writes only its banks of 4 lanes
+    constexpr int lo_banks = M == 4 ? 0x5 : 0x3, hi_banks = M == 4 ? 0xA : 0xC;
+    r = __builtin_amdgcn_update_dpp(x, x, 0x100 + M, 0xF, lo_banks, false);
+    r = __builtin_amdgcn_update_dpp(r, x, 0x110 + M, 0xF, hi_banks, false);
+  }
+  return __builtin_bit_cast(float, r);
+}
+
 __device__ __forceinline__ void h128_wave(float& v0, float& v1) {
   const int lane = threadIdx.x & 63;
   {
@@ -37,19 +60,36 @@ __device__ __forceinline__ void h128_wave(float& v0, float& v1) {
     v0 = a + b;
     v1 = a - b;
   }
-#pragma unroll
-  for (int s = 1; s < 7; ++s) {
-    const int m = 1 << (s - 1);
-    float o0 = __shfl_xor(v0, m);
-    float o1 = __shfl_xor(v1, m);
-    if (lane & m) {
+  auto stage = [&](float o0, float o1, bool upper) {
+    if (upper) {
       v0 = o0 - v0;
       v1 = o1 - v1;
     } else {
       v0 = v0 + o0;
       v1 = v1 + o1;
     }
-  }
+  };
+  stage(lane_xor<1>(v0), lane_xor<1>(v1), lane & 1);
+  stage(lane_xor<2>(v0), lane_xor<2>(v1), lane & 2);
+  stage(lane_xor<4>(v0), lane_xor<4>(v1), lane & 4);
+  stage(lane_xor<8>(v0), lane_xor<8>(v1), lane & 8);
+  // ^ 16 and ^ 32: the swap returns the lower partner's value (lo) and the
+  // upper partner's (hi) in every lane: a + b below, a - b above
+  auto swap_stage = [&](auto swp, bool upper) {
+    const auto p0 = swp(__builtin_bit_cast(unsigned, v0));
+    const auto p1 = swp(__builtin_bit_cast(unsigned, v1));
+    // elements copied out first: __builtin_bit_cast of a vector element
+    // reads element 0 with this compiler
+    const unsigned l0 = p0[0], h0 = p0[1], l1 = p1[0], h1 = p1[1];
+    const float lo0 = __builtin_bit_cast(float, l0), hi0 = __builtin_bit_cast(float, h0);
+    const float lo1 = __builtin_bit_cast(float, l1), hi1 = __builtin_bit_cast(float, h1);
+    v0 = upper ? lo0 - hi0 : lo0 + hi0;
+    v1 = upper ? lo1 - hi1 : lo1 + hi1;
+  };
+  swap_stage([](unsigned x) { return __builtin_amdgcn_permlane16_swap(x, x, false, false); },
+             lane & 16);
+  swap_stage([](unsigned x) { return __builtin_amdgcn_permlane32_swap(x, x, false, false); },
+             lane & 32);
 }
 
 // Transform kernels: one wave per (row, 128-block); a 256-thread workgroup

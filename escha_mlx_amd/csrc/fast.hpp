@@ -391,8 +391,46 @@ __device__ __forceinline__ void mma_store(const f32x4_t* acc, int g, float* dst)
   }
 }
 
+// One wave's share of the split-K row-group GEMM on the matrix core: tiles
+// [tile0, tile0 + 16/LPT) of the stream at code_e over kt [z*KS, (z+1)*KS),
+// B column c = input row xr_c (the lane's row, xr), accumulated into acc.
+template <int K, bool LUT>
+__device__ __forceinline__ void rows_mma_accum(const uint16_t* __restrict__ xh,
+                                               const uint32_t* __restrict__ code_e, int xr,
+                                               int TK, int TN, int KS, int z, int tile0,
+                                               const uint16_t* s_lut, f32x4_t* acc) {
+  using G = Geo<K>;
+  const int lane = threadIdx.x & 63;
+  const int gk = lane >> 4, tc = (lane & 15) / G::LPT, q = lane % G::LPT;
+  const int src = (lane & ~(G::LPT - 1)) | ((lane + G::LPT - 1) & (G::LPT - 1));
+  const uint4* xq = reinterpret_cast<const uint4*>(xh + (size_t)xr * TK * 16);
+  const size_t kstride = (size_t)TN * (8 * K);
+  const uint32_t* lp = code_e + (size_t)(tile0 + tc) * (8 * K) + q * G::WPL;
+  const int kt0 = z * KS + gk, nsteps = KS / 4;
+#pragma unroll
+  for (int i = 0; i < G::NCOL; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  LaneWords<K> cur = load_lane_words<K>(lp + (size_t)kt0 * kstride);
+  uint4 xa = xq[2 * kt0], xb = xq[2 * kt0 + 1];
+  for (int k = 0; k < nsteps; ++k) {
+    LaneWords<K> nxt = cur;
+    uint4 na = xa, nb = xb;
+    if (k + 1 < nsteps) {
+      const int kt = kt0 + 4 * (k + 1);
+      nxt = load_lane_words<K>(lp + (size_t)kt * kstride);
+      na = xq[2 * kt];
+      nb = xq[2 * kt + 1];
+    }
+    const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
+    mma_tile<K, LUT>(cur, wprev, __builtin_bit_cast(u32x4_t, xa), __builtin_bit_cast(u32x4_t, xb),
+                     acc, s_lut);
+    cur = nxt;
+    xa = na;
+    xb = nb;
+  }
+}
+
 // Split-K GEMM for up to 16 rows sharing every decoded weight, on the matrix
-// core (mma_tile; B column c = row c of the group): part[z][row][OC] as
+// core (rows_mma_accum; B column c = row c of the group): part[z][row][OC] as
 // k_gemv_fast.  grid (ceil(TN/TPW), n_groups, S), block 256; wave w owns tiles
 // [TPW*x + (16/LPT)*w, +16/LPT) over the block's KS kt (KS % 4 == 0), so no
 // cross-wave reduction.  Dense (rows_idx null): group g is rows gR..gR+R-1 of
@@ -417,43 +455,18 @@ __global__ __launch_bounds__(256) void k_gemv_fast_rows(const uint16_t* __restri
   __shared__ uint16_t s_lut[LUT ? 65536 : 1];
   stage_lut<LUT>(s_lut);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int z = blockIdx.z;
-  const int IC = TK * 16, OC = TN * 16;
   const int tile0 = blockIdx.x * G::TPW + TPS * wave;
   if (tile0 >= TN) return;  // whole wave (TN is a multiple of TPS)
-  const int gk = lane >> 4, c = lane & 15, tc = c / G::LPT, q = lane % G::LPT;
-  const int src = (lane & ~(G::LPT - 1)) | ((lane + G::LPT - 1) & (G::LPT - 1));
+  const int gk = lane >> 4, c = lane & 15;
   // the lane's B column: row min(c, R-1) of the group
   const int rc = c < R ? c : R - 1;
   const int row = rows_idx ? rows_idx[grp * R + rc] : min(grp * R + rc, M);
   const int xr = row < M ? row : (rows_idx ? 0 : M - 1);
-  const uint4* xq = reinterpret_cast<const uint4*>(xh + (size_t)xr * IC);
-  const size_t kstride = (size_t)TN * (8 * K);
-  const uint32_t* lp = code + (size_t)e * TK * kstride + (size_t)(tile0 + tc) * (8 * K) +
-                       q * G::WPL;
-  const int kt0 = z * KS + gk, nsteps = KS / 4;
   f32x4_t acc[G::NCOL];
-#pragma unroll
-  for (int i = 0; i < G::NCOL; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  LaneWords<K> cur = load_lane_words<K>(lp + (size_t)kt0 * kstride);
-  uint4 xa = xq[2 * kt0], xb = xq[2 * kt0 + 1];
-  for (int k = 0; k < nsteps; ++k) {
-    LaneWords<K> nxt = cur;
-    uint4 na = xa, nb = xb;
-    if (k + 1 < nsteps) {
-      const int kt = kt0 + 4 * (k + 1);
-      nxt = load_lane_words<K>(lp + (size_t)kt * kstride);
-      na = xq[2 * kt];
-      nb = xq[2 * kt + 1];
-    }
-    const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
-    mma_tile<K, LUT>(cur, wprev, __builtin_bit_cast(u32x4_t, xa), __builtin_bit_cast(u32x4_t, xb),
-                     acc, s_lut);
-    cur = nxt;
-    xa = na;
-    xb = nb;
-  }
-  if (c < R && row < M) mma_store<K>(acc, gk, part + ((size_t)z * M + row) * OC + 16 * tile0);
+  rows_mma_accum<K, LUT>(xh, code + (size_t)e * TK * TN * (8 * K), xr, TK, TN, KS, blockIdx.z,
+                         tile0, s_lut, acc);
+  if (c < R && row < M)
+    mma_store<K>(acc, gk, part + ((size_t)blockIdx.z * M + row) * TN * 16 + 16 * tile0);
 }
 
 // Partial GEMV: part[z][row][OC] = sum over the block's kt range.

@@ -34,31 +34,32 @@ __device__ __forceinline__ half_t swiglu1(half_t g, half_t u) {
   return to_f16((float)s16 * (float)u);
 }
 
-// One 128-block of the gate_up output of one row, from split-K partials:
-// f16((H128(sum_z part) * RS) * rout[e]) for the lane's two elements.
-__device__ __forceinline__ void gu_block(const float* __restrict__ part, int S, int M, int OC,
-                                         int row, int blk, const float* __restrict__ rout_e,
-                                         float rs, half_t& y0, half_t& y1) {
-  const int lane = threadIdx.x & 63;
-  const int c = blk * 128 + 2 * lane;
-  float v0 = 0.f, v1 = 0.f;
-  // loads issued 8 at a time so their latencies overlap; summed in z order
-  for (int z0 = 0; z0 < S; z0 += 8) {
-    float2 pv[8];
+// Split-K sums, in z order, of the partials of several (row, column pair)
+// points at once: every point's loads of a 4-split chunk are issued before
+// any add, so the points' memory latencies overlap.
+template <int NP>
+__device__ __forceinline__ void sum_splits(const float* __restrict__ part, int S, int M, int OC,
+                                           const int* rows, const int* cols, float2* v) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (z0 + j < S)
-        pv[j] = *reinterpret_cast<const float2*>(part + ((size_t)(z0 + j) * M + row) * OC + c);
+  for (int j = 0; j < NP; ++j) v[j] = make_float2(0.f, 0.f);
+  for (int z0 = 0; z0 < S; z0 += 4) {
+    float2 pv[NP][4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (z0 + j < S) {
-        v0 = v0 + pv[j].x;
-        v1 = v1 + pv[j].y;
-      }
+    for (int j = 0; j < NP; ++j)
+#pragma unroll
+      for (int zz = 0; zz < 4; ++zz)
+        if (rows[j] >= 0 && z0 + zz < S)
+          pv[j][zz] = *reinterpret_cast<const float2*>(
+              part + ((size_t)(z0 + zz) * M + rows[j]) * OC + cols[j]);
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+#pragma unroll
+      for (int zz = 0; zz < 4; ++zz)
+        if (rows[j] >= 0 && z0 + zz < S) {
+          v[j].x = v[j].x + pv[j][zz].x;
+          v[j].y = v[j].y + pv[j][zz].y;
+        }
   }
-  h128_wave(v0, v1);
-  y0 = to_f16((v0 * rs) * rout_e[c]);
-  y1 = to_f16((v1 * rs) * rout_e[c + 1]);
 }
 
 // gate_up epilogue -> swiglu -> down input transform, one wave per
@@ -72,11 +73,16 @@ __global__ __launch_bounds__(64) void k_moe_mid(const float* __restrict__ part, 
   const int e = ids[row];
   const int OC = 2 * I;
   const float* ro = gu_rout + (size_t)e * OC;
-  half_t g0, g1, u0, u1;
-  gu_block(part, S, M, OC, row, b, ro, rs, g0, g1);
-  gu_block(part, S, M, OC, row, b + I / 128, ro, rs, u0, u1);
-  const half_t h0 = swiglu1(g0, u0), h1 = swiglu1(g1, u1);
   const int c = b * 128 + 2 * lane;
+  // the gate and up partials of the lane's two columns, summed in z order
+  const int rows2[2] = {row, row}, cols2[2] = {c, I + c};
+  float2 gu[2];
+  sum_splits<2>(part, S, M, OC, rows2, cols2, gu);
+  h128_wave(gu[0].x, gu[0].y);
+  h128_wave(gu[1].x, gu[1].y);
+  const half_t g0 = to_f16((gu[0].x * rs) * ro[c]), g1 = to_f16((gu[0].y * rs) * ro[c + 1]);
+  const half_t u0 = to_f16((gu[1].x * rs) * ro[I + c]), u1 = to_f16((gu[1].y * rs) * ro[I + c + 1]);
+  const half_t h0 = swiglu1(g0, u0), h1 = swiglu1(g1, u1);
   const float* ri = dn_rin + (size_t)e * I + c;
   float v0 = (float)h0 * ri[0];
   float v1 = (float)h1 * ri[1];
@@ -87,8 +93,9 @@ __global__ __launch_bounds__(64) void k_moe_mid(const float* __restrict__ part, 
 }
 
 // down epilogue + weighted combine: y[t] = f16(sum_s f32(d16[t*k+s]) * f32(f16(score)))
-// summed in slot order in float32 (models/qwen3_5_moe.py:227-253).
-// grid (H/128, T), block 64.
+// summed in slot order in float32 (models/qwen3_5_moe.py:227-253).  The
+// partials of 8 slots are requested together, then transformed and summed
+// in slot order.  grid (H/128, T), block 64.
 __global__ __launch_bounds__(64) void k_moe_combine(const float* __restrict__ part, int S,
                                                     int M, int H, const int* __restrict__ ids,
                                                     const float* __restrict__ scores, int top_k,
@@ -97,13 +104,27 @@ __global__ __launch_bounds__(64) void k_moe_combine(const float* __restrict__ pa
   const int blk = blockIdx.x, tok = blockIdx.y, lane = threadIdx.x;
   const int c = blk * 128 + 2 * lane;
   float a0 = 0.f, a1 = 0.f;
-  for (int s = 0; s < top_k; ++s) {
-    const int row = tok * top_k + s, e = ids[row];
-    half_t d0, d1;
-    gu_block(part, S, M, H, row, blk, dn_rout + (size_t)e * H, rs, d0, d1);
-    const float w = (float)(half_t)scores[row];
-    a0 = a0 + (float)d0 * w;
-    a1 = a1 + (float)d1 * w;
+  for (int s0 = 0; s0 < top_k; s0 += 8) {
+    int rows[8], cols[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      rows[j] = s0 + j < top_k ? tok * top_k + s0 + j : -1;
+      cols[j] = c;
+    }
+    float2 d[8];
+    sum_splits<8>(part, S, M, H, rows, cols, d);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (rows[j] < 0) break;  // uniform
+      const int row = rows[j], e = ids[row];
+      h128_wave(d[j].x, d[j].y);
+      const float* ro = dn_rout + (size_t)e * H;
+      const half_t d0 = to_f16((d[j].x * rs) * ro[c]);
+      const half_t d1 = to_f16((d[j].y * rs) * ro[c + 1]);
+      const float w = (float)(half_t)scores[row];
+      a0 = a0 + (float)d0 * w;
+      a1 = a1 + (float)d1 * w;
+    }
   }
   y[(size_t)tok * H + c] = __builtin_bit_cast(uint16_t, (half_t)a0);
   y[(size_t)tok * H + c + 1] = __builtin_bit_cast(uint16_t, (half_t)a1);

@@ -167,7 +167,10 @@ int esc_moe_combine(const uint16_t* d16, const float* scores, int T, int top_k, 
  * gate_up linear (H -> 2I, K_gu) -> swiglu -> down linear (I -> H, K_dn).
  * gu_code [E][H/16][2I/16][8K_gu], gu_rin [E][H], gu_rout [E][2I],
  * dn_code [E][I/16][H/16][8K_dn], dn_rin [E][I], dn_rout [E][H] (f32).
- * Tolerance contract (reassociated GEMV sums; decode bit-exact).
+ * Tolerance contract (reassociated GEMV sums; decode bit-exact).  ws:
+ * esc_moe_expert_path_workspace bytes, zero-filled before its first use (the
+ * counters it holds are left zero by every call); calls sharing one ws must
+ * not overlap.
  * Replaces EschaSparseMoeBlock._expert_path (escha_mlx/models/qwen3_5_moe.py:207-253). */
 size_t esc_moe_expert_path_workspace(int T, int top_k, int E, int H, int I);
 int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, int T,

@@ -408,13 +408,16 @@ def test_moe_exact_chain_stagewise_bit_exact(K_gu, K_dn):
     assert np.array_equal(bits16(y), y_ref.astype(np.float16).view(np.uint16))
 
 
-@pytest.mark.parametrize("E,T,K_gu,K_dn", [(64, 9, 2, 3), (16, 12, 3, 2), (256, 9, 2, 2)],
-                         ids=["grouped", "grouped_experts_over_8_rows", "per_row"])
-def test_moe_multi_launch_path_vs_oracle(E, T, K_gu, K_dn, monkeypatch):
+@pytest.mark.parametrize("E,T,K_gu,K_dn,H", [(64, 9, 2, 3, 256), (16, 12, 3, 2, 256),
+                                             (256, 9, 2, 2, 256), (16, 12, 2, 2, 384)],
+                         ids=["grouped", "grouped_experts_over_8_rows", "per_row",
+                              "grouped_partial_tile_group"])
+def test_moe_multi_launch_path_vs_oracle(E, T, K_gu, K_dn, H, monkeypatch):
     """More rows than the one-launch path takes (T*k > 64): split-K chain, with
     rows of one expert sharing each decoded weight once rows >= experts
-    (groups in the moe.build_groups layout), per row otherwise; deterministic."""
-    H, I, k = 256, 128, 8
+    (groups in the moe.build_groups layout), per row otherwise; deterministic,
+    and repeat calls on one workspace agree."""
+    I, k = 128, 8
     c = _moe_case(E, H, I, K_gu, K_dn, T, k, 5 + E)
     blk = _block(c, E, k, K_gu, K_dn, monkeypatch, exact=False)
     ids, sc = ops().route_topk(torch.from_numpy(c["logits"]).to(DEV), k)
