@@ -64,8 +64,9 @@ def parse():
     ap.add_argument("--only", choices=["both", "sustained", "chained"], default="both")
     ap.add_argument("--probe", action="store_true",
                     help="run the calibration copy and two sustained calls, untimed (for PMC)")
-    ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5], default=3,
-                    help="BASELINE config; 3 (the headline metric) by default")
+    ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5, 6], default=3,
+                    help="BASELINE config; 3 (the headline metric) by default; 6 is not a "
+                         "BASELINE config: the w8a16 vocabulary-head GEMV around the MoE block")
     return ap.parse_args()
 
 
@@ -441,6 +442,42 @@ def bench_c4(args, torch, ops):
             "distinct_experts_per_layer": distinct, "tok_s_per_layer": round(T / (ms * 1e-3), 1)}
 
 
+def bench_q8_head(args, torch, ops):
+    """Not a BASELINE config: the int8 vocabulary head of the 35B model
+    (248,320 x 2048 w8a16, the reference's lm_head bench shape,
+    bench/results/m5-pro-24gb/roofline.json:15-24) at batch 1 and 8."""
+    dev = "cuda:0"
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    stream = torch.cuda.current_stream()
+    O, K, copies = 248320, 2048, 2   # 2 x 509 MB rotated: beyond the 256 MB Infinity Cache
+    w8 = [torch.randint(-128, 128, (O, K), dtype=torch.int8, device=dev, generator=g)
+          for _ in range(copies)]
+    sc = [torch.rand(O, generator=g, device=dev) * 4e-3 + 1e-3 for _ in range(copies)]
+    nbytes = O * K + O * 4
+    per = {}
+    for M in (1, 8):
+        x = torch.randn(M, K, generator=g, device=dev).half()
+        y = torch.empty(M, O, dtype=torch.float16, device=dev)
+        ms = timed(torch, lambda i: ops.w8a16(x, w8[i % copies], sc[i % copies], out=y),
+                   args.steps * 5, args.warmup, stream)
+        per[f"M{M}_us"] = round(ms * 1e3, 2)
+        per[f"M{M}_gbs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    gbs = per["M1_gbs"]
+    return {"metric": "w8a16 GEMV GB/s (int8 weights + f32 row scales), 248320x2048 vocabulary "
+                      "head at batch 1", "value": gbs, "unit": "GB/s", "n_gpus": 1,
+            "steps": args.steps * 5, "warmup": args.warmup, "ms_per_step": per["M1_us"] / 1e3,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "int8 weights -> f16 (w8a16 contract), f32 accumulate",
+            "data": "synthetic: uniform int8, U[1e-3, 5e-3] scales, x ~ N(0,1) f16",
+            "config": {"workload": "not a BASELINE config: 248320x2048 w8a16 head (k_rows_gemv), "
+                                   "M=1 and M=8, 2 weight copies rotated"},
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": 8000.0, "unit": "GB/s",
+                         "frac": round(gbs / 8000.0, 4), "traffic": None,
+                         "kernel": "k_rows_gemv<true,1,64,2>", "bytes_per_launch": nbytes},
+            **per}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -453,8 +490,12 @@ def main():
         from escha_mlx_amd import ops
         torch.cuda.set_device(0)
         ops.init()
-        res = bench_c4(args, torch, ops) if args.config == 4 else bench_dense(args, torch, ops,
-                                                                              args.config)
+        if args.config == 4:
+            res = bench_c4(args, torch, ops)
+        elif args.config == 6:
+            res = bench_q8_head(args, torch, ops)
+        else:
+            res = bench_dense(args, torch, ops, args.config)
         print(json.dumps(res))
         return
     traffic, traffic_detail = None, "not measured (--no-traffic)"

@@ -9,8 +9,10 @@ reached from Python through ctypes with the reference's call surface:
   ops    — escha_mlx.msl kernel wrappers (decode_tiles, moe_gemv, scaled_had, ...)
   dense  — escha_mlx.dense (EschaWeight, EschaLinear, build, pack_code, ...)
   moe    — escha_mlx.moe (EschaExperts, build_groups, ...) + the expert path
+           and the whole MoE block (router, shared expert)
+  quant  — escha_mlx.quant's w8a16 linears (EschaQ8Linear, make_linear, ...)
 """
-from . import _lib, dense, envs, moe, ops  # noqa: F401
+from . import _lib, dense, envs, moe, ops, quant  # noqa: F401
 
-__all__ = ["ops", "dense", "moe", "envs"]
+__all__ = ["ops", "dense", "moe", "quant", "envs"]
 __version__ = "0.1.0"

@@ -15,6 +15,7 @@
 #include "fused.hpp"
 #include "mfma.hpp"
 #include "linear.hpp"
+#include "q8.hpp"
 
 namespace {
 
@@ -568,6 +569,91 @@ int esc_moe_combine(const uint16_t* d16, const float* scores, int T, int top_k, 
   hipLaunchKernelGGL(esc::k_combine, dim3((H + 255) / 256, T), dim3(256), 0, S(stream), d16,
                      scores, top_k, H, y);
   return launched("k_combine");
+}
+
+// ---- dense int8 / f16 GEMV (q8.hpp): shared expert, gates, vocabulary head
+
+}  // extern "C"
+
+namespace {
+// one launch of k_rows_gemv for up to 8 rows of x
+template <bool Q8, int NR>
+int rows_gemv_nr(const uint16_t* x, const void* w, const float* scale, int M, int K, int O,
+                 uint16_t* y, hipStream_t s) {
+  const int chunks = K / (Q8 ? 16 : 8);
+  const int lpr = chunks >= 64 ? 64 : 32, cpl = chunks / lpr;
+  const long steps = ((long)O + 64 / lpr - 1) / (64 / lpr);
+  // four workgroups per CU, each wave striding over the row steps (measured
+  // on MI355X: 1024 workgroups stream the 248320 x 2048 head fastest)
+  const int blocks = (int)std::min<long>((steps + 3) / 4, 4L * device_cus());
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, x, w, scale, M, K, O, y, O);
+  };
+  if (lpr == 32) go(esc::k_rows_gemv<Q8, NR, 32, 1>);
+  else if (cpl == 1) go(esc::k_rows_gemv<Q8, NR, 64, 1>);
+  else if (cpl == 2) go(esc::k_rows_gemv<Q8, NR, 64, 2>);
+  else go(esc::k_rows_gemv<Q8, NR, 64, 4>);
+  return launched("k_rows_gemv");
+}
+
+template <bool Q8>
+int rows_gemv(const uint16_t* x, const void* w, const float* scale, int M, int K, int O,
+              uint16_t* y, hipStream_t s) {
+  const int chunks = K / (Q8 ? 16 : 8);
+  ESC_REQUIRE(K > 0 && K % (Q8 ? 16 : 8) == 0 &&
+                  (chunks == 32 || chunks == 64 || chunks == 128 || chunks == 256),
+              "K=%d: need %s", K, Q8 ? "512, 1024, 2048 or 4096" : "256, 512, 1024 or 2048");
+  for (int m0 = 0; m0 < M; m0 += 8) {
+    const int mr = std::min(8, M - m0);
+    const uint16_t* xm = x + (size_t)m0 * K;
+    uint16_t* ym = y + (size_t)m0 * O;
+    int rc;
+    if (mr == 1) rc = rows_gemv_nr<Q8, 1>(xm, w, scale, mr, K, O, ym, s);
+    else if (mr == 2) rc = rows_gemv_nr<Q8, 2>(xm, w, scale, mr, K, O, ym, s);
+    else if (mr <= 4) rc = rows_gemv_nr<Q8, 4>(xm, w, scale, mr, K, O, ym, s);
+    else rc = rows_gemv_nr<Q8, 8>(xm, w, scale, mr, K, O, ym, s);
+    if (rc) return rc;
+  }
+  return ESC_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int esc_w8a16(const uint16_t* x, const int8_t* w8, const float* scale, int M, int K, int O,
+              uint16_t* y, void* stream) {
+  ESC_REQUIRE(x && w8 && scale && y, "null pointer");
+  ESC_REQUIRE(M >= 0 && O > 0, "bad M=%d / O=%d", M, O);
+  if (M == 0) return ESC_OK;
+  return rows_gemv<true>(x, w8, scale, M, K, O, y, S(stream));
+}
+
+int esc_gemv_f16w(const uint16_t* x, const uint16_t* w, int M, int K, int O, uint16_t* y,
+                  void* stream) {
+  ESC_REQUIRE(x && w && y, "null pointer");
+  ESC_REQUIRE(M >= 0 && O > 0, "bad M=%d / O=%d", M, O);
+  if (M == 0) return ESC_OK;
+  return rows_gemv<false>(x, w, nullptr, M, K, O, y, S(stream));
+}
+
+int esc_moe_shared_act(const uint16_t* g, const uint16_t* u, int m, int I, uint16_t* hh,
+                       void* stream) {
+  ESC_REQUIRE(g && u && hh, "null pointer");
+  ESC_REQUIRE(m >= 0 && I > 0, "bad m=%d / I=%d", m, I);
+  if (m == 0) return ESC_OK;
+  hipLaunchKernelGGL(esc::k_shared_act, dim3((I + 255) / 256, m), dim3(256), 0, S(stream), g, u,
+                     I, hh);
+  return launched("k_shared_act");
+}
+
+int esc_moe_block_out(const uint16_t* y, const uint16_t* sh, const uint16_t* shg, int m, int H,
+                      uint16_t* out, void* stream) {
+  ESC_REQUIRE(y && sh && shg && out, "null pointer");
+  ESC_REQUIRE(m >= 0 && H > 0, "bad m=%d / H=%d", m, H);
+  if (m == 0) return ESC_OK;
+  hipLaunchKernelGGL(esc::k_block_out, dim3((H + 255) / 256, m), dim3(256), 0, S(stream), y, sh,
+                     shg, H, out);
+  return launched("k_block_out");
 }
 
 }  // extern "C"

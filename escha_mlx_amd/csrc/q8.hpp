@@ -1,0 +1,178 @@
+// Dense int8 / f16 GEMV around the routed experts: the w8a16 linears of the
+// shared expert and the vocabulary head (escha_mlx/quant.py:1-30, contract
+// wf = f16(f32(w8) * f32(scale)), y = f16(f32-accumulated x @ wf^T); CPU
+// statement ref.w8a16, escha_mlx/ref.py:308-311), and the f16 router /
+// shared-expert gates (y = f16(x @ w^T), escha_mlx/models/qwen3_5_moe.py:257-273).
+//
+// Weights are [O][K] row-major (one output channel per row), read once from
+// HBM with 16-byte loads: LPR = min(64, K/16) lanes share a row, each owning
+// CPL = K/16/LPR 16-byte chunks of it, so a wave-step covers 64/LPR rows.  The
+// lane's inputs for its chunks (NR rows of x) stay in VGPRs for the whole
+// launch; the rows' partial sums meet through lane exchanges (DPP / permlane).
+// Each weight is rounded exactly as the contract says (int8 -> f32, one fma
+// with the row scale, RNE to f16) before the f16 x f16 products, which
+// v_dot2c_f32_f16 sums in float32 (tolerance contract: reassociated sum).
+#pragma once
+
+#include "basic.hpp"
+#include "fast.hpp"
+
+namespace esc {
+
+// partial sum of the lanes of one row group (LPR lanes, LPR a power of two)
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+  if constexpr (LPR >= 2) v = v + lane_xor<1>(v);
+  if constexpr (LPR >= 4) v = v + lane_xor<2>(v);
+  if constexpr (LPR >= 8) v = v + lane_xor<4>(v);
+  if constexpr (LPR >= 16) v = v + lane_xor<8>(v);
+  if constexpr (LPR >= 32) {
+    const unsigned x = __builtin_bit_cast(unsigned, v);
+    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    const unsigned lo = p[0], hi = p[1];
+    v = __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
+  }
+  if constexpr (LPR >= 64) {
+    const unsigned x = __builtin_bit_cast(unsigned, v);
+    const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    const unsigned lo = p[0], hi = p[1];
+    v = __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
+  }
+  return v;
+}
+
+// 4 int8 weights (one word) -> two packed f16 pairs per the w8a16 contract:
+// f32(w8) * f32(scale), RNE to f16.  q = w8 ^ 0x80 is the unsigned byte w8 + 128,
+// and fma(q, s, -128 s) rounds the exact (q - 128) * s once, as the product does.
+__device__ __forceinline__ void w8_to_f16x4(uint32_t w, float s, float ms, uint32_t& p0,
+                                            uint32_t& p1) {
+  const uint32_t q = w ^ 0x80808080u;
+  const float f0 = __builtin_fmaf((float)(q & 0xFFu), s, ms);
+  const float f1 = __builtin_fmaf((float)((q >> 8) & 0xFFu), s, ms);
+  const float f2 = __builtin_fmaf((float)((q >> 16) & 0xFFu), s, ms);
+  const float f3 = __builtin_fmaf((float)(q >> 24), s, ms);
+  p0 = pack2(to_f16(f0), to_f16(f1));
+  p1 = pack2(to_f16(f2), to_f16(f3));
+}
+
+// y[m][o] (ldy between rows) for m < M <= NR.  Q8: w is int8 [O][K] with
+// scale [O]; otherwise w is f16 [O][K] and scale unused.  K = 16-byte chunks
+// x LPR x CPL.  grid: any; block 256.
+template <bool Q8, int NR, int LPR, int CPL>
+__global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ x,
+                                                   const void* __restrict__ wv,
+                                                   const float* __restrict__ scale, int M, int K,
+                                                   int O, uint16_t* __restrict__ y, int ldy) {
+  constexpr int RPS = 64 / LPR;                  // rows per wave-step
+  constexpr int WB = Q8 ? 1 : 2;                 // bytes per weight
+  constexpr int CW = 16 / WB;                    // weights per 16-byte chunk
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = lane % LPR, rsel = lane / LPR;
+  // the lane's inputs: NR rows x CPL chunks x CW halves, as f16 pairs
+  uint32_t xr[NR][CPL][CW / 2];
+#pragma unroll
+  for (int m = 0; m < NR; ++m)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+      for (int i = 0; i < CW / 2; ++i) xr[m][j][i] = 0u;
+#pragma unroll
+  for (int m = 0; m < NR; ++m) {
+    if (m >= M) break;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const uint16_t* xp = x + (size_t)m * K + (size_t)(sub + LPR * j) * CW;
+#pragma unroll
+      for (int i = 0; i < CW / 8; ++i) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xp + 8 * i);
+        xr[m][j][4 * i] = v.x;
+        xr[m][j][4 * i + 1] = v.y;
+        xr[m][j][4 * i + 2] = v.z;
+        xr[m][j][4 * i + 3] = v.w;
+      }
+    }
+  }
+  const uint8_t* w8 = reinterpret_cast<const uint8_t*>(wv);
+  const int nwaves = gridDim.x * 4;
+  const int steps = (O + RPS - 1) / RPS;
+  // the weights (and scale) of the wave's next step are requested before the
+  // current step is converted and multiplied
+  auto load_step = [&](int st, uint4* wc, float& s) {
+    const int oc = min(st * RPS + rsel, O - 1);  // in-bounds reads for a partial last step
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      wc[j] = *reinterpret_cast<const uint4*>(w8 + ((size_t)oc * K + (size_t)(sub + LPR * j) * CW) * WB);
+    if constexpr (Q8) s = scale[oc];
+  };
+  int st = blockIdx.x * 4 + wave;
+  uint4 wn[CPL];
+  float sn = 0.f;
+  if (st < steps) load_step(st, wn, sn);
+  for (; st < steps; st += nwaves) {
+    const int o = st * RPS + rsel;
+    const bool ok = o < O;
+    uint4 wc[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) wc[j] = wn[j];
+    const float s = sn, ms = -128.f * sn;
+    if (st + nwaves < steps) load_step(st + nwaves, wn, sn);
+    float acc[NR];
+#pragma unroll
+    for (int m = 0; m < NR; ++m) acc[m] = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const uint32_t ww[4] = {wc[j].x, wc[j].y, wc[j].z, wc[j].w};
+      uint32_t wp[CW / 2];
+      if constexpr (Q8) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w8_to_f16x4(ww[i], s, ms, wp[2 * i], wp[2 * i + 1]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wp[i] = ww[i];
+      }
+#pragma unroll
+      for (int m = 0; m < NR; ++m)
+#pragma unroll
+        for (int i = 0; i < CW / 2; ++i) acc[m] = dot2(xr[m][j][i], wp[i], acc[m]);
+    }
+#pragma unroll
+    for (int m = 0; m < NR; ++m) acc[m] = row_sum<LPR>(acc[m]);
+    if (ok && sub == 0) {
+#pragma unroll
+      for (int m = 0; m < NR; ++m)
+        if (m < M) y[(size_t)m * ldy + o] = __builtin_bit_cast(uint16_t, to_f16(acc[m]));
+    }
+  }
+}
+
+// Shared-expert activation (escha_mlx/ref.py:345): hh = f16((g / (1 + exp(-g))) * u)
+// in float32, g and u f16 [m][I].  grid (ceil(I/256), m), block 256.
+__global__ __launch_bounds__(256) void k_shared_act(const uint16_t* __restrict__ g,
+                                                    const uint16_t* __restrict__ u, int I,
+                                                    uint16_t* __restrict__ hh) {
+  const int i = blockIdx.x * 256 + threadIdx.x, row = blockIdx.y;
+  if (i >= I) return;
+  const size_t o = (size_t)row * I + i;
+  const float gf = (float)__builtin_bit_cast(half_t, g[o]);
+  const float uf = (float)__builtin_bit_cast(half_t, u[o]);
+  hh[o] = __builtin_bit_cast(uint16_t, to_f16((gf / (1.0f + expf(-gf))) * uf));
+}
+
+// Block output (escha_mlx/ref.py:346-349, models/qwen3_5_moe.py:270-272):
+// out = f16(f32(y) + f32(sh) * sigmoid(f32(shg))), y the f16 routed sum, sh
+// the shared expert's f16 output, shg [m] the f16 shared gate logit.
+// grid (ceil(H/256), m), block 256.
+__global__ __launch_bounds__(256) void k_block_out(const uint16_t* __restrict__ yr,
+                                                   const uint16_t* __restrict__ sh,
+                                                   const uint16_t* __restrict__ shg, int H,
+                                                   uint16_t* __restrict__ out) {
+  const int c = blockIdx.x * 256 + threadIdx.x, row = blockIdx.y;
+  if (c >= H) return;
+  const size_t o = (size_t)row * H + c;
+  const float sg = 1.0f / (1.0f + expf(-(float)__builtin_bit_cast(half_t, shg[row])));
+  const float v = (float)__builtin_bit_cast(half_t, yr[o]) +
+                  (float)__builtin_bit_cast(half_t, sh[o]) * sg;
+  out[o] = __builtin_bit_cast(uint16_t, to_f16(v));
+}
+
+}  // namespace esc

@@ -153,3 +153,36 @@ class EschaMoEExperts(torch.nn.Module):
         gu, dn = self._gu, self._dn
         return ops.moe_expert_path(x, ids, scores, gu.code, gu.rin, gu.rout, gu.K, dn.code,
                                    dn.rin, dn.rout, dn.K, lut=self._lut, ws=ws)
+
+
+class EschaSparseMoeBlock(torch.nn.Module):
+    """The whole MoE block (models/qwen3_5_moe.py:257-273; ref.moe_block,
+    escha_mlx/ref.py:314-349): router gate (f16 Linear) -> top-k softmax ->
+    routed experts (f16 sum) -> shared expert (w8a16 gate / up, activation,
+    w8a16 down) scaled by sigmoid(shared gate) -> f16.
+
+    gate_w [E, H] f16, experts an ``EschaMoEExperts``, sh_gate / sh_up /
+    sh_down ``quant.EschaQ8Linear``, shg_w [1, H] f16.  The routed sum is
+    rounded to f16 before the shared expert is added (the model's forward
+    contract, models/qwen3_5_moe.py:250-253).
+    """
+
+    def __init__(self, gate_w, experts: EschaMoEExperts, sh_gate, sh_up, sh_down, shg_w,
+                 top_k: int, device="cuda") -> None:
+        super().__init__()
+        as16 = lambda a: (a if torch.is_tensor(a) else torch.from_numpy(np.asarray(a, np.float16))
+                          ).to(device=device, dtype=torch.float16).contiguous()
+        self.gate_w, self.shg_w = as16(gate_w), as16(shg_w)
+        self.experts, self.top_k = experts, top_k
+        self.sh_gate, self.sh_up, self.sh_down = sh_gate, sh_up, sh_down
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape
+        xf = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
+        logits = ops.gemv_f16w(xf, self.gate_w).to(torch.float32)
+        ids, scores = route(logits, self.top_k)
+        y = self.experts(xf, ids, scores)
+        hh = ops.moe_shared_act(self.sh_gate(xf), self.sh_up(xf))
+        sh = self.sh_down(hh)
+        shg = ops.gemv_f16w(xf, self.shg_w)
+        return ops.moe_block_out(y, sh, shg).reshape(shape).to(x.dtype)

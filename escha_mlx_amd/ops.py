@@ -328,6 +328,58 @@ def moe_combine(d16: torch.Tensor, scores: torch.Tensor, top_k: int) -> torch.Te
     return y
 
 
+def w8a16(x: torch.Tensor, w8: torch.Tensor, scale: torch.Tensor,
+          out: torch.Tensor | None = None) -> torch.Tensor:
+    """x f16 [M, K], w8 int8 [O, K], scale f32 [O] -> f16 [M, O]: the w8a16
+    contract wf = f16(f32(w8) * f32(scale)), y = f16(f32-accum x @ wf^T)
+    (escha_mlx/quant.py:1-30, ref.py:308-311)."""
+    _dev(x, w8, scale)
+    if x.dtype != torch.float16 or w8.dtype != torch.int8 or scale.dtype != torch.float32:
+        raise ValueError("x must be float16, w8 int8 and scale float32")
+    m, k = x.shape
+    o = w8.shape[0]
+    if w8.shape != (o, k) or scale.shape != (o,):
+        raise ValueError(f"shapes x {tuple(x.shape)}, w8 {tuple(w8.shape)}, scale {tuple(scale.shape)}")
+    y = out if out is not None else torch.empty((m, o), dtype=torch.float16, device=x.device)
+    _lib.call("esc_w8a16", _ptr(x), _ptr(w8), _ptr(scale), m, k, o, _ptr(y), _stream())
+    return y
+
+
+def gemv_f16w(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x f16 [M, K], w f16 [O, K] -> f16 [M, O] = f16(f32-accum x @ w^T): the
+    router and shared-expert gates (models/qwen3_5_moe.py:259, 271)."""
+    _dev(x, w)
+    if x.dtype != torch.float16 or w.dtype != torch.float16:
+        raise ValueError("x and w must be float16")
+    m, k = x.shape
+    o = w.shape[0]
+    if w.shape != (o, k):
+        raise ValueError(f"shapes x {tuple(x.shape)}, w {tuple(w.shape)}")
+    y = out if out is not None else torch.empty((m, o), dtype=torch.float16, device=x.device)
+    _lib.call("esc_gemv_f16w", _ptr(x), _ptr(w), m, k, o, _ptr(y), _stream())
+    return y
+
+
+def moe_shared_act(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    """f16 [m, I] gate and up -> f16((g / (1 + exp(-g))) * u) (ref.py:345)."""
+    _dev(g, u)
+    m, i = g.shape
+    hh = torch.empty_like(g)
+    _lib.call("esc_moe_shared_act", _ptr(g), _ptr(u), m, i, _ptr(hh), _stream())
+    return hh
+
+
+def moe_block_out(y: torch.Tensor, sh: torch.Tensor, shg: torch.Tensor) -> torch.Tensor:
+    """f16(f32(y) + f32(sh) * sigmoid(f32(shg))) (models/qwen3_5_moe.py:270-272);
+    y, sh f16 [m, H], shg f16 [m, 1] or [m]."""
+    _dev(y, sh, shg)
+    m, h = y.shape
+    out = torch.empty_like(y)
+    _lib.call("esc_moe_block_out", _ptr(y), _ptr(sh), _ptr(shg.contiguous()), m, h, _ptr(out),
+              _stream())
+    return out
+
+
 def moe_status(ws: torch.Tensor, T: int, top_k: int, H: int, I: int) -> int:
     """1 if a one-launch expert path using ``ws`` ever hit its bounded wait (synchronises)."""
     flag = ctypes.c_int32(0)

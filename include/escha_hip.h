@@ -162,6 +162,35 @@ int esc_swiglu(const uint16_t* gu, int m, int I, uint16_t* h, void* stream);
 int esc_moe_combine(const uint16_t* d16, const float* scores, int T, int top_k, int H,
                     uint16_t* y, void* stream);
 
+/* Dense w8a16 linear: y f16 [M][O] = f16(f32-accumulated x @ wf^T) with
+ * wf = f16(f32(w8) * f32(scale)), w8 int8 [O][K] (one output channel per row),
+ * scale f32 [O], x f16 [M][K]; K in {512, 1024, 2048, 4096}.  Each weight is
+ * rounded as the contract states; the float32 sum is reassociated (tolerance
+ * contract, deterministic).  The contract of EschaQ8Linear
+ * (escha_mlx/quant.py:1-30, CPU statement ref.w8a16, escha_mlx/ref.py:308-311):
+ * the shared expert's gate/up/down and the vocabulary head. */
+int esc_w8a16(const uint16_t* x, const int8_t* w8, const float* scale, int M, int K, int O,
+              uint16_t* y, void* stream);
+
+/* f16-weight linear without bias: y f16 [M][O] = f16(f32-accumulated x @ w^T),
+ * w f16 [O][K], K in {256, 512, 1024, 2048}.  The router gate and the shared
+ * expert gate of the MoE block (escha_mlx/models/qwen3_5_moe.py:259, 271;
+ * ref.moe_block, escha_mlx/ref.py:324, 347). */
+int esc_gemv_f16w(const uint16_t* x, const uint16_t* w, int M, int K, int O, uint16_t* y,
+                  void* stream);
+
+/* Shared-expert activation: hh f16 [m][I] = f16((g / (1 + exp(-g))) * u) in
+ * float32 from the f16 gate and up outputs (escha_mlx/ref.py:345,
+ * models/qwen3_5_moe.py:268). */
+int esc_moe_shared_act(const uint16_t* g, const uint16_t* u, int m, int I, uint16_t* hh,
+                       void* stream);
+
+/* MoE block output: out f16 [m][H] = f16(f32(y) + f32(sh) * sigmoid(f32(shg))),
+ * y the f16 routed sum, sh f16 [m][H] the shared expert's output, shg f16 [m]
+ * the shared-expert gate logit (models/qwen3_5_moe.py:250-253, 270-272). */
+int esc_moe_block_out(const uint16_t* y, const uint16_t* sh, const uint16_t* shg, int m, int H,
+                      uint16_t* out, void* stream);
+
 /* Routed-expert path for T tokens: y f16 [T][H] = f16(sum over the k slots,
  * in slot order, of f32(d16) * f32(f16(score))), where per (token, slot):
  * gate_up linear (H -> 2I, K_gu) -> swiglu -> down linear (I -> H, K_dn).

@@ -34,6 +34,12 @@ Pinning status of each function (what checks it independently of its own code):
                    (tests/test_blocked.py:25-66 of the reference).
   moe_routed       pinned by composition of the above; f64 variant checked
                    against vectors from ref.moe_block's routed sum.
+  w8a16            pinned: the reference's w8a16 goldens (tests/data/codec/
+                   w8a16_*, tolerance: float32 sum order) and one-hot inputs
+                   (each output is one contract weight f16(f32(w8)*f32(scale))).
+  linear_f16,      pinned: vectors from ref.moe_block with a non-zero shared
+  shared_act,      expert and router (tests/golden/make_ref_vectors.py),
+  moe_block        tolerance (numpy BLAS order, f64 routed sum).
 """
 from __future__ import annotations
 
@@ -314,3 +320,64 @@ def moe_routed(x, ids, scores, gu, dn, K_gu, K_dn, ordered=True, acc64=False):
             c = d[0].astype(np.float32) * w16
             out[ti] = out[ti] + (c.astype(np.float64) if acc64 else c)
     return out.astype(np.float16)
+
+
+# ---------------------------------------------------------------- dense int8 / full MoE block
+
+def w8a16(x: np.ndarray, w8: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """y = f16(f32(x) @ f32(wf)^T), wf = f16(f32(w8) * f32(scale)); w8 [O, K]
+    int8, scale [O] (escha_mlx/ref.py:308-311, quant.py:1-30)."""
+    wf = (w8.astype(np.float32) * np.asarray(scale, np.float32)[:, None]).astype(np.float16)
+    return (x.astype(np.float32) @ wf.astype(np.float32).T).astype(np.float16)
+
+
+def linear_f16(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """A bias-free f16 Linear: f16(f32(x) @ f32(w)^T) (the router and shared
+    gates, escha_mlx/ref.py:324, 347)."""
+    return (x.astype(np.float32) @ w.astype(np.float32).T).astype(np.float16)
+
+
+def shared_act(g16: np.ndarray, u16: np.ndarray) -> np.ndarray:
+    """f16((g / (1 + exp(-g))) * u) in float32 (escha_mlx/ref.py:345)."""
+    g = g16.astype(np.float32)
+    return ((g / (np.float32(1.0) + np.exp(-g))) * u16.astype(np.float32)).astype(np.float16)
+
+
+def moe_block(x, w, top_k, ids=None, scores=None, K_gu=2, K_dn=3, routed_f16=True):
+    """Full MoE block (escha_mlx/ref.py:314-349; models/qwen3_5_moe.py:257-273).
+
+    w: gate_w [E, H] f16; gu / dn dicts as in moe_routed; sh_{gate,up,down}_w8 /
+    _scale; shg_w [1, H] f16.  Router: f16-rounded logits, top-k (stable),
+    softmax over the k values; ids/scores may be injected.  routed_f16 rounds
+    the routed sum to f16 before the shared expert is added (the model's
+    forward contract, models/qwen3_5_moe.py:250-253); False keeps
+    ref.moe_block's float64 routed sum.
+    """
+    logits = linear_f16(x, w["gate_w"]).astype(np.float32)
+    if ids is None:
+        ids, scores = route_topk(logits, top_k)
+    if routed_f16:
+        y = moe_routed(x, ids, scores, w["gu"], w["dn"], K_gu, K_dn, ordered=False).astype(np.float32)
+    else:
+        y = _routed_f64(x, ids, scores, w["gu"], w["dn"], K_gu, K_dn)
+    g = w8a16(x, w["sh_gate_w8"], w["sh_gate_scale"])
+    u = w8a16(x, w["sh_up_w8"], w["sh_up_scale"])
+    hh = shared_act(g, u)
+    sh = w8a16(hh, w["sh_down_w8"], w["sh_down_scale"]).astype(np.float32)
+    shg = linear_f16(x, w["shg_w"]).astype(np.float32)
+    sgate = np.float32(1.0) / (np.float32(1.0) + np.exp(-shg))
+    return (y + sh * sgate).astype(np.float16)
+
+
+def _routed_f64(x, ids, scores, gu, dn, K_gu, K_dn):
+    t, k = ids.shape
+    out = np.zeros((t, x.shape[1]), dtype=np.float64)
+    for ti in range(t):
+        for s in range(k):
+            e = int(ids[ti, s])
+            h = expert_linear(x[ti:ti + 1], None, gu["rin"][e], gu["rout"][e], K_gu,
+                              w_bare=gu["w"][e])
+            h = swiglu(h)
+            d = expert_linear(h, None, dn["rin"][e], dn["rout"][e], K_dn, w_bare=dn["w"][e])
+            out[ti] += (d[0].astype(np.float32) * np.float32(np.float16(scores[ti, s]))).astype(np.float64)
+    return out

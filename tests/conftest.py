@@ -85,3 +85,32 @@ def dense_linear_golden(request):
 def ref_vectors():
     with np.load(GOLDEN / "ref_vectors.npz") as z:
         return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope="session")
+def w8a16_golden(digests):
+    """The reference's w8a16 golden (reference tests/data/codec/w8a16_*), cut to
+    its first output channels: w8 [n, 2048] int8, scale [n] f32, x [8, 2048]
+    f16, expected [8, n] f16."""
+    n = digests["w8a16_w8_2048x2048.i8"]["kept_output_channels"]
+    w8 = np.fromfile(CODEC / f"w8a16_w8_{n}x2048.i8", dtype=np.int8).reshape(n, 2048)
+    scale = np.fromfile(CODEC / f"w8a16_scale_{n}.f32", dtype=np.float32)
+    x = np.fromfile(CODEC / "w8a16_x_8x2048.f16", dtype=np.float16).reshape(8, 2048)
+    want = np.fromfile(CODEC / f"w8a16_expected_8x{n}.f16", dtype=np.float16).reshape(8, n)
+    return w8, scale, x, want
+
+
+def moe_block_weights(v, prefix="blk_"):
+    """The full-block weights of a ref_vectors set as oracle.moe_block takes them."""
+    from oracle import ref_np as R
+    E, H = v[prefix + "gate_w"].shape
+    I = v[prefix + "gu_rout"].shape[1] // 2
+    gu = {"w": np.stack([R.reconstruct(v[prefix + "gu_code"][e], H, 2 * I, 2) for e in range(E)]),
+          "rin": v[prefix + "gu_rin"], "rout": v[prefix + "gu_rout"]}
+    dn = {"w": np.stack([R.reconstruct(v[prefix + "dn_code"][e], I, H, 3) for e in range(E)]),
+          "rin": v[prefix + "dn_rin"], "rout": v[prefix + "dn_rout"]}
+    w = {"gate_w": v[prefix + "gate_w"], "gu": gu, "dn": dn, "shg_w": v[prefix + "shg_w"]}
+    for k in ("sh_gate_w8", "sh_gate_scale", "sh_up_w8", "sh_up_scale", "sh_down_w8",
+              "sh_down_scale"):
+        w[k] = v[prefix + k]
+    return w

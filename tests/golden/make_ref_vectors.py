@@ -2,7 +2,8 @@
 
 Only for the functions that the goldens and closed forms leave open at the bit
 level: the H128 butterfly's float32 rounding order, the two transforms, swiglu
-(numpy exp), the router softmax, and the routed MoE sum in float64.  The decode
+(numpy exp), the router softmax, the routed MoE sum in float64, and the full
+MoE block (router gate, int8 shared expert, sigmoid gate).  The decode
 itself is pinned by the committed goldens and is NOT generated here.
 
 Runs in the build container only (it loads /root/reference/escha_mlx/ref.py by
@@ -94,6 +95,31 @@ def main() -> None:
     e = np.exp(top - top.max(axis=-1, keepdims=True))
     v["route_logits"], v["route_ids"] = lg, ids.astype(np.int32)
     v["route_scores"] = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+
+    # full MoE block: router gate, routed experts, a non-zero int8 shared
+    # expert and its sigmoid gate (ref.moe_block end to end)
+    E, H, I, Ish, k, T = 8, 512, 128, 512, 2, 3
+    wb = {
+        "gate_w": (rng.standard_normal((E, H)) * 0.05).astype(np.float16),
+        "gu_code": rng.integers(-32768, 32768, size=(E, H // 16, 2 * I // 16, 32), dtype=np.int16),
+        "gu_rin": rng.choice([-1.0, 1.0], (E, H)).astype(np.float16),
+        "gu_rout": (rng.choice([-1.0, 1.0], (E, 2 * I)) * 0.01).astype(np.float16),
+        "dn_code": rng.integers(-32768, 32768, size=(E, I // 16, H // 16, 48), dtype=np.int16),
+        "dn_rin": rng.choice([-1.0, 1.0], (E, I)).astype(np.float16),
+        "dn_rout": (rng.choice([-1.0, 1.0], (E, H)) * 0.01).astype(np.float16),
+        "sh_gate_w8": rng.integers(-128, 128, size=(Ish, H), dtype=np.int8),
+        "sh_gate_scale": rng.uniform(1e-3, 4e-3, Ish).astype(np.float16).astype(np.float32),
+        "sh_up_w8": rng.integers(-128, 128, size=(Ish, H), dtype=np.int8),
+        "sh_up_scale": rng.uniform(1e-3, 4e-3, Ish).astype(np.float16).astype(np.float32),
+        "sh_down_w8": rng.integers(-128, 128, size=(H, Ish), dtype=np.int8),
+        "sh_down_scale": rng.uniform(1e-4, 4e-4, H).astype(np.float16).astype(np.float32),
+        "shg_w": (rng.standard_normal((1, H)) * 0.05).astype(np.float16),
+    }
+    xb = rng.standard_normal((T, H)).astype(np.float16)
+    v["blk_x"] = xb
+    v["blk_y"] = ref.moe_block(xb, wb, top_k=k)
+    for key, val in wb.items():
+        v["blk_" + key] = val
 
     np.savez_compressed(OUT, **v)
     print("wrote", OUT, sorted(v))

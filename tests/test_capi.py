@@ -191,3 +191,20 @@ def test_experts_container_validation():
     ex = moe.EschaExperts(np.zeros((2, 8, 16, 32), np.int16), np.ones((2, 128)),
                           np.ones((2, 256)), device="cpu")
     assert (ex.E, ex.IC, ex.OC, ex.K) == (2, 128, 256, 2)
+
+
+@pytest.mark.parametrize("fn,K", [("esc_w8a16", 640), ("esc_w8a16", 256), ("esc_gemv_f16w", 128),
+                                  ("esc_gemv_f16w", 4096)])
+def test_dense_gemv_rejects_unsupported_K(fn, K):
+    if fn == "esc_w8a16":
+        rc, msg = _rc_msg(fn, DUMMY, DUMMY, DUMMY, 1, K, 256, DUMMY, None)
+    else:
+        rc, msg = _rc_msg(fn, DUMMY, DUMMY, 1, K, 256, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and f"K={K}" in msg
+
+
+def test_w8a16_rejects_null_and_bad_sizes():
+    rc, msg = _rc_msg("esc_w8a16", None, DUMMY, DUMMY, 1, 2048, 256, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "null" in msg
+    rc, msg = _rc_msg("esc_w8a16", DUMMY, DUMMY, DUMMY, 1, 2048, 0, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "O=0" in msg

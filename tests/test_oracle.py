@@ -15,7 +15,7 @@ from scipy.linalg import hadamard
 
 from oracle import ref_np as R
 
-from .conftest import sha256
+from .conftest import moe_block_weights, sha256
 
 
 # ---------------------------------------------------------------- codebook
@@ -293,3 +293,43 @@ def test_build_groups_model(m, E, R_):
         occ = blk[blk < m]
         if len(occ):
             assert (re[occ] == b[g]).all()
+
+
+def test_w8a16_vs_reference_golden(w8a16_golden):
+    """The contract's weights f16(f32(w8) * f32(scale)) through a float32 matmul
+    agree with the reference's w8a16 golden to its own bar (reference
+    tests/test_mlx_cpu.py:55-65: max |diff| / max |want| < 2e-3); the shipped
+    outputs are float32 sums in another order, so a few differ by an ulp."""
+    w8, scale, x, want = w8a16_golden
+    got = R.w8a16(x, w8, scale).astype(np.float32)
+    w = want.astype(np.float32)
+    assert np.abs(got - w).max() / np.abs(w).max() < 2e-3
+    assert (got != w).mean() < 0.05
+
+
+def test_w8a16_one_hot_reads_contract_weights(w8a16_golden):
+    """x = e_k gives y[:, o] = f16(f32(w8[o, k]) * f32(scale[o])) exactly."""
+    w8, scale, _, _ = w8a16_golden
+    ks = np.array([0, 7, 1000, 2047])
+    x = np.zeros((len(ks), 2048), np.float16)
+    x[np.arange(len(ks)), ks] = 1.0
+    got = R.w8a16(x, w8, scale)
+    for i, k in enumerate(ks):
+        want = (np.float32(1.0) * (w8[:, k].astype(np.float32) * scale)).astype(np.float16)
+        assert np.array_equal(got[i].view(np.uint16), want.view(np.uint16))
+
+
+def test_moe_block_vs_reference_moe_block(ref_vectors):
+    """The full block (router gate, routed experts, int8 shared expert, sigmoid
+    gate) against ref.moe_block: with its float64 routed sum, within an f16
+    ulp; with the model's f16 rounding of the routed sum
+    (models/qwen3_5_moe.py:250-253), within the f16 tolerance of that extra
+    rounding."""
+    v = ref_vectors
+    w = moe_block_weights(v)
+    want = v["blk_y"].astype(np.float32)
+    scale = np.abs(want).max()
+    got64 = R.moe_block(v["blk_x"], w, 2, routed_f16=False).astype(np.float32)
+    assert np.abs(got64 - want).max() <= scale * 2 ** -10
+    got16 = R.moe_block(v["blk_x"], w, 2).astype(np.float32)
+    assert np.abs(got16 - want).max() <= scale * 2 ** -8
