@@ -63,7 +63,8 @@ def parse():
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 PMC passes")
     ap.add_argument("--only", choices=["both", "sustained", "chained"], default="both")
     ap.add_argument("--probe", action="store_true",
-                    help="run the calibration copy and two sustained calls, untimed (for PMC)")
+                    help="run the calibration copy and two sustained calls (config 6: two head "
+                         "calls), untimed, as the PMC target")
     ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5, 6], default=3,
                     help="BASELINE config; 3 (the headline metric) by default; 6 is not a "
                          "BASELINE config: the w8a16 vocabulary-head GEMV around the MoE block")
@@ -170,10 +171,10 @@ def _counter_rows(path: Path):
     return per
 
 
-def measure_traffic(layers: int):
-    """HBM bytes per sustained call, from FETCH_SIZE and WRITE_SIZE passes of
-    rocprofv3 over `bench.py --probe`, each calibrated by the 1 GiB copy the
-    probe runs first.  Runs before this process touches the GPU."""
+def measure_traffic(probe_args: list, kernels=KERNELS):
+    """HBM bytes per call of `kernels` (summed), from FETCH_SIZE and WRITE_SIZE
+    passes of rocprofv3 over `bench.py --probe <probe_args>`, each calibrated by
+    the 1 GiB copy the probe runs first.  Runs before this process touches the GPU."""
     exe = shutil.which("rocprofv3")
     if exe is None:
         return None, "rocprofv3 not found"
@@ -181,7 +182,7 @@ def measure_traffic(layers: int):
     with tempfile.TemporaryDirectory(dir="/tmp") as d:
         for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
             cmd = [exe, "--pmc", ctr, "--output-format", "csv", "-d", d, "-o", ctr, "--",
-                   sys.executable, str(ROOT / "bench.py"), "--probe", "--layers", str(layers)]
+                   sys.executable, str(ROOT / "bench.py"), "--probe", *probe_args]
             try:
                 subprocess.run(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"),
                                stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=240,
@@ -191,7 +192,7 @@ def measure_traffic(layers: int):
             per = _counter_rows(Path(d) / f"{ctr}_counter_collection.csv")
             copy = max(v for k, vals in per.items() if "copyBuffer" in k for v in vals)
             factor = COPY_BYTES / (copy * 1024.0)
-            for kname in KERNELS:
+            for kname in kernels:
                 vals = [v for k, vv in per.items() if kname in k for v in vv]
                 if not vals:
                     return None, f"no {kname} dispatch in the {ctr} pass"
@@ -203,16 +204,21 @@ def measure_traffic(layers: int):
     return int(total), detail
 
 
-def probe(torch, args):
-    """Calibration copy, then two sustained calls (PMC target)."""
-    from escha_mlx_amd import ops
-    dev = "cuda:0"
-    ops.init()
+def calibration_copy(torch, dev):
+    """The plain device copy of COPY_BYTES that scales the PMC byte counters."""
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
+
+
+def probe(torch, args):
+    """Calibration copy, then two sustained calls (PMC target)."""
+    from escha_mlx_amd import ops
+    dev = "cuda:0"
+    ops.init()
+    calibration_copy(torch, dev)
     layers = make_layers(torch, args.layers, dev)
     routes = route_sets(torch, layers)
     ws = torch.zeros(ops.moe_layers_workspace(args.layers, 1, TOP_K, H, I), dtype=torch.uint8,
@@ -442,18 +448,41 @@ def bench_c4(args, torch, ops):
             "distinct_experts_per_layer": distinct, "tok_s_per_layer": round(T / (ms * 1e-3), 1)}
 
 
+Q8_HEAD_O, Q8_HEAD_K = 248320, 2048
+Q8_HEAD_KERNEL = "k_rows_gemv"
+
+
+def _q8_head_weights(torch, dev):
+    """2 independent 248320 x 2048 int8 heads + scales (2 x 509 MB, rotated:
+    beyond the 256 MB Infinity Cache)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    w8 = [torch.randint(-128, 128, (Q8_HEAD_O, Q8_HEAD_K), dtype=torch.int8, device=dev,
+                        generator=g) for _ in range(2)]
+    sc = [torch.rand(Q8_HEAD_O, generator=g, device=dev) * 4e-3 + 1e-3 for _ in range(2)]
+    return g, w8, sc
+
+
+def probe_q8_head(torch, ops):
+    """Calibration copy, then one batch-1 head call on each weight copy (PMC target)."""
+    dev = "cuda:0"
+    calibration_copy(torch, dev)
+    g, w8, sc = _q8_head_weights(torch, dev)
+    x = torch.randn(1, Q8_HEAD_K, generator=g, device=dev).half()
+    for i in range(len(w8)):
+        ops.w8a16(x, w8[i], sc[i])
+    torch.cuda.synchronize()
+    print(f"probe: copy {COPY_BYTES} B, {len(w8)} head calls", flush=True)
+
+
 def bench_q8_head(args, torch, ops):
     """Not a BASELINE config: the int8 vocabulary head of the 35B model
     (248,320 x 2048 w8a16, the reference's lm_head bench shape,
     bench/results/m5-pro-24gb/roofline.json:15-24) at batch 1 and 8."""
     dev = "cuda:0"
-    g = torch.Generator(device=dev)
-    g.manual_seed(6)
     stream = torch.cuda.current_stream()
-    O, K, copies = 248320, 2048, 2   # 2 x 509 MB rotated: beyond the 256 MB Infinity Cache
-    w8 = [torch.randint(-128, 128, (O, K), dtype=torch.int8, device=dev, generator=g)
-          for _ in range(copies)]
-    sc = [torch.rand(O, generator=g, device=dev) * 4e-3 + 1e-3 for _ in range(copies)]
+    g, w8, sc = _q8_head_weights(torch, dev)
+    O, K, copies = Q8_HEAD_O, Q8_HEAD_K, len(w8)
     nbytes = O * K + O * 4
     per = {}
     for M in (1, 8):
@@ -478,12 +507,36 @@ def bench_q8_head(args, torch, ops):
             **per}
 
 
+def run_q8_head(args):
+    """Config 6: live HBM traffic first (before this process touches the GPU), then the line."""
+    traffic, detail = None, "not measured (--no-traffic)"
+    if not args.probe and not args.no_traffic:
+        traffic, detail = measure_traffic(["--config", "6"], (Q8_HEAD_KERNEL,))
+    import torch
+
+    from escha_mlx_amd import ops
+    torch.cuda.set_device(0)
+    ops.init()
+    if args.probe:
+        probe_q8_head(torch, ops)
+        return None
+    res = bench_q8_head(args, torch, ops)
+    res["roofline"]["traffic"] = traffic
+    res["roofline"]["traffic_detail"] = detail
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus N>1 is not supported "
                                    "(the sharding design is described, not built)"}))
         sys.exit(2)
+    if args.config == 6:
+        res = run_q8_head(args)
+        if res is not None:
+            print(json.dumps(res))
+        return
     if args.config != 3:
         import torch
 
@@ -492,15 +545,13 @@ def main():
         ops.init()
         if args.config == 4:
             res = bench_c4(args, torch, ops)
-        elif args.config == 6:
-            res = bench_q8_head(args, torch, ops)
         else:
             res = bench_dense(args, torch, ops, args.config)
         print(json.dumps(res))
         return
     traffic, traffic_detail = None, "not measured (--no-traffic)"
     if not args.probe and not args.no_traffic and args.only != "chained":
-        traffic, traffic_detail = measure_traffic(args.layers)
+        traffic, traffic_detail = measure_traffic(["--layers", str(args.layers)])
     import torch
 
     if args.probe:

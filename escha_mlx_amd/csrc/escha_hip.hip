@@ -583,9 +583,10 @@ int rows_gemv_nr(const uint16_t* x, const void* w, const float* scale, int M, in
   const int chunks = K / (Q8 ? 16 : 8);
   const int lpr = chunks >= 64 ? 64 : 32, cpl = chunks / lpr;
   const long steps = ((long)O + 64 / lpr - 1) / (64 / lpr);
-  // four workgroups per CU, each wave striding over the row steps (measured
-  // on MI355X: 1024 workgroups stream the 248320 x 2048 head fastest)
-  const int blocks = (int)std::min<long>((steps + 3) / 4, 4L * device_cus());
+  // eight workgroups per CU, each wave striding over the row steps (measured
+  // on MI355X with the 248320 x 2048 head: 103 us at 8 per CU, 107 us at 4,
+  // 16 no better than 8)
+  const int blocks = (int)std::min<long>((steps + 3) / 4, 8L * device_cus());
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, x, w, scale, M, K, O, y, O);
   };
