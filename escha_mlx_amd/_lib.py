@@ -52,6 +52,7 @@ SIGNATURES = {
     "esc_gemv_f16w": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "esc_moe_shared_act": (_I, [_P, _P, _I, _I, _P, _P]),
     "esc_moe_block_out": (_I, [_P, _P, _P, _I, _I, _P, _P]),
+    "esc_q8_embed": (_I, [_P, _I, _P, _P, _I, _I, _P, _P]),
     "esc_moe_expert_path_workspace": (_Z, [_I, _I, _I, _I, _I]),
     "esc_moe_status": (_I, [_P, _Z, _I, _I, _I, _I, _P, _P]),
     "esc_moe_layers_workspace": (_Z, [_I, _I, _I, _I, _I]),

@@ -576,43 +576,84 @@ int esc_moe_combine(const uint16_t* d16, const float* scores, int T, int top_k, 
 }  // extern "C"
 
 namespace {
-// one launch of k_rows_gemv for up to 8 rows of x
+// k_rows_gemv geometry: LPR lanes per output row (the row's 16-byte chunk
+// count rounded up to a power of two, 8..64), CPL chunks per lane (1..8).
+// The lanes keep NR rows of x in registers, NR * CPL * XW words (XW = 8 f16
+// pairs per int8 chunk, 4 per f16 chunk): rows per launch are capped at 128
+// such words.
+constexpr int kRowsXWords = 128;
+constexpr int kRowsMaxCpl = 8;
+
+struct RowsGeo {
+  int lpr, cpl;
+};
+RowsGeo rows_geo(int chunks) {
+  int lpr = 8;
+  while (lpr < chunks && lpr < 64) lpr *= 2;
+  return {lpr, (chunks + lpr - 1) / lpr};
+}
+constexpr int rows_x_words(bool q8) { return q8 ? 8 : 4; }
+int rows_nr_max(bool q8, int cpl) {
+  int nr = 8;
+  while (nr > 1 && nr * cpl * rows_x_words(q8) > kRowsXWords) nr /= 2;
+  return nr;
+}
+
+template <bool Q8, int NR, int LPR, int CPL>
+int rows_launch(const uint16_t* x, const void* w, const float* scale, int M, int K, int O,
+                uint16_t* y, hipStream_t s) {
+  if constexpr (NR * CPL * rows_x_words(Q8) > kRowsXWords) {
+    return fail(ESC_EINVAL, "internal: %d rows x %d chunks exceed the register budget", NR, CPL);
+  } else {
+    const long steps = ((long)O + 64 / LPR - 1) / (64 / LPR);
+    // eight workgroups per CU, each wave striding over the row steps (measured
+    // on MI355X with the 248320 x 2048 head: 103 us at 8 per CU, 107 us at 4,
+    // 16 no better than 8)
+    const int blocks = (int)std::min<long>((steps + 3) / 4, 8L * device_cus());
+    hipLaunchKernelGGL((esc::k_rows_gemv<Q8, NR, LPR, CPL>), dim3(blocks), dim3(256), 0, s, x, w,
+                       scale, M, K, O, y, O);
+    return launched("k_rows_gemv");
+  }
+}
+
 template <bool Q8, int NR>
-int rows_gemv_nr(const uint16_t* x, const void* w, const float* scale, int M, int K, int O,
-                 uint16_t* y, hipStream_t s) {
-  const int chunks = K / (Q8 ? 16 : 8);
-  const int lpr = chunks >= 64 ? 64 : 32, cpl = chunks / lpr;
-  const long steps = ((long)O + 64 / lpr - 1) / (64 / lpr);
-  // eight workgroups per CU, each wave striding over the row steps (measured
-  // on MI355X with the 248320 x 2048 head: 103 us at 8 per CU, 107 us at 4,
-  // 16 no better than 8)
-  const int blocks = (int)std::min<long>((steps + 3) / 4, 8L * device_cus());
-  auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, s, x, w, scale, M, K, O, y, O);
-  };
-  if (lpr == 32) go(esc::k_rows_gemv<Q8, NR, 32, 1>);
-  else if (cpl == 1) go(esc::k_rows_gemv<Q8, NR, 64, 1>);
-  else if (cpl == 2) go(esc::k_rows_gemv<Q8, NR, 64, 2>);
-  else go(esc::k_rows_gemv<Q8, NR, 64, 4>);
-  return launched("k_rows_gemv");
+int rows_by_geo(RowsGeo g, const uint16_t* x, const void* w, const float* scale, int M, int K,
+                int O, uint16_t* y, hipStream_t s) {
+  switch (g.lpr) {
+    case 8: return rows_launch<Q8, NR, 8, 1>(x, w, scale, M, K, O, y, s);
+    case 16: return rows_launch<Q8, NR, 16, 1>(x, w, scale, M, K, O, y, s);
+    case 32: return rows_launch<Q8, NR, 32, 1>(x, w, scale, M, K, O, y, s);
+  }
+  switch (g.cpl) {
+    case 1: return rows_launch<Q8, NR, 64, 1>(x, w, scale, M, K, O, y, s);
+    case 2: return rows_launch<Q8, NR, 64, 2>(x, w, scale, M, K, O, y, s);
+    case 3: return rows_launch<Q8, NR, 64, 3>(x, w, scale, M, K, O, y, s);
+    case 4: return rows_launch<Q8, NR, 64, 4>(x, w, scale, M, K, O, y, s);
+    case 5: return rows_launch<Q8, NR, 64, 5>(x, w, scale, M, K, O, y, s);
+    case 6: return rows_launch<Q8, NR, 64, 6>(x, w, scale, M, K, O, y, s);
+    case 7: return rows_launch<Q8, NR, 64, 7>(x, w, scale, M, K, O, y, s);
+    default: return rows_launch<Q8, NR, 64, 8>(x, w, scale, M, K, O, y, s);
+  }
 }
 
 template <bool Q8>
 int rows_gemv(const uint16_t* x, const void* w, const float* scale, int M, int K, int O,
               uint16_t* y, hipStream_t s) {
-  const int chunks = K / (Q8 ? 16 : 8);
-  ESC_REQUIRE(K > 0 && K % (Q8 ? 16 : 8) == 0 &&
-                  (chunks == 32 || chunks == 64 || chunks == 128 || chunks == 256),
-              "K=%d: need %s", K, Q8 ? "512, 1024, 2048 or 4096" : "256, 512, 1024 or 2048");
-  for (int m0 = 0; m0 < M; m0 += 8) {
-    const int mr = std::min(8, M - m0);
+  const int cw = Q8 ? 16 : 8;  // weights per 16-byte chunk
+  const int chunks = K / cw;
+  ESC_REQUIRE(K > 0 && K % cw == 0 && chunks >= 8 && chunks <= 64 * kRowsMaxCpl,
+              "K=%d: need a multiple of %d in [%d, %d]", K, cw, 8 * cw, 64 * kRowsMaxCpl * cw);
+  const RowsGeo g = rows_geo(chunks);
+  const int nr_max = rows_nr_max(Q8, g.cpl);
+  for (int m0 = 0; m0 < M; m0 += nr_max) {
+    const int mr = std::min(nr_max, M - m0);
     const uint16_t* xm = x + (size_t)m0 * K;
     uint16_t* ym = y + (size_t)m0 * O;
     int rc;
-    if (mr == 1) rc = rows_gemv_nr<Q8, 1>(xm, w, scale, mr, K, O, ym, s);
-    else if (mr == 2) rc = rows_gemv_nr<Q8, 2>(xm, w, scale, mr, K, O, ym, s);
-    else if (mr <= 4) rc = rows_gemv_nr<Q8, 4>(xm, w, scale, mr, K, O, ym, s);
-    else rc = rows_gemv_nr<Q8, 8>(xm, w, scale, mr, K, O, ym, s);
+    if (mr == 1) rc = rows_by_geo<Q8, 1>(g, xm, w, scale, mr, K, O, ym, s);
+    else if (mr == 2) rc = rows_by_geo<Q8, 2>(g, xm, w, scale, mr, K, O, ym, s);
+    else if (mr <= 4) rc = rows_by_geo<Q8, 4>(g, xm, w, scale, mr, K, O, ym, s);
+    else rc = rows_by_geo<Q8, 8>(g, xm, w, scale, mr, K, O, ym, s);
     if (rc) return rc;
   }
   return ESC_OK;
@@ -655,6 +696,16 @@ int esc_moe_block_out(const uint16_t* y, const uint16_t* sh, const uint16_t* shg
   hipLaunchKernelGGL(esc::k_block_out, dim3((H + 255) / 256, m), dim3(256), 0, S(stream), y, sh,
                      shg, H, out);
   return launched("k_block_out");
+}
+
+int esc_q8_embed(const int32_t* ids, int T, const int8_t* w8, const float* scale, int N, int K,
+                 uint16_t* out, void* stream) {
+  ESC_REQUIRE(ids && w8 && scale && out, "null pointer");
+  ESC_REQUIRE(T >= 0 && N > 0 && K > 0 && K % 16 == 0, "bad T=%d / N=%d / K=%d (K a multiple of 16)",
+              T, N, K);
+  if (T == 0) return ESC_OK;
+  hipLaunchKernelGGL(esc::k_q8_embed, dim3(T), dim3(256), 0, S(stream), ids, w8, scale, N, K, out);
+  return launched("k_q8_embed");
 }
 
 }  // extern "C"

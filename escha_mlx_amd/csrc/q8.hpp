@@ -5,8 +5,9 @@
 // shared-expert gates (y = f16(x @ w^T), escha_mlx/models/qwen3_5_moe.py:257-273).
 //
 // Weights are [O][K] row-major (one output channel per row), read once from
-// HBM with 16-byte loads: LPR = min(64, K/16) lanes share a row, each owning
-// CPL = K/16/LPR 16-byte chunks of it, so a wave-step covers 64/LPR rows.  The
+// HBM with 16-byte loads: LPR lanes share a row (the chunk count rounded up to
+// a power of two, at most 64), each owning up to CPL 16-byte chunks of it, so
+// a wave-step covers 64/LPR rows.  The
 // lane's inputs for its chunks (NR rows of x) stay in VGPRs for the whole
 // launch; the rows' partial sums meet through lane exchanges (DPP / permlane).
 // Each weight is rounded exactly as the contract says (int8 -> f32, one fma
@@ -56,8 +57,10 @@ __device__ __forceinline__ void w8_to_f16x4(uint32_t w, float s, float ms, uint3
 }
 
 // y[m][o] (ldy between rows) for m < M <= NR.  Q8: w is int8 [O][K] with
-// scale [O]; otherwise w is f16 [O][K] and scale unused.  K = 16-byte chunks
-// x LPR x CPL.  grid: any; block 256.
+// scale [O]; otherwise w is f16 [O][K] and scale unused.  The row's `chunks`
+// 16-byte pieces are spread over LPR lanes x CPL pieces each; a lane's piece
+// sub + LPR*j beyond the row (chunks not a multiple of LPR) reads nothing and
+// adds zero.  grid: any; block 256.
 template <bool Q8, int NR, int LPR, int CPL>
 __global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ x,
                                                    const void* __restrict__ wv,
@@ -68,6 +71,10 @@ __global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ 
   constexpr int CW = 16 / WB;                    // weights per 16-byte chunk
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % LPR, rsel = lane / LPR;
+  const int chunks = K / CW;
+  bool has[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) has[j] = sub + LPR * j < chunks;
   // the lane's inputs: NR rows x CPL chunks x CW halves, as f16 pairs
   uint32_t xr[NR][CPL][CW / 2];
 #pragma unroll
@@ -81,6 +88,7 @@ __global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ 
     if (m >= M) break;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
+      if (!has[j]) continue;
       const uint16_t* xp = x + (size_t)m * K + (size_t)(sub + LPR * j) * CW;
 #pragma unroll
       for (int i = 0; i < CW / 8; ++i) {
@@ -101,7 +109,9 @@ __global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ 
     const int oc = min(st * RPS + rsel, O - 1);  // in-bounds reads for a partial last step
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
-      wc[j] = *reinterpret_cast<const uint4*>(w8 + ((size_t)oc * K + (size_t)(sub + LPR * j) * CW) * WB);
+      wc[j] = has[j] ? *reinterpret_cast<const uint4*>(
+                           w8 + ((size_t)oc * K + (size_t)(sub + LPR * j) * CW) * WB)
+                     : make_uint4(0u, 0u, 0u, 0u);
     if constexpr (Q8) s = scale[oc];
   };
   int st = blockIdx.x * 4 + wave;
@@ -130,6 +140,7 @@ __global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ 
 #pragma unroll
         for (int i = 0; i < 4; ++i) wp[i] = ww[i];
       }
+      // a piece beyond the row has zero inputs: its product adds +0
 #pragma unroll
       for (int m = 0; m < NR; ++m)
 #pragma unroll
@@ -142,6 +153,38 @@ __global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ 
       for (int m = 0; m < NR; ++m)
         if (m < M) y[(size_t)m * ldy + o] = __builtin_bit_cast(uint16_t, to_f16(acc[m]));
     }
+  }
+}
+
+// Embedding rows of an int8 table (escha_mlx/quant.py:253-266 under the w8a16
+// contract): out[t][k] = f16(f32(w8[ids[t]][k]) * f32(scale[ids[t]])), the
+// same rounding as the GEMV's weights.  An id outside [0, N) yields a row of
+// f16 NaN (0x7E00) instead of a read outside the table.  K a multiple of 16;
+// grid (T), block 256, each thread converting 16-byte chunks of the row.
+__global__ __launch_bounds__(256) void k_q8_embed(const int32_t* __restrict__ ids,
+                                                  const int8_t* __restrict__ w8,
+                                                  const float* __restrict__ scale, int N, int K,
+                                                  uint16_t* __restrict__ out) {
+  const int t = blockIdx.x;
+  const int id = ids[t];
+  const bool ok = id >= 0 && id < N;
+  const float s = ok ? scale[id] : 0.f, ms = -128.f * s;
+  uint4* dst = reinterpret_cast<uint4*>(out + (size_t)t * K);
+  const uint4* src = reinterpret_cast<const uint4*>(w8 + (size_t)(ok ? id : 0) * K);
+  for (int c = threadIdx.x; c < K / 16; c += 256) {
+    uint32_t p[8];
+    if (ok) {
+      const uint4 v = src[c];
+      w8_to_f16x4(v.x, s, ms, p[0], p[1]);
+      w8_to_f16x4(v.y, s, ms, p[2], p[3]);
+      w8_to_f16x4(v.z, s, ms, p[4], p[5]);
+      w8_to_f16x4(v.w, s, ms, p[6], p[7]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p[i] = 0x7E007E00u;
+    }
+    dst[2 * c] = make_uint4(p[0], p[1], p[2], p[3]);
+    dst[2 * c + 1] = make_uint4(p[4], p[5], p[6], p[7]);
   }
 }
 

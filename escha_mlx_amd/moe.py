@@ -21,7 +21,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from . import envs, ops
+from . import envs, ops, quant
 
 RS = ops.RS
 
@@ -156,25 +156,41 @@ class EschaMoEExperts(torch.nn.Module):
 
 
 class EschaSparseMoeBlock(torch.nn.Module):
-    """The whole MoE block (models/qwen3_5_moe.py:257-273; ref.moe_block,
+    """The whole MoE block (models/qwen3_5_moe.py:60-80, 257-273; ref.moe_block,
     escha_mlx/ref.py:314-349): router gate (f16 Linear) -> top-k softmax ->
     routed experts (f16 sum) -> shared expert (w8a16 gate / up, activation,
     w8a16 down) scaled by sigmoid(shared gate) -> f16.
 
-    gate_w [E, H] f16, experts an ``EschaMoEExperts``, sh_gate / sh_up /
-    sh_down ``quant.EschaQ8Linear``, shg_w [1, H] f16.  The routed sum is
-    rounded to f16 before the shared expert is added (the model's forward
-    contract, models/qwen3_5_moe.py:250-253).
+    Constructor inputs as the reference's: hidden size, expert count, top-k,
+    the gate_up / down ``EschaExperts``, the router weight gate_w [E, H] and
+    shared gate shg_w [1, H] (f16), and ``shared`` with the shared expert's
+    ``{gate,up,down}_w8`` int8 [N, K] and ``{gate,up,down}_scale`` [N].  The
+    routed sum is rounded to f16 before the shared expert is added (the
+    model's forward contract, models/qwen3_5_moe.py:250-253).
     """
 
-    def __init__(self, gate_w, experts: EschaMoEExperts, sh_gate, sh_up, sh_down, shg_w,
-                 top_k: int, device="cuda") -> None:
+    def __init__(self, hidden_size: int, num_experts: int, top_k: int, gu: EschaExperts,
+                 dn: EschaExperts, gate_w, shg_w, shared: dict,
+                 group_size: int = quant.DEFAULT_GROUP, device=None) -> None:
         super().__init__()
+        device = gu.code.device if device is None else device
+        if gu.IC != hidden_size or gu.E != num_experts or dn.E != num_experts:
+            raise ValueError(f"experts [{gu.E}] {gu.IC} -> {gu.OC} do not match hidden_size "
+                             f"{hidden_size} / num_experts {num_experts}")
         as16 = lambda a: (a if torch.is_tensor(a) else torch.from_numpy(np.asarray(a, np.float16))
                           ).to(device=device, dtype=torch.float16).contiguous()
         self.gate_w, self.shg_w = as16(gate_w), as16(shg_w)
-        self.experts, self.top_k = experts, top_k
-        self.sh_gate, self.sh_up, self.sh_down = sh_gate, sh_up, sh_down
+        if tuple(self.gate_w.shape) != (num_experts, hidden_size):
+            raise ValueError(f"router gate must be [{num_experts}, {hidden_size}], got "
+                             f"{tuple(self.gate_w.shape)}")
+        if tuple(self.shg_w.shape) != (1, hidden_size):
+            raise ValueError(f"shared expert gate must be [1, {hidden_size}], got "
+                             f"{tuple(self.shg_w.shape)}")
+        self.experts = EschaMoEExperts(gu, dn, num_experts, top_k)
+        self.top_k, self.num_experts = top_k, num_experts
+        self.sh_gate = quant.make_linear(shared["gate_w8"], shared["gate_scale"], group_size, device)
+        self.sh_up = quant.make_linear(shared["up_w8"], shared["up_scale"], group_size, device)
+        self.sh_down = quant.make_linear(shared["down_w8"], shared["down_scale"], group_size, device)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shape = x.shape

@@ -380,6 +380,23 @@ def moe_block_out(y: torch.Tensor, sh: torch.Tensor, shg: torch.Tensor) -> torch
     return out
 
 
+def q8_embed(ids: torch.Tensor, w8: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """ids int [...], w8 int8 [N, K], scale f32 [N] -> f16 [..., K], the rows
+    f16(f32(w8[id]) * f32(scale[id])) (escha_mlx/quant.py:253-266).  An id
+    outside [0, N) gives a row of NaN."""
+    flat = ids.reshape(-1).to(torch.int32).contiguous()
+    _dev(flat, w8, scale)
+    if w8.dtype != torch.int8 or scale.dtype != torch.float32 or w8.ndim != 2:
+        raise ValueError("w8 must be int8 [N, K] and scale float32 [N]")
+    n, k = w8.shape
+    if scale.shape != (n,):
+        raise ValueError(f"scale shape {tuple(scale.shape)} does not match w8 {tuple(w8.shape)}")
+    out = torch.empty((flat.shape[0], k), dtype=torch.float16, device=w8.device)
+    _lib.call("esc_q8_embed", _ptr(flat), flat.shape[0], _ptr(w8), _ptr(scale), n, k, _ptr(out),
+              _stream())
+    return out.reshape(*ids.shape, k)
+
+
 def moe_status(ws: torch.Tensor, T: int, top_k: int, H: int, I: int) -> int:
     """1 if a one-launch expert path using ``ws`` ever hit its bounded wait (synchronises)."""
     flag = ctypes.c_int32(0)

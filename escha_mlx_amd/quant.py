@@ -11,7 +11,8 @@ the per-row scale directly (16-byte loads, one weight rounded per the contract
 before its product).  ``group_size`` is accepted for the call surface and has
 no effect: the scale is per output channel, so grouping never changes a value
 (escha_mlx/quant.py:27-34).  ``EschaQ8Head`` is the same linear used as the
-vocabulary projection (escha_mlx/quant.py:236-251).
+vocabulary projection (escha_mlx/quant.py:236-251), ``EschaQ8Embedding`` the
+token embedding over the same int8 rows (escha_mlx/quant.py:253-266).
 """
 from __future__ import annotations
 
@@ -49,6 +50,27 @@ class EschaQ8Head(EschaQ8Linear):
     one to eight flattened rows share each weight row read."""
 
 
+class EschaQ8Embedding(torch.nn.Module):
+    """int8 token embedding (escha_mlx/quant.py:253-266): ids -> f16 rows
+    f16(f32(w8[id]) * f32(scale[id])), the contract's dequantised weights."""
+
+    def __init__(self, w8, scale, device="cuda") -> None:
+        super().__init__()
+        w8 = torch.as_tensor(np.asarray(w8, dtype=np.int8)) if not torch.is_tensor(w8) else w8
+        scale = (torch.as_tensor(np.asarray(scale, dtype=np.float32)) if not torch.is_tensor(scale)
+                 else scale.to(torch.float32))
+        if w8.ndim != 2 or w8.dtype != torch.int8 or scale.shape != (w8.shape[0],):
+            raise ValueError(f"need int8 [N, K] and scale [N], got {tuple(w8.shape)} / {tuple(scale.shape)}")
+        if w8.shape[1] % 16:
+            raise ValueError(f"embedding width {w8.shape[1]} must be a multiple of 16")
+        self.w8 = w8.contiguous().to(device)
+        self.scale = scale.contiguous().to(device)
+        self.num_embeddings, self.embedding_dim = self.w8.shape
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        return ops.q8_embed(ids.to(self.w8.device), self.w8, self.scale)
+
+
 def make_linear(w8: np.ndarray, scale: np.ndarray, group_size: int = DEFAULT_GROUP,
                 device="cuda") -> EschaQ8Linear:
     """escha_mlx.quant.make_linear (quant.py:269-279): int8 [N, K] + scale [N]."""
@@ -61,3 +83,10 @@ def make_head(w8: np.ndarray, scale: np.ndarray, group_size: int = DEFAULT_GROUP
     """escha_mlx.quant.make_head (quant.py:282-296)."""
     del group_size
     return EschaQ8Head(w8, scale, device)
+
+
+def make_embedding(w8: np.ndarray, scale: np.ndarray, group_size: int = DEFAULT_GROUP,
+                   device="cuda") -> EschaQ8Embedding:
+    """escha_mlx.quant.make_embedding (quant.py:298-308)."""
+    del group_size
+    return EschaQ8Embedding(w8, scale, device)

@@ -164,7 +164,7 @@ int esc_moe_combine(const uint16_t* d16, const float* scores, int T, int top_k, 
 
 /* Dense w8a16 linear: y f16 [M][O] = f16(f32-accumulated x @ wf^T) with
  * wf = f16(f32(w8) * f32(scale)), w8 int8 [O][K] (one output channel per row),
- * scale f32 [O], x f16 [M][K]; K in {512, 1024, 2048, 4096}.  Each weight is
+ * scale f32 [O], x f16 [M][K]; K a multiple of 16 in [128, 8192].  Each weight is
  * rounded as the contract states; the float32 sum is reassociated (tolerance
  * contract, deterministic).  The contract of EschaQ8Linear
  * (escha_mlx/quant.py:1-30, CPU statement ref.w8a16, escha_mlx/ref.py:308-311):
@@ -173,7 +173,7 @@ int esc_w8a16(const uint16_t* x, const int8_t* w8, const float* scale, int M, in
               uint16_t* y, void* stream);
 
 /* f16-weight linear without bias: y f16 [M][O] = f16(f32-accumulated x @ w^T),
- * w f16 [O][K], K in {256, 512, 1024, 2048}.  The router gate and the shared
+ * w f16 [O][K], K a multiple of 8 in [64, 4096].  The router gate and the shared
  * expert gate of the MoE block (escha_mlx/models/qwen3_5_moe.py:259, 271;
  * ref.moe_block, escha_mlx/ref.py:324, 347). */
 int esc_gemv_f16w(const uint16_t* x, const uint16_t* w, int M, int K, int O, uint16_t* y,
@@ -190,6 +190,14 @@ int esc_moe_shared_act(const uint16_t* g, const uint16_t* u, int m, int I, uint1
  * the shared-expert gate logit (models/qwen3_5_moe.py:250-253, 270-272). */
 int esc_moe_block_out(const uint16_t* y, const uint16_t* sh, const uint16_t* shg, int m, int H,
                       uint16_t* out, void* stream);
+
+/* int8 embedding lookup: out f16 [T][K] = f16(f32(w8[ids[t]]) * f32(scale[ids[t]])),
+ * w8 int8 [N][K] (K a multiple of 16), scale f32 [N], ids int32 [T]: the
+ * dequantised rows of EschaQ8Embedding (escha_mlx/quant.py:253-266; the same
+ * rounding as the w8a16 linear's weights).  An id outside [0, N) yields a row
+ * of f16 NaN rather than a read outside the table. */
+int esc_q8_embed(const int32_t* ids, int T, const int8_t* w8, const float* scale, int N, int K,
+                 uint16_t* out, void* stream);
 
 /* Routed-expert path for T tokens: y f16 [T][H] = f16(sum over the k slots,
  * in slot order, of f32(d16) * f32(f16(score))), where per (token, slot):

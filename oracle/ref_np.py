@@ -37,6 +37,9 @@ Pinning status of each function (what checks it independently of its own code):
   w8a16            pinned: the reference's w8a16 goldens (tests/data/codec/
                    w8a16_*, tolerance: float32 sum order) and one-hot inputs
                    (each output is one contract weight f16(f32(w8)*f32(scale))).
+  q8_dequant,      pinned: exact rational products w8 * scale rounded once to
+  q8_embed         f16 (f16 scales: the float32 product is exact), for all 256
+                   int8 values, and the one-hot w8a16 check above.
   linear_f16,      pinned: vectors from ref.moe_block with a non-zero shared
   shared_act,      expert and router (tests/golden/make_ref_vectors.py),
   moe_block        tolerance (numpy BLAS order, f64 routed sum).
@@ -324,11 +327,25 @@ def moe_routed(x, ids, scores, gu, dn, K_gu, K_dn, ordered=True, acc64=False):
 
 # ---------------------------------------------------------------- dense int8 / full MoE block
 
+def q8_dequant(w8: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """The contract weights wf = f16(f32(w8) * f32(scale)), w8 [N, K] int8,
+    scale [N] (escha_mlx/quant.py:1-30, ref.py:308-311)."""
+    return (w8.astype(np.float32) * np.asarray(scale, np.float32)[:, None]).astype(np.float16)
+
+
 def w8a16(x: np.ndarray, w8: np.ndarray, scale: np.ndarray) -> np.ndarray:
-    """y = f16(f32(x) @ f32(wf)^T), wf = f16(f32(w8) * f32(scale)); w8 [O, K]
+    """y = f16(f32(x) @ f32(wf)^T), wf = q8_dequant(w8, scale); w8 [O, K]
     int8, scale [O] (escha_mlx/ref.py:308-311, quant.py:1-30)."""
-    wf = (w8.astype(np.float32) * np.asarray(scale, np.float32)[:, None]).astype(np.float16)
+    wf = q8_dequant(w8, scale)
     return (x.astype(np.float32) @ wf.astype(np.float32).T).astype(np.float16)
+
+
+def q8_embed(ids: np.ndarray, w8: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """Embedding rows q8_dequant(w8, scale)[ids] (escha_mlx/quant.py:253-266:
+    the affine dequant there is exact in float32, then one f16 rounding)."""
+    ids = np.asarray(ids)
+    rows = q8_dequant(w8[ids.reshape(-1)], np.asarray(scale)[ids.reshape(-1)])
+    return rows.reshape(*ids.shape, w8.shape[1])
 
 
 def linear_f16(x: np.ndarray, w: np.ndarray) -> np.ndarray:

@@ -193,8 +193,9 @@ def test_experts_container_validation():
     assert (ex.E, ex.IC, ex.OC, ex.K) == (2, 128, 256, 2)
 
 
-@pytest.mark.parametrize("fn,K", [("esc_w8a16", 640), ("esc_w8a16", 256), ("esc_gemv_f16w", 128),
-                                  ("esc_gemv_f16w", 4096)])
+@pytest.mark.parametrize("fn,K", [("esc_w8a16", 648), ("esc_w8a16", 112), ("esc_w8a16", 8208),
+                                  ("esc_gemv_f16w", 60), ("esc_gemv_f16w", 56),
+                                  ("esc_gemv_f16w", 4104)])
 def test_dense_gemv_rejects_unsupported_K(fn, K):
     if fn == "esc_w8a16":
         rc, msg = _rc_msg(fn, DUMMY, DUMMY, DUMMY, 1, K, 256, DUMMY, None)
@@ -208,3 +209,14 @@ def test_w8a16_rejects_null_and_bad_sizes():
     assert rc == _lib.ESC_EINVAL and "null" in msg
     rc, msg = _rc_msg("esc_w8a16", DUMMY, DUMMY, DUMMY, 1, 2048, 0, DUMMY, None)
     assert rc == _lib.ESC_EINVAL and "O=0" in msg
+
+
+def test_q8_embed_rejects_null_and_bad_sizes():
+    rc, msg = _rc_msg("esc_q8_embed", None, 1, DUMMY, DUMMY, 4, 32, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "null" in msg
+    rc, msg = _rc_msg("esc_q8_embed", DUMMY, 1, DUMMY, DUMMY, 4, 24, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "K=24" in msg
+    rc, msg = _rc_msg("esc_q8_embed", DUMMY, 1, DUMMY, DUMMY, 0, 32, DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "N=0" in msg
+    rc, _ = _rc_msg("esc_q8_embed", DUMMY, 0, DUMMY, DUMMY, 4, 32, DUMMY, None)
+    assert rc == _lib.ESC_OK  # nothing to launch

@@ -52,12 +52,13 @@ def test_w8a16_vs_reference_golden(w8a16_golden):
     assert _rel(got, x.astype(np.float64) @ wf.T) < 2e-3
 
 
-@pytest.mark.parametrize("K", [512, 1024, 2048, 4096])
+# K = 128 / 256 / 384: 8 / 16 / 32 lanes per row (384: 24 chunks, 8 lanes
+# idle); 5120 and 8192: 5 and 8 chunks per lane, at most 2 rows per launch
+@pytest.mark.parametrize("K", [128, 256, 384, 512, 1024, 2048, 4096, 5120, 8192])
 @pytest.mark.parametrize("m", [1, 3, 8, 11])
 def test_w8a16_one_hot_bit_exact(K, m):
     rng = np.random.default_rng(K + m)
-    O = 384 if K < 4096 else 96  # a partial last wave-step for K = 512 (2 rows per step)
-    O += 1 if K == 512 else 0
+    O = (384 if K < 4096 else 96) + 1  # a partial last wave-step where rows share a wave
     w8 = rng.integers(-128, 128, size=(O, K), dtype=np.int8)
     scale = rng.uniform(1e-3, 5e-3, O).astype(np.float16).astype(np.float32)
     ks = rng.integers(0, K, size=m)
@@ -69,7 +70,8 @@ def test_w8a16_one_hot_bit_exact(K, m):
         assert np.array_equal(got[r].view(np.uint16), want.view(np.uint16)), r
 
 
-@pytest.mark.parametrize("K,m", [(2048, 1), (512, 4), (1024, 8), (2048, 13)])
+@pytest.mark.parametrize("K,m", [(2048, 1), (512, 4), (1024, 8), (2048, 13), (256, 3), (384, 9),
+                                 (5120, 5), (8192, 3)])
 def test_w8a16_vs_f64_and_deterministic(K, m):
     rng = np.random.default_rng(3 * K + m)
     O = 640
@@ -83,8 +85,8 @@ def test_w8a16_vs_f64_and_deterministic(K, m):
     assert torch.equal(ops().w8a16(*args), y)
 
 
-@pytest.mark.parametrize("K", [256, 512, 1024, 2048])
-@pytest.mark.parametrize("m", [1, 5])
+@pytest.mark.parametrize("K", [64, 200, 256, 512, 1024, 2048, 4096])
+@pytest.mark.parametrize("m", [1, 5, 9])
 def test_gemv_f16w_one_hot_and_f64(K, m):
     rng = np.random.default_rng(7 * K + m)
     O = 256
@@ -120,16 +122,13 @@ def test_shared_act_and_block_out_vs_oracle():
 
 
 def _block(v):
-    from escha_mlx_amd import moe, quant
+    from escha_mlx_amd import moe
     E, H = v["blk_gate_w"].shape
     gu = moe.EschaExperts(v["blk_gu_code"], v["blk_gu_rin"], v["blk_gu_rout"], device=DEV)
     dn = moe.EschaExperts(v["blk_dn_code"], v["blk_dn_rin"], v["blk_dn_rout"], device=DEV)
-    ex = moe.EschaMoEExperts(gu, dn, E, 2)
-    return moe.EschaSparseMoeBlock(
-        v["blk_gate_w"], ex, quant.make_linear(v["blk_sh_gate_w8"], v["blk_sh_gate_scale"]),
-        quant.make_linear(v["blk_sh_up_w8"], v["blk_sh_up_scale"]),
-        quant.make_linear(v["blk_sh_down_w8"], v["blk_sh_down_scale"]), v["blk_shg_w"], 2,
-        device=DEV)
+    shared = {f"{p}_{leaf}": v[f"blk_sh_{p}_{leaf}"] for p in ("gate", "up", "down")
+              for leaf in ("w8", "scale")}
+    return moe.EschaSparseMoeBlock(H, E, 2, gu, dn, v["blk_gate_w"], v["blk_shg_w"], shared)
 
 
 def test_moe_block_vs_oracle_and_reference(ref_vectors):
@@ -144,3 +143,23 @@ def test_moe_block_vs_oracle_and_reference(ref_vectors):
     assert _rel(got, want) < 5e-3
     assert _rel(got, v["blk_y"]) < 5e-3
     assert torch.equal(blk(x), y)
+
+
+@pytest.mark.parametrize("K", [256, 2048])
+def test_q8_embed_bit_exact(K):
+    """Embedding rows are the contract weights, bit for bit (the same rounding
+    the w8a16 golden pins); an id outside the table gives a NaN row."""
+    from escha_mlx_amd import quant
+    rng = np.random.default_rng(K)
+    N = 300
+    w8 = rng.integers(-128, 128, size=(N, K), dtype=np.int8)
+    scale = rng.uniform(1e-3, 5e-3, N).astype(np.float16)  # f16 scales, as exported
+    emb = quant.make_embedding(w8, scale, device=DEV)
+    ids = rng.integers(0, N, size=(2, 5))
+    got = emb(torch.from_numpy(ids).to(DEV))
+    assert got.shape == (2, 5, K) and got.dtype == torch.float16
+    want = R.q8_embed(ids, w8, scale)
+    assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+    bad = emb(torch.tensor([0, N, -1, N - 1], device=DEV)).cpu().numpy()
+    assert np.isnan(bad[1]).all() and np.isnan(bad[2]).all()
+    assert np.array_equal(bad[[0, 3]].view(np.uint16), R.q8_embed(np.array([0, N - 1]), w8, scale).view(np.uint16))

@@ -319,6 +319,40 @@ def test_w8a16_one_hot_reads_contract_weights(w8a16_golden):
         assert np.array_equal(got[i].view(np.uint16), want.view(np.uint16))
 
 
+def test_q8_dequant_exact_products():
+    """Every int8 value times a spread of scales: f16 scales make w8 * scale
+    exact in float32 (8 + 11 significant bits), so the contract weight is the
+    exact rational product rounded once to f16; f32 scales round the exact
+    product to float32 first (the contract's f32 multiply), then to f16.
+    Products of an int8 and a float32 are exact in float64, which makes both
+    expectations independent of numpy's float32 multiply."""
+    from fractions import Fraction
+    w8 = np.arange(-128, 128, dtype=np.int8)[None, :]
+    s16 = np.array([1e-3, 3.7e-3, 0.0123, 6.1e-5, 1.0, 0.33], np.float16)
+    for sc in s16:
+        got = R.q8_dequant(w8, np.array([sc], np.float32))[0]
+        want = np.array([np.float16(float(Fraction(int(w)) * Fraction(float(sc))))
+                         for w in w8[0]], np.float16)
+        assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), sc
+    for sc in np.array([1.0000001e-3, 2.345678e-3, 7.777777e-2], np.float32):
+        got = R.q8_dequant(w8, np.array([sc], np.float32))[0]
+        want = np.array([np.float16(np.float32(float(Fraction(int(w)) * Fraction(float(sc)))))
+                         for w in w8[0]], np.float16)
+        assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), sc
+
+
+def test_q8_embed_rows_and_shape():
+    rng = np.random.default_rng(4)
+    w8 = rng.integers(-128, 128, size=(50, 32), dtype=np.int8)
+    scale = rng.uniform(1e-3, 5e-3, 50).astype(np.float16)
+    ids = np.array([[3, 49], [0, 3]])
+    got = R.q8_embed(ids, w8, scale)
+    assert got.shape == (2, 2, 32) and got.dtype == np.float16
+    wf = R.q8_dequant(w8, scale)
+    assert np.array_equal(got[0, 1], wf[49]) and np.array_equal(got[1, 0], wf[0])
+    assert np.array_equal(got[0, 0], got[1, 1])
+
+
 def test_moe_block_vs_reference_moe_block(ref_vectors):
     """The full block (router gate, routed experts, int8 shared expert, sigmoid
     gate) against ref.moe_block: with its float64 routed sum, within an f16
