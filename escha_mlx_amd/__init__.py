@@ -10,9 +10,11 @@ reached from Python through ctypes with the reference's call surface:
   dense  — escha_mlx.dense (EschaWeight, EschaLinear, build, pack_code, ...)
   moe    — escha_mlx.moe (EschaExperts, build_groups, ...) + the expert path
            and the whole MoE block (router, shared expert)
-  quant  — escha_mlx.quant's w8a16 linears (EschaQ8Linear, make_linear, ...)
+  quant  — escha_mlx.quant's int8 modules (EschaQ8Linear / Head / Embedding)
+  loader — escha_mlx.loader + the architecture plugins' checkpoint loaders
+           (load_model, resolve, is_escha_checkpoint, LastPositionHead)
 """
-from . import _lib, dense, envs, moe, ops, quant  # noqa: F401
+from . import _lib, dense, envs, loader, moe, ops, quant  # noqa: F401
 
-__all__ = ["ops", "dense", "moe", "quant", "envs"]
+__all__ = ["ops", "dense", "moe", "quant", "loader", "envs"]
 __version__ = "0.1.0"

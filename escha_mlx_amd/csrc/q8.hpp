@@ -58,9 +58,12 @@ __device__ __forceinline__ void w8_to_f16x4(uint32_t w, float s, float ms, uint3
 
 // y[m][o] (ldy between rows) for m < M <= NR.  Q8: w is int8 [O][K] with
 // scale [O]; otherwise w is f16 [O][K] and scale unused.  The row's `chunks`
-// 16-byte pieces are spread over LPR lanes x CPL pieces each; a lane's piece
-// sub + LPR*j beyond the row (chunks not a multiple of LPR) reads nothing and
-// adds zero.  grid: any; block 256.
+// 16-byte pieces are spread over LPR lanes x CPL pieces each.  A lane's piece
+// sub + LPR*j beyond the row (chunks not a multiple of LPR) has zero inputs
+// and reads the row's last piece instead, so every weight load stays
+// unconditional; int8 weights convert to finite values, whose products with
+// the zero inputs add +0, while f16 weights (which may hold Inf) are replaced
+// by zeros.  grid: any; block 256.
 template <bool Q8, int NR, int LPR, int CPL>
 __global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ x,
                                                    const void* __restrict__ wv,
@@ -73,8 +76,12 @@ __global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ 
   const int sub = lane % LPR, rsel = lane / LPR;
   const int chunks = K / CW;
   bool has[CPL];
+  int coff[CPL];  // byte offset of the lane's piece j within a weight row
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) has[j] = sub + LPR * j < chunks;
+  for (int j = 0; j < CPL; ++j) {
+    has[j] = sub + LPR * j < chunks;
+    coff[j] = min(sub + LPR * j, chunks - 1) * 16;
+  }
   // the lane's inputs: NR rows x CPL chunks x CW halves, as f16 pairs
   uint32_t xr[NR][CPL][CW / 2];
 #pragma unroll
@@ -107,11 +114,13 @@ __global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ 
   // current step is converted and multiplied
   auto load_step = [&](int st, uint4* wc, float& s) {
     const int oc = min(st * RPS + rsel, O - 1);  // in-bounds reads for a partial last step
+    const uint8_t* row = w8 + (size_t)oc * K * WB;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j)
-      wc[j] = has[j] ? *reinterpret_cast<const uint4*>(
-                           w8 + ((size_t)oc * K + (size_t)(sub + LPR * j) * CW) * WB)
-                     : make_uint4(0u, 0u, 0u, 0u);
+    for (int j = 0; j < CPL; ++j) {
+      wc[j] = *reinterpret_cast<const uint4*>(row + coff[j]);
+      if constexpr (!Q8)
+        if (!has[j]) wc[j] = make_uint4(0u, 0u, 0u, 0u);
+    }
     if constexpr (Q8) s = scale[oc];
   };
   int st = blockIdx.x * 4 + wave;
@@ -140,7 +149,6 @@ __global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ 
 #pragma unroll
         for (int i = 0; i < 4; ++i) wp[i] = ww[i];
       }
-      // a piece beyond the row has zero inputs: its product adds +0
 #pragma unroll
       for (int m = 0; m < NR; ++m)
 #pragma unroll
