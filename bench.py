@@ -262,6 +262,20 @@ def _linear(ops, P, x, i, lut, mat=True):
     return ops.linear(x, code, P["rin"], P["rout"], P["K"], P["ic"], P["oc"], lut=lut, ws=ws)
 
 
+def _linear_pair(ops, P0, P1, x, i, lut):
+    """dense.project_pair on copy i of two projections of the same input: one
+    esc_linear_pair launch below 16 rows."""
+    import torch
+    m = x.shape[0]
+    key = ("pair_ws", m, id(P1))
+    if key not in P0:   # zero-filled once, before any graph capture
+        P0[key] = torch.zeros(max(ops.linear_pair_workspace(m, P0["K"], P1["K"], P0["ic"],
+                                                            P0["oc"], P1["oc"]), 4),
+                              dtype=torch.uint8, device=x.device)
+    sel = lambda P: (P["code"][i % len(P["code"])], P["rin"], P["rout"], P["K"], P["oc"], None)
+    return ops.linear_pair(x, sel(P0), sel(P1), lut=lut, ws=P0[key])
+
+
 def _linear_parts(ops, P, x, i, lut, mat=True):
     """The same linear as separate launches (input transform, GEMV/GEMM, output)."""
     from escha_mlx_amd.dense import DENSE_MAT_R, dense_block_r
@@ -366,6 +380,17 @@ def bench_dense(args, torch, ops, cfg):
                   for i in range(L)]
             per[f"M{M}_layer_graph_us"] = round(graph_time(torch, fl, args.steps, args.warmup,
                                                            stream, f"M{M} layer") * 1e3, 2)
+            # k and v as one pair dispatch (dense.project_pair), alone and in the layer
+            pk, pv = P["k"][0], P["v"][0]
+            fkv = [lambda i=i: _linear_pair(ops, pk, pv, xs["k"], i, True) for i in range(L)]
+            per[f"M{M}_kv_pair_us"] = round(graph_time(torch, fkv, args.steps * 5, args.warmup,
+                                                       stream, f"M{M} kv pair") * 1e3, 2)
+            rest = [n for n in P if n not in ("k", "v")]
+            flp = [lambda i=i: (*_linear_pair(ops, pk, pv, xs["k"], i, True),
+                                *(_linear(ops, P[n][0], xs[n], i, P[n][1]) for n in rest))
+                   for i in range(L)]
+            per[f"M{M}_layer_graph_kv_pair_us"] = round(
+                graph_time(torch, flp, args.steps, args.warmup, stream, f"M{M} layer kv pair") * 1e3, 2)
             per[f"M{M}_layer_us"] = round(t_layer * 1e3, 2)
             per[f"M{M}_layer_gbs"] = round(total_b / (t_layer * 1e-3) / 1e9, 1)
             per[f"M{M}_tok_s_per_layer"] = round(M / (t_layer * 1e-3), 1)

@@ -42,6 +42,9 @@ SIGNATURES = {
     "esc_gemm_mfma": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "esc_linear_workspace": (_Z, [_I, _I, _I, _I]),
     "esc_linear": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _Z, _P]),
+    "esc_linear_pair_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),
+    "esc_linear_pair": (_I, [_P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I, _F,
+                             _P, _P, _P, _Z, _P]),
     "esc_gemm_rows_fast_workspace": (_Z, [_I, _I, _I, _I, _I]),
     "esc_gemm_rows_fast_out": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _Z, _P]),
     "esc_build_groups": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),

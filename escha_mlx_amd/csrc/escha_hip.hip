@@ -230,24 +230,50 @@ LinearPlan linear_plan(int M, int K, int IC, int OC, bool lut) {
   return p;
 }
 
+esc::LinearSmallArgs small_args(const uint16_t* x, const float* rin, const uint32_t* code,
+                                const float* rout, const uint16_t* bias, int M, int TK, int TN,
+                                const LinearPlan& lp, float rs, float* part, int* cnt,
+                                uint16_t* y) {
+  return {x, rin, code, rout, bias, M, TK, TN, lp.KS, lp.R, lp.S, lp.groups, lp.row_groups, rs,
+          part, cnt, y};
+}
+
 template <int K, bool LUT>
 struct LinearSmallF {
-  static int run(const uint16_t* x, const float* rin, const uint32_t* code, const float* rout,
-                 const uint16_t* bias, int M, int TK, int TN, const LinearPlan& lp, float rs,
-                 float* part, int* cnt, uint16_t* y, hipStream_t s) {
+  static int run(const esc::LinearSmallArgs& a, hipStream_t s) {
     // one row: VALU GEMV; several rows: matrix-core row-blocked GEMM
     constexpr int RMAX = LUT ? kLinearSmallRowsLut : kLinearSmallRows;
-    if (lp.R < 1 || lp.R > RMAX) return fail(ESC_EINVAL, "rows per group %d > %d", lp.R, RMAX);
-    const dim3 grid(lp.groups, lp.row_groups, lp.S);
-    if (lp.R == 1)
-      hipLaunchKernelGGL((esc::k_linear_small<K, LUT, 1>), grid, dim3(256), 0, s, x, rin, code,
-                         rout, bias, M, TK, TN, lp.KS, 1, rs, part, cnt, y);
+    if (a.R < 1 || a.R > RMAX) return fail(ESC_EINVAL, "rows per group %d > %d", a.R, RMAX);
+    const dim3 grid(a.groups, a.row_groups, a.S);
+    if (a.R == 1)
+      hipLaunchKernelGGL((esc::k_linear_small<K, LUT, 1>), grid, dim3(256), 0, s, a);
     else
-      hipLaunchKernelGGL((esc::k_linear_small<K, LUT, RMAX>), grid, dim3(256), 0, s, x, rin, code,
-                         rout, bias, M, TK, TN, lp.KS, lp.R, rs, part, cnt, y);
+      hipLaunchKernelGGL((esc::k_linear_small<K, LUT, RMAX>), grid, dim3(256), 0, s, a);
     return launched("k_linear_small");
   }
 };
+
+template <int K0, int K1, bool LUT>
+int linear_pair_launch(const esc::LinearSmallArgs& a0, const esc::LinearSmallArgs& a1,
+                       hipStream_t s) {
+  constexpr int RMAX = LUT ? kLinearSmallRowsLut : kLinearSmallRows;
+  if (a0.R != a1.R || a0.R < 1 || a0.R > RMAX)
+    return fail(ESC_EINVAL, "rows per group %d / %d (max %d)", a0.R, a1.R, RMAX);
+  const long n = (long)a0.groups * a0.row_groups * a0.S + (long)a1.groups * a1.row_groups * a1.S;
+  if (a0.R == 1)
+    hipLaunchKernelGGL((esc::k_linear_pair<K0, K1, LUT, 1>), dim3(n), dim3(256), 0, s, a0, a1);
+  else
+    hipLaunchKernelGGL((esc::k_linear_pair<K0, K1, LUT, RMAX>), dim3(n), dim3(256), 0, s, a0, a1);
+  return launched("k_linear_pair");
+}
+
+template <bool LUT>
+int linear_pair_k(int K0, int K1, const esc::LinearSmallArgs& a0, const esc::LinearSmallArgs& a1,
+                  hipStream_t s) {
+  if (K0 == 2) return K1 == 2 ? linear_pair_launch<2, 2, LUT>(a0, a1, s)
+                              : linear_pair_launch<2, 3, LUT>(a0, a1, s);
+  return K1 == 2 ? linear_pair_launch<3, 2, LUT>(a0, a1, s) : linear_pair_launch<3, 3, LUT>(a0, a1, s);
+}
 
 // Compute units of the current device (queried once per device).
 int device_cus() {
@@ -413,11 +439,9 @@ int esc_linear(const uint16_t* x, const float* rin, const uint32_t* code, const 
       if (int rc = ensure_lut()) return rc;
     float* part = reinterpret_cast<float*>(w + lp.off_part);
     int* cnt = reinterpret_cast<int*>(w + lp.off_cnt);
-    if (K == 2)
-      return use_lut ? LinearSmallF<2, true>::run(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s)
-                     : LinearSmallF<2, false>::run(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
-    return use_lut ? LinearSmallF<3, true>::run(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s)
-                   : LinearSmallF<3, false>::run(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y, s);
+    const esc::LinearSmallArgs a = small_args(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y);
+    if (K == 2) return use_lut ? LinearSmallF<2, true>::run(a, s) : LinearSmallF<2, false>::run(a, s);
+    return use_lut ? LinearSmallF<3, true>::run(a, s) : LinearSmallF<3, false>::run(a, s);
   }
   // many rows: input transform, then the matrix-core GEMM with the output
   // transform in its epilogue (or GEMM + output transform for OC % 256 != 0)
@@ -427,6 +451,53 @@ int esc_linear(const uint16_t* x, const float* rin, const uint32_t* code, const 
   float* mid = reinterpret_cast<float*>(w + lp.off_mid);
   if (int rc = esc_gemm_mfma(xh, code, M, K, IC, OC, use_lut, mid, stream)) return rc;
   return esc_output_transform(mid, rout, nullptr, bias, M, OC, rs, y, stream);
+}
+
+size_t esc_linear_pair_workspace(int M, int K0, int K1, int IC, int OC0, int OC1) {
+  const size_t a = esc_linear_workspace(M, K0, IC, OC0), b = esc_linear_workspace(M, K1, IC, OC1);
+  if (!a || !b) return 0;
+  return ((a + 255) & ~size_t(255)) + b;
+}
+
+int esc_linear_pair(const uint16_t* x, int M, int IC, const float* rin0, const uint32_t* code0,
+                    const float* rout0, const uint16_t* bias0, int K0, int OC0, const float* rin1,
+                    const uint32_t* code1, const float* rout1, const uint16_t* bias1, int K1,
+                    int OC1, int use_lut, float rs, uint16_t* y0, uint16_t* y1, void* ws,
+                    size_t ws_bytes, void* stream) {
+  if (int rc = check_proj(K0, IC, OC0)) return rc;
+  if (int rc = check_proj(K1, IC, OC1)) return rc;
+  ESC_REQUIRE(x && rin0 && code0 && rout0 && y0 && rin1 && code1 && rout1 && y1, "null pointer");
+  ESC_REQUIRE(M >= 0, "negative row count");
+  if (M == 0) return ESC_OK;
+  const size_t need = esc_linear_pair_workspace(M, K0, K1, IC, OC0, OC1);
+  if (!ws || ws_bytes < need)
+    return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, need);
+  // projection 1's workspace follows projection 0's (each as esc_linear's)
+  const size_t ws0 = esc_linear_workspace(M, K0, IC, OC0);
+  const size_t off1 = (ws0 + 255) & ~size_t(255);
+  char* w = static_cast<char*>(ws);
+  if (M >= kLinearSmallRows) {
+    // many rows: each projection's GEMM fills the GPU on its own
+    if (int rc = esc_linear(x, rin0, code0, rout0, bias0, M, K0, IC, OC0, use_lut, rs, y0, w, ws0,
+                            stream))
+      return rc;
+    return esc_linear(x, rin1, code1, rout1, bias1, M, K1, IC, OC1, use_lut, rs, y1, w + off1,
+                      ws_bytes - off1, stream);
+  }
+  if (use_lut)
+    if (int rc = ensure_lut()) return rc;
+  const int TK = IC / 16;
+  const LinearPlan p0 = linear_plan(M, K0, IC, OC0, use_lut != 0);
+  const LinearPlan p1 = linear_plan(M, K1, IC, OC1, use_lut != 0);
+  char* w1 = w + off1;
+  const esc::LinearSmallArgs a0 =
+      small_args(x, rin0, code0, rout0, bias0, M, TK, OC0 / 16, p0, rs,
+                 reinterpret_cast<float*>(w + p0.off_part), reinterpret_cast<int*>(w + p0.off_cnt), y0);
+  const esc::LinearSmallArgs a1 =
+      small_args(x, rin1, code1, rout1, bias1, M, TK, OC1 / 16, p1, rs,
+                 reinterpret_cast<float*>(w1 + p1.off_part), reinterpret_cast<int*>(w1 + p1.off_cnt), y1);
+  return use_lut ? linear_pair_k<true>(K0, K1, a0, a1, S(stream))
+                 : linear_pair_k<false>(K0, K1, a0, a1, S(stream));
 }
 
 size_t esc_gemm_rows_fast_workspace(int M, int R, int K, int IC, int OC) {

@@ -25,25 +25,58 @@
 
 namespace esc {
 
+// Arguments of one projection's one-launch linear: the launch covers
+// groups x row_groups x S workgroups (column group, row group, kt split).
+struct LinearSmallArgs {
+  const uint16_t* x;
+  const float* rin;
+  const uint32_t* code;
+  const float* rout;
+  const uint16_t* bias;
+  int M, TK, TN, KS, R, S, groups, row_groups;
+  float rs;
+  float* part;
+  int* cnt;
+  uint16_t* y;
+};
+
+// The workgroup's LDS: decode table (table decode only), the transformed
+// inputs of its rows, the VALU path's wave partials, the finishing sums.
 template <int K, bool LUT, int RMAX>
-__global__ __launch_bounds__(256) void k_linear_small(
-    const uint16_t* __restrict__ x, const float* __restrict__ rin,
-    const uint32_t* __restrict__ code, const float* __restrict__ rout,
-    const uint16_t* __restrict__ bias, int M, int TK, int TN, int KS, int R, float rs,
-    float* __restrict__ part, int* __restrict__ cnt, uint16_t* __restrict__ y) {
+struct LinearSmallSmem {
+  uint16_t lut[LUT ? 65536 : 1];
+  alignas(16) uint32_t x[RMAX][8 * 64];  // up to 64 kt per row
+  float red[RMAX > 1 ? 1 : 4][64][Geo<K>::NCOL];
+  float sum[2][Geo<K>::TPW * 16];
+  int last;
+};
+
+template <int K, bool LUT, int RMAX>
+__device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int ntg, int rg, int z,
+                                                  LinearSmallSmem<K, LUT, RMAX>& sm) {
+  const uint16_t* __restrict__ x = a.x;
+  const float* __restrict__ rin = a.rin;
+  const uint32_t* __restrict__ code = a.code;
+  const float* __restrict__ rout = a.rout;
+  const uint16_t* __restrict__ bias = a.bias;
+  const int M = a.M, TK = a.TK, TN = a.TN, KS = a.KS, R = a.R, S = a.S;
+  const float rs = a.rs;
+  float* __restrict__ part = a.part;
+  int* __restrict__ cnt = a.cnt;
+  uint16_t* __restrict__ y = a.y;
   using G = Geo<K>;
   constexpr int TPS = 16 / G::LPT;
   constexpr int kCols = G::TPW * 16;  // columns per column group
   constexpr int kBlocks = kCols / 128;  // 128-column blocks per group
   constexpr bool kMma = RMAX > 1;
-  __shared__ uint16_t s_lut[LUT ? 65536 : 1];
-  __shared__ __attribute__((aligned(16))) uint32_t s_x[RMAX][8 * 64];  // up to 64 kt per row
-  __shared__ float s_red[kMma ? 1 : 4][64][G::NCOL];
-  __shared__ float s_sum[2][kCols];
-  __shared__ int s_last;
+  uint16_t* s_lut = sm.lut;
+  auto& s_x = sm.x;
+  auto& s_red = sm.red;
+  auto& s_sum = sm.sum;
+  int& s_last = sm.last;
   stage_lut<LUT>(s_lut);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int ntg = blockIdx.x, row0 = blockIdx.y * R, z = blockIdx.z, S = gridDim.z;
+  const int row0 = rg * R;
   const int IC = TK * 16, OC = TN * 16;
   const int nb = KS / 8;  // 128-input blocks of the block's kt range
   const size_t kstride = (size_t)TN * (8 * K);
@@ -128,7 +161,7 @@ __global__ __launch_bounds__(256) void k_linear_small(
   __syncthreads();
   // 3. the last split of (row group, column group) finishes the columns
   if (threadIdx.x == 0) {
-    int* cn = &cnt[(size_t)blockIdx.y * gridDim.x + ntg];
+    int* cn = &cnt[(size_t)rg * a.groups + ntg];
     const bool last = add_relaxed(cn, 1) == S - 1;
     if (last) __hip_atomic_store(cn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = last;
@@ -180,6 +213,43 @@ __global__ __launch_bounds__(256) void k_linear_small(
       yr[1] = __builtin_bit_cast(uint16_t, y1);
     }
     __syncthreads();
+  }
+}
+
+
+template <int K, bool LUT, int RMAX>
+__global__ __launch_bounds__(256) void k_linear_small(LinearSmallArgs a) {
+  __shared__ LinearSmallSmem<K, LUT, RMAX> sm;
+  linear_small_body<K, LUT, RMAX>(a, blockIdx.x, blockIdx.y, blockIdx.z, sm);
+}
+
+// Two projections of the same input rows in one launch (the projection-pair
+// dispatch of escha_mlx/dense.py:365-437): the flat grid holds projection
+// 0's workgroups, then projection 1's, each running exactly the single
+// projection's plan (its own column groups, splits, partials and counters),
+// so each output is bit-identical to its own k_linear_small launch.  The two
+// projections' LDS layouts share one allocation.
+template <int K0, int K1, bool LUT, int RMAX>
+__global__ __launch_bounds__(256) void k_linear_pair(LinearSmallArgs a0, LinearSmallArgs a1) {
+  __shared__ union {
+    LinearSmallSmem<K0, LUT, RMAX> p0;
+    LinearSmallSmem<K1, LUT, RMAX> p1;
+  } sm;
+  const int n0 = a0.groups * a0.row_groups * a0.S;
+  const bool first = (int)blockIdx.x < n0;
+  const int b = first ? (int)blockIdx.x : (int)blockIdx.x - n0;
+  if constexpr (K0 == K1) {
+    // one body, its arguments chosen per workgroup (two inlined copies of the
+    // same body would spill)
+    const LinearSmallArgs& a = first ? a0 : a1;
+    const int gr = a.groups * a.row_groups;
+    linear_small_body<K0, LUT, RMAX>(a, b % a.groups, (b % gr) / a.groups, b / gr, sm.p0);
+  } else if (first) {
+    const int gr = a0.groups * a0.row_groups;
+    linear_small_body<K0, LUT, RMAX>(a0, b % a0.groups, (b % gr) / a0.groups, b / gr, sm.p0);
+  } else {
+    const int gr = a1.groups * a1.row_groups;
+    linear_small_body<K1, LUT, RMAX>(a1, b % a1.groups, (b % gr) / a1.groups, b / gr, sm.p1);
   }
 }
 

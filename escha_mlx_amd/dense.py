@@ -137,6 +137,7 @@ class EschaLinear(torch.nn.Module):
         self._block_r_pin = envs.dense_block_r_pin()
         self._mat = envs.dense_mat()
         self._ws = {}  # zero-filled one-launch workspaces per (rows, device)
+        self._pair_ws = {}  # the same for project_pair with this linear first
 
     @property
     def K(self) -> int:
@@ -183,6 +184,73 @@ class EschaLinear(torch.nn.Module):
         if self.bias is not None:
             y = (y.float() + self.bias.float()).to(torch.float16)
         return y.reshape(*shape[:-1], w.OC).to(x.dtype)
+
+
+def project_pair(first: EschaLinear, second: EschaLinear, x: torch.Tensor):
+    """Two coded projections of the same input in one dispatch
+    (escha_mlx/dense.py:365-437): (first(x), second(x)), each bit-identical
+    to its own call.  Pairs that do not share the input width or the latched
+    decode mode, or that run the order-exact or pinned-R kernels, take two
+    calls, as in the reference.  Unlike the reference, one row is fused too:
+    the pair launch runs each projection's own one-launch plan, so nothing
+    is traded for the saved launch."""
+    w0, w1 = first._w, second._w
+    shape = x.shape
+    rows = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
+    m = rows.shape[0]
+    compatible = (
+        w0.IC == w1.IC == rows.shape[-1]
+        and first._lut == second._lut
+        and not (first._exact or second._exact)
+        and first._block_r_pin is None and second._block_r_pin is None
+        and (m < ops.LINEAR_SMALL_ROWS or (first._mat and second._mat))
+    )
+    if not compatible:
+        return first(x), second(x)
+    key = (m, rows.device, id(second))
+    ws = first._pair_ws.get(key)
+    if ws is None:
+        need = ops.linear_pair_workspace(m, w0.K, w1.K, w0.IC, w0.OC, w1.OC)
+        ws = first._pair_ws[key] = torch.zeros(max(need, 4), dtype=torch.uint8, device=rows.device)
+    y0, y1 = ops.linear_pair(rows, (w0.code, w0.rin, w0.rout, w0.K, w0.OC, first.bias),
+                             (w1.code, w1.rin, w1.rout, w1.K, w1.OC, second.bias),
+                             lut=first._lut, ws=ws)
+    return (y0.reshape(*shape[:-1], w0.OC).to(x.dtype), y1.reshape(*shape[:-1], w1.OC).to(x.dtype))
+
+
+class EschaMLP(torch.nn.Module):
+    """A dense SwiGLU MLP over coded projections with one dispatch for gate and
+    up (the fused MLP of escha_mlx/models/qwen3_5.py:63-87):
+    down(f16(silu(gate(x)) * up(x))), the activation in float32 with one f16
+    rounding."""
+
+    def __init__(self, gate_proj: EschaLinear, up_proj: EschaLinear,
+                 down_proj: EschaLinear) -> None:
+        super().__init__()
+        if gate_proj._w.OC != up_proj._w.OC or down_proj._w.IC != gate_proj._w.OC:
+            raise ValueError("gate/up [IC -> I] and down [I -> OC] shapes disagree")
+        self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape
+        gate, up = project_pair(self.gate_proj, self.up_proj, x)
+        g = gate.reshape(-1, gate.shape[-1]).to(torch.float16).contiguous()
+        u = up.reshape(-1, up.shape[-1]).to(torch.float16).contiguous()
+        h = ops.moe_shared_act(g, u)
+        return self.down_proj(h).reshape(*shape[:-1], self.down_proj._w.OC).to(x.dtype)
+
+
+class EschaKVProjection(torch.nn.Module):
+    """k and v of an attention layer in one dispatch (the k/v pair of
+    escha_mlx/models/qwen3_5.py:90-170; the attention itself is the caller's):
+    forward(x) -> (k_proj(x), v_proj(x))."""
+
+    def __init__(self, k_proj: EschaLinear, v_proj: EschaLinear) -> None:
+        super().__init__()
+        self.k_proj, self.v_proj = k_proj, v_proj
+
+    def forward(self, x: torch.Tensor):
+        return project_pair(self.k_proj, self.v_proj, x)
 
 
 def build(group: dict, device="cuda") -> EschaLinear:

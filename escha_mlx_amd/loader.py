@@ -130,7 +130,7 @@ class LoadedCheckpoint:
         self.modules: dict[str, torch.nn.Module] = {}
         self.tensors: dict[str, np.ndarray] = {}
         self.escha_arrays: list[torch.Tensor] = []
-        self.n_layers = self.n_coded = self.n_q8 = self.n_bias = self.dropped = 0
+        self.n_layers = self.n_coded = self.n_q8 = self.n_bias = self.dropped = self.n_fused = 0
         self.rates: dict[int, int] = {}
 
     def __getitem__(self, path: str) -> torch.nn.Module:
@@ -332,7 +332,30 @@ class DenseCheckpointLoader(_Q8Mixin):
             ck.tensors[orig] = w
         self._bias.clear()
         ck.n_layers = self.n_layers
+        install_projection_fusion(ck)
         return ck
+
+
+def install_projection_fusion(ck: LoadedCheckpoint) -> int:
+    """One dispatch per projection pair of each decoder layer
+    (escha_mlx/models/qwen3_5.py:173-198): ``layers.N.mlp`` becomes a
+    ``dense.EschaMLP`` over coded gate/up/down, ``layers.N.self_attn.kv`` a
+    ``dense.EschaKVProjection`` over coded k/v.  The projections stay
+    available under their own paths.  Returns the number of groups installed."""
+    installed = 0
+    for i in range(ck.n_layers):
+        p = f"layers.{i}."
+        mlp = [ck.modules.get(p + f"mlp.{n}_proj") for n in ("gate", "up", "down")]
+        if all(isinstance(m, dense.EschaLinear) for m in mlp) and not isinstance(
+                ck.modules.get(p + "mlp"), dense.EschaMLP):
+            ck.modules[p + "mlp"] = dense.EschaMLP(*mlp)
+            installed += 1
+        kv = [ck.modules.get(p + f"self_attn.{n}_proj") for n in ("k", "v")]
+        if all(isinstance(m, dense.EschaLinear) for m in kv) and p + "self_attn.kv" not in ck.modules:
+            ck.modules[p + "self_attn.kv"] = dense.EschaKVProjection(*kv)
+            installed += 1
+    ck.n_fused = installed
+    return installed
 
 
 #: model_type -> plugin (escha_mlx/models/__init__.py:36-50).

@@ -231,6 +231,35 @@ def linear(x: torch.Tensor, code_u32: torch.Tensor, rin: torch.Tensor, rout: tor
     return y
 
 
+def linear_pair_workspace(m: int, K0: int, K1: int, IC: int, OC0: int, OC1: int) -> int:
+    return int(_lib.load().esc_linear_pair_workspace(m, K0, K1, IC, OC0, OC1))
+
+
+def linear_pair(x: torch.Tensor, p0: tuple, p1: tuple, lut: bool | None = None, rs: float = RS,
+                ws: torch.Tensor | None = None):
+    """Two coded linears over the same rows in one dispatch (dense.py:365-437):
+    p0 / p1 = (code_u32, rin, rout, K, OC, bias or None); returns (y0, y1),
+    each bit-identical to ``linear`` on its own.  ws must be zero-filled
+    before its first use."""
+    c0, rin0, rout0, K0, OC0, b0 = p0
+    c1, rin1, rout1, K1, OC1, b1 = p1
+    _dev(x, c0, rin0, rout0, b0, c1, rin1, rout1, b1)
+    m, IC = x.shape
+    if x.dtype != torch.float16:
+        raise ValueError("x must be float16")
+    y0 = torch.empty((m, OC0), dtype=torch.float16, device=x.device)
+    y1 = torch.empty((m, OC1), dtype=torch.float16, device=x.device)
+    if m == 0:
+        return y0, y1
+    need = linear_pair_workspace(m, K0, K1, IC, OC0, OC1)
+    if ws is None:
+        ws = torch.zeros(max(need, 4), dtype=torch.uint8, device=x.device)
+    _lib.call("esc_linear_pair", _ptr(x), m, IC, _ptr(rin0), _ptr(_as_u32(c0)), _ptr(rout0),
+              _ptr(b0), K0, OC0, _ptr(rin1), _ptr(_as_u32(c1)), _ptr(rout1), _ptr(b1), K1, OC1,
+              _lut_flag(lut), rs, _ptr(y0), _ptr(y1), _ptr(ws), ws.numel(), _stream())
+    return y0, y1
+
+
 def dense_gemm_rows_fast_out(xh: torch.Tensor, code_u32: torch.Tensor, rout: torch.Tensor,
                              K: int, IC: int, OC: int, R: int, rs: float = RS,
                              lut: bool | None = None) -> torch.Tensor:

@@ -126,6 +126,22 @@ int esc_linear(const uint16_t* x, const float* rin, const uint32_t* code, const 
                const uint16_t* bias, int M, int K, int IC, int OC, int use_lut, float rs,
                uint16_t* y, void* ws, size_t ws_bytes, void* stream);
 
+/* Two coded linears over the same rows x f16 [M][IC] in one dispatch:
+ * y0 = esc_linear(x; rin0, code0, rout0, bias0, K0, OC0) and likewise y1
+ * (K0 and K1 may differ), each bit-identical to its own esc_linear call.
+ * M < 16: one launch whose workgroups run either projection's plan; M >= 16:
+ * the two linears one after the other.  ws: esc_linear_pair_workspace bytes
+ * (projection 0's esc_linear workspace, then projection 1's), zero-filled
+ * before its first use.  Replaces dense.project_pair with msl.dense_gemm_pair
+ * / dense_gemm_pair_out and the pair transforms (escha_mlx/dense.py:365-437,
+ * escha_mlx/msl.py:1491-1527, 1873-1950): the gate/up and k/v projections. */
+size_t esc_linear_pair_workspace(int M, int K0, int K1, int IC, int OC0, int OC1);
+int esc_linear_pair(const uint16_t* x, int M, int IC, const float* rin0, const uint32_t* code0,
+                    const float* rout0, const uint16_t* bias0, int K0, int OC0, const float* rin1,
+                    const uint32_t* code1, const float* rout1, const uint16_t* bias1, int K1,
+                    int OC1, int use_lut, float rs, uint16_t* y0, uint16_t* y1, void* ws,
+                    size_t ws_bytes, void* stream);
+
 /* Dense GEMM for a few rows, tolerance contract: y f16 [M][OC] =
  * f16((H128(xh @ decode(code)) * rs) * rout), R rows (2, 4 or 8) per
  * workgroup share every decoded weight (one row per B column of

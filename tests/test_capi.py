@@ -220,3 +220,29 @@ def test_q8_embed_rejects_null_and_bad_sizes():
     assert rc == _lib.ESC_EINVAL and "N=0" in msg
     rc, _ = _rc_msg("esc_q8_embed", DUMMY, 0, DUMMY, DUMMY, 4, 32, DUMMY, None)
     assert rc == _lib.ESC_OK  # nothing to launch
+
+
+def test_linear_pair_rejections_and_workspace():
+    lib = _lib.load()
+    a = lib.esc_linear_workspace(4, 2, 1024, 384)
+    assert lib.esc_linear_pair_workspace(4, 2, 3, 1024, 384, 1280) == \
+        ((a + 255) & ~255) + lib.esc_linear_workspace(4, 3, 1024, 1280)
+    assert lib.esc_linear_pair_workspace(4, 4, 3, 1024, 384, 1280) == 0
+    args = [DUMMY, 4, 1024, DUMMY, DUMMY, DUMMY, None, 2, 384, DUMMY, DUMMY, DUMMY, None, 3, 1280,
+            0, 0.088, DUMMY, DUMMY, DUMMY, 1 << 30, None]
+    bad = list(args)
+    bad[13] = 4
+    rc, msg = _rc_msg("esc_linear_pair", *bad)
+    assert rc == _lib.ESC_EINVAL and "K=4" in msg
+    bad = list(args)
+    bad[14] = 1000
+    rc, msg = _rc_msg("esc_linear_pair", *bad)
+    assert rc == _lib.ESC_EINVAL and "multiples of 128" in msg
+    bad = list(args)
+    bad[18] = None
+    rc, msg = _rc_msg("esc_linear_pair", *bad)
+    assert rc == _lib.ESC_EINVAL and "null" in msg
+    bad = list(args)
+    bad[20] = 16
+    rc, msg = _rc_msg("esc_linear_pair", *bad)
+    assert rc == _lib.ESC_ENOSPACE and "workspace" in msg

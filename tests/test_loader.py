@@ -149,6 +149,12 @@ def test_dense_checkpoint_structure_and_fold(tmp_path, monkeypatch, leaf_shards)
     assert ck.n_bias == len(W.DENSE_PROJ) + 2
     assert ck.dropped == 2
     assert W.PFX + "layers.0.linear_attn.in_proj_a.weight" in ck.tensors
+    # projection fusion (qwen3_5.py:173-198): layer 0's coded MLP, layer 1's k/v
+    assert isinstance(ck["layers.0.mlp"], dense.EschaMLP)
+    assert ck["layers.0.mlp"].up_proj is ck["layers.0.mlp.up_proj"]
+    kv = ck["layers.1.self_attn.kv"]
+    assert isinstance(kv, dense.EschaKVProjection) and kv.v_proj is ck["layers.1.self_attn.v_proj"]
+    assert "layers.1.mlp" not in ck.modules and ck.n_fused == 2
 
 
 def real_corners():
