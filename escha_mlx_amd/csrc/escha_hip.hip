@@ -865,9 +865,14 @@ bool fused_eligible(int T, int top_k, int H, int I) {
 // in total the two-launch path uses the small size to fill the GPU.
 constexpr int kSmallItemsBelow = 0;
 
+// kt per item of the many-layer two-launch path (gate_up, down)
+// (measured on MI355X: 32 kt per item for either kernel is no faster)
+constexpr int kKtaLayers = 16, kKtbLayers = 16;
+
 FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput) {
   const bool large = throughput && L * T * top_k * (I / 128) * std::max(1, H / 256) >= kSmallItemsBelow;
-  const int kta = large ? 16 : 8, ktb = large ? 16 : 4;
+  const bool layers = large && L > 1;
+  const int kta = layers ? kKtaLayers : large ? 16 : 8, ktb = layers ? kKtbLayers : large ? 16 : 4;
   FusedPlan f;
   f.L = L;
   f.M = T * top_k;
@@ -933,9 +938,9 @@ int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
       return launched("k_moe_down_items");
     }
     if (p.L > 1) {
-      hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 16, true>), ga, blk, 0, s, p);
+      hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, kKtaLayers, true>), ga, blk, 0, s, p);
       if (int rc = launched("k_moe_gate_up_items")) return rc;
-      hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, 16, true>), gb, blk, 0, s, p);
+      hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, kKtbLayers, true>), gb, blk, 0, s, p);
       return launched("k_moe_down_items");
     }
     hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 16, false>), ga, blk, 0, s, p);

@@ -147,12 +147,24 @@ __device__ __forceinline__ ItemCode<K, NKT> load_item(const uint32_t* __restrict
 }
 
 // Decode + multiply the item (inputs: 8 f16-pair words per kt in s_x) and
+// The item kernels keep their inputs in LDS as the decode's input pairs:
+// per kt, word i (= xpair_index(r), r in {0,1,4,5,8,9,12,13}) holds
+// [x(r+2) | x(r)], so the decode reads them as they are (no per-step
+// permutes).  A lane holding the natural word [x(2j) | x(2j+1)] of kt-local
+// position j = lane % 8 writes the paired word of the same position: even j
+// [x(2j+2) | x(2j)], odd j [x(2j+1) | x(2j-1)], from its neighbour's word.
+__device__ __forceinline__ uint32_t paired_word(uint32_t w) {
+  const uint32_t nb = __builtin_bit_cast(uint32_t, lane_xor<1>(__builtin_bit_cast(float, w)));
+  return (threadIdx.x & 1) ? __builtin_amdgcn_perm(nb, w, 0x07060302u)
+                           : __builtin_amdgcn_perm(w, nb, 0x05040100u);
+}
+
 // publish its 256 float32 column partials to dst (device-coherent stores when
 // COH, for a consumer in the same launch; plain stores when the only consumer
 // runs in a later launch).
-template <int K, int NKT, bool WAIT = true, bool COH = true>
-__device__ __forceinline__ void compute_item(const ItemCode<K, NKT>& code, const uint32_t* s_x,
-                                             float (*s_red)[64][4], float* __restrict__ dst) {
+template <int K, int NKT, bool WAIT = true, bool COH = true, bool STORE = true>
+__device__ __forceinline__ float compute_item(const ItemCode<K, NKT>& code, const uint32_t* s_x,
+                                              float (*s_red)[64][4], float* __restrict__ dst) {
   using G = Geo<K>;
   using IG = ItemGeo<K, NKT>;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -165,12 +177,10 @@ __device__ __forceinline__ void compute_item(const ItemCode<K, NKT>& code, const
 #pragma unroll
   for (int k = 0; k < IG::NSTEP; ++k) {
     const int kl = wi * IG::NSTEP + k;
-    uint32_t xw[8];
+    uint32_t xp[8];  // the kt's input pairs, stored paired (paired_word)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) xw[j] = s_x[8 * kl + j];
+    for (int j = 0; j < 8; ++j) xp[j] = s_x[8 * kl + j];
     const uint32_t wprev = __shfl(code.w[k].w[G::WPL - 1], src);
-    uint32_t xp[8];
-    x_pairs(xw, xp);
     fast_tile_packed<K>(code.w[k], wprev, xp, acc);
   }
 #pragma unroll
@@ -184,14 +194,17 @@ __device__ __forceinline__ void compute_item(const ItemCode<K, NKT>& code, const
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < IG::WPG; ++w) v = v + s_red[gg * IG::WPG + w][ii * G::LPT + qq][ci];
-    if constexpr (COH)
-      st_coherent(dst + j, v);
-    else
-      dst[j] = v;
-  }
-  if constexpr (WAIT) {
-    wait_vm();
-    __syncthreads();
+    if constexpr (STORE) {
+      if constexpr (COH)
+        st_coherent(dst + j, v);
+      else
+        dst[j] = v;
+    }
+    if constexpr (WAIT) {
+      wait_vm();
+      __syncthreads();
+    }
+    return v;
   }
 }
 
@@ -236,19 +249,19 @@ __device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, K
     float v0 = (float)__builtin_bit_cast(half_t, xr[0]) * ri[0];
     float v1 = (float)__builtin_bit_cast(half_t, xr[1]) * ri[1];
     h128_wave(v0, v1);
-    s_x[64 * wave + lane] = pack2(to_f16(v0 * kRS), to_f16(v1 * kRS));
+    s_x[64 * wave + lane] = paired_word(pack2(to_f16(v0 * kRS), to_f16(v1 * kRS)));
   }
   __syncthreads();
   compute_item<K, KTA, PUBLISH, COH>(code, s_x, s_red, p.partA + ((size_t)l * p.nA + a) * 256);
   if (PUBLISH && threadIdx.x == 0) publish_gate_up(p, l, a);
 }
 
-// h-block kb of row r (layer l) -> this lane's pair of its 128 down inputs
-// (f16 pair, columns 128kb + 2lane, +1): the gate_up partials summed in fixed
+// h-block kb of row r (layer l) -> this lane's word of its 128 down inputs
+// (columns 128kb + 2lane, +1, stored as paired_word): the gate_up partials summed in fixed
 // kc order, the gate_up output transform, SwiGLU and the down input transform.
 // COH: the partials were published in this launch (device-coherent loads);
 // otherwise by an earlier launch (plain loads, which may hit L2).
-template <bool COH = true>
+template <bool COH = true, int CH = 8>
 __device__ uint32_t h_pair(const FusedMoe& p, int l, int r, int kb) {
   const int lane = threadIdx.x & 63;
   const MoeLayer& L = p.layer(l);
@@ -256,10 +269,10 @@ __device__ uint32_t h_pair(const FusedMoe& p, int l, int r, int kb) {
   const float* base =
       p.partA + ((size_t)l * p.nA + (size_t)(r * p.NB + kb) * p.NKC) * 256 + 2 * lane;
   float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
-  for (int kc0 = 0; kc0 < p.NKC; kc0 += 8) {
-    float2 gv[8], uv[8];
+  for (int kc0 = 0; kc0 < p.NKC; kc0 += CH) {
+    float2 gv[CH], uv[CH];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < CH; ++j)
       if (kc0 + j < p.NKC) {
         if constexpr (COH) {
           gv[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256);
@@ -270,7 +283,7 @@ __device__ uint32_t h_pair(const FusedMoe& p, int l, int r, int kb) {
         }
       }
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < CH; ++j)
       if (kc0 + j < p.NKC) {
         g0 = g0 + gv[j].x;
         g1 = g1 + gv[j].y;
@@ -288,10 +301,10 @@ __device__ uint32_t h_pair(const FusedMoe& p, int l, int r, int kb) {
   float v0 = (float)h0 * ri[0];
   float v1 = (float)h1 * ri[1];
   h128_wave(v0, v1);
-  return pack2(to_f16(v0 * kRS), to_f16(v1 * kRS));
+  return paired_word(pack2(to_f16(v0 * kRS), to_f16(v1 * kRS)));
 }
 
-// h-block kb of row r (layer l) -> its 128 down inputs (f16 pairs) in s_x[0..63].
+// h-block kb of row r (layer l) -> its 128 down inputs (paired words) in s_x[0..63].
 template <bool COH = true>
 __device__ void down_inputs(const FusedMoe& p, int l, int r, int kb, uint32_t* s_x) {
   s_x[threadIdx.x & 63] = h_pair<COH>(p, l, r, kb);
