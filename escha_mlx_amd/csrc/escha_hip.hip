@@ -868,11 +868,14 @@ constexpr int kSmallItemsBelow = 0;
 // kt per item of the many-layer two-launch path (gate_up, down)
 // (measured on MI355X: 32 kt per item for either kernel is no faster)
 constexpr int kKtaLayers = 16, kKtbLayers = 16;
+// kt per item of one token-layer (latency-bound)
+constexpr int kKtaSingle = 16, kKtbSingle = 16;
 
 FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput) {
   const bool large = throughput && L * T * top_k * (I / 128) * std::max(1, H / 256) >= kSmallItemsBelow;
   const bool layers = large && L > 1;
-  const int kta = layers ? kKtaLayers : large ? 16 : 8, ktb = layers ? kKtbLayers : large ? 16 : 4;
+  const int kta = layers ? kKtaLayers : large ? kKtaSingle : 8;
+  const int ktb = layers ? kKtbLayers : large ? kKtbSingle : 4;
   FusedPlan f;
   f.L = L;
   f.M = T * top_k;
@@ -931,7 +934,10 @@ int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
     // inputs are precomputed once per (row, h-block) for multi-layer calls
     (void)grid;
     const dim3 ga(p.L * p.nA), gb(p.L * p.nB), blk(esc::kFusedThreads);
-    if (p.NKC == p.H / 128) {
+    // the plan's item sizes: small (below kSmallItemsBelow items), many
+    // layers, or one token-layer
+    const int kta = p.H / (16 * p.NKC), ktb = p.I / (16 * p.NKB);
+    if (kta == 8 && ktb == 4) {
       hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 8, false>), ga, blk, 0, s, p);
       if (int rc = launched("k_moe_gate_up_items")) return rc;
       hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, 4, false>), gb, blk, 0, s, p);
@@ -943,9 +949,9 @@ int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
       hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, kKtbLayers, true>), gb, blk, 0, s, p);
       return launched("k_moe_down_items");
     }
-    hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 16, false>), ga, blk, 0, s, p);
+    hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, kKtaSingle, false>), ga, blk, 0, s, p);
     if (int rc = launched("k_moe_gate_up_items")) return rc;
-    hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, 16, false>), gb, blk, 0, s, p);
+    hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, kKtbSingle, false>), gb, blk, 0, s, p);
     return launched("k_moe_down_items");
   } else {
     hipLaunchKernelGGL((esc::k_moe_fused<KG, KD, 8, 4, true>), dim3(grid),
