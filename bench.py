@@ -109,11 +109,13 @@ def route_sets(torch, layers):
 
 
 def cpu_baseline(sample):
-    """The NumPy oracle (decode + transforms + f32 matmul, no weight cache), one BLAS thread."""
+    """The NumPy oracle (decode + transforms + f32 matmul, no weight cache), one
+    BLAS thread.  Returns the baseline record and the oracle's outputs, which
+    also check the GPU's outputs for the same token-layers."""
     from threadpoolctl import threadpool_limits
 
     from oracle import ref_np
-    t_total = 0.0
+    t_total, outs = 0.0, []
     with threadpool_limits(limits=1):
         for L in sample:
             t0 = time.perf_counter()
@@ -121,7 +123,8 @@ def cpu_baseline(sample):
             w_dn = {e: ref_np.reconstruct(L["dn"][e], I, H, K) for e in L["ids"][0]}
             gu = {"w": w_gu, "rin": L["gu_rin"], "rout": L["gu_rout"]}
             dn = {"w": w_dn, "rin": L["dn_rin"], "rout": L["dn_rout"]}
-            ref_np.moe_routed(L["x"], L["ids"], L["scores"], gu, dn, K, K, ordered=False)
+            outs.append(ref_np.moe_routed(L["x"], L["ids"], L["scores"], gu, dn, K, K,
+                                          ordered=False))
             t_total += time.perf_counter() - t0
     per = t_total / len(sample)
     return {"value": round(BYTES_TOKEN_LAYER / per / 1e9, 4), "unit": "GB/s", "cores": 1,
@@ -129,7 +132,50 @@ def cpu_baseline(sample):
             "sample": f"{len(sample)} token-layers of config 3 (distinct layer x routing pairs) "
                       f"through oracle/ref_np.py: vectorised decode of 8 experts x 2 legs, no "
                       f"cache, f32 matmul, 1 BLAS thread; {per * 1e3:.1f} ms per token-layer, "
-                      f"{t_total:.1f} s total"}
+                      f"{t_total:.1f} s total"}, outs
+
+
+def parity_check(torch, ops, routes, sample, want):
+    """The GPU's outputs for the sampled token-layers against the oracle's
+    (max |diff|, and max |diff| / max |want|), and one sampled expert's gate_up
+    stream decoded on the GPU against the oracle's decode (bit-exact)."""
+    from oracle import ref_np
+    dev = "cuda:0"
+    ws = torch.zeros(ops.moe_expert_path_workspace(1, TOP_K, E, H, I), dtype=torch.uint8,
+                     device=dev)
+    max_abs, max_rel = 0.0, 0.0
+    for L, w in zip(sample, want):
+        R = routes[L["set"]][L["layer"]]
+        y = ops.moe_expert_path(R["x"], R["ids"], R["scores"], R["gu_code"], R["gu_rin"],
+                                R["gu_rout"], K, R["dn_code"], R["dn_rin"], R["dn_rout"], K,
+                                ws=ws).cpu().numpy().astype(np.float64)
+        d = np.abs(y - w.astype(np.float64)).max()
+        max_abs = max(max_abs, float(d))
+        max_rel = max(max_rel, float(d / np.abs(w.astype(np.float64)).max()))
+    L0 = sample[0]
+    e0 = int(L0["ids"][0][0])
+    R0 = routes[L0["set"]][L0["layer"]]
+    got = ops.decode_tiles(R0["gu_code"][e0].contiguous(), K, H, 2 * I).cpu().numpy()
+    ref = ref_np.reconstruct(L0["gu"][e0], H, 2 * I, K)
+    return {"decode_bit_exact": bool(np.array_equal(got.view(np.uint16), ref.view(np.uint16))),
+            "decoded": f"gate_up stream of expert {e0} ({H}x{2 * I}, K={K})",
+            "max_abs_err": max_abs, "max_rel_err": round(max_rel, 6),
+            "tolerance": "max |diff| / max |oracle| < 5e-3 (reassociated float32 sums)",
+            "token_layers": len(sample)}
+
+
+def measured_roofline(torch, dev, stream):
+    """This box's streaming rates: a 1 GiB device copy (bytes read + written)
+    and a read-only reduction over 1 GiB (torch's own kernels)."""
+    src = torch.zeros(COPY_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    ms_copy = timed(torch, lambda i: dst.copy_(src), 10, 2, stream)
+    del dst
+    f = src.view(torch.float32)
+    ms_read = timed(torch, lambda i: f.sum(), 10, 2, stream)
+    del src, f
+    return {"copy_gbs": round(2 * COPY_BYTES / (ms_copy * 1e-3) / 1e9, 1),
+            "read_gbs": round(COPY_BYTES / (ms_read * 1e-3) / 1e9, 1)}
 
 
 def cpu_sample(routes, n: int):
@@ -142,7 +188,8 @@ def cpu_sample(routes, n: int):
         def sel(t):
             rows = {int(e): t[int(e)].cpu().numpy() for e in ids[0]}
             return {e: (a.view(np.uint32) if a.dtype == np.int32 else a) for e, a in rows.items()}
-        out.append({"gu": sel(L["gu_code"]), "dn": sel(L["dn_code"]),
+        out.append({"set": (i // len(routes[0])) % ROUTE_SETS, "layer": i % len(routes[0]),
+                    "gu": sel(L["gu_code"]), "dn": sel(L["dn_code"]),
                     "gu_rin": sel(L["gu_rin"]), "dn_rin": sel(L["dn_rin"]),
                     "gu_rout": sel(L["gu_rout"]), "dn_rout": sel(L["dn_rout"]),
                     "ids": ids, "scores": L["scores"].cpu().numpy(), "x": L["x"].cpu().numpy()})
@@ -657,8 +704,17 @@ def main():
             result.update({"value": round(gbs_c, 2), "ms_per_step": round(ms_c, 4)})
     result["wall_s"] = round(time.perf_counter() - t_wall, 3)
 
+    if "value" in result:
+        mr = measured_roofline(torch, dev, stream)
+        best = max(mr["copy_gbs"], mr["read_gbs"])
+        result["measured_roofline"] = dict(mr, gbs=best, how="the faster of a 1 GiB device copy "
+                                           "(bytes read + written) and a 1 GiB float32 sum "
+                                           "(bytes read), torch kernels, same box")
+        result["pct_measured_roofline"] = round(100 * result["value"] / best, 2)
     if not args.no_cpu and args.cpu_sample > 0:
-        result["cpu_baseline"] = cpu_baseline(cpu_sample(routes, args.cpu_sample))
+        sample = cpu_sample(routes, args.cpu_sample)
+        result["cpu_baseline"], want = cpu_baseline(sample)
+        result["parity"] = parity_check(torch, ops, routes, sample, want)
     print(json.dumps(result))
 
 
