@@ -571,8 +571,9 @@ def bench_q8_head(args, torch, ops):
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": "int8 weights -> f16 (w8a16 contract), f32 accumulate",
             "data": "synthetic: uniform int8, U[1e-3, 5e-3] scales, x ~ N(0,1) f16",
-            "config": {"workload": "not a BASELINE config: 248320x2048 w8a16 head (k_rows_gemv), "
-                                   "M=1 and M=8, 2 weight copies rotated"},
+            "config": {"workload": "not a BASELINE config: 248320x2048 w8a16 head, M=1 "
+                                   "(k_rows_gemv) and M=8 (k_rows_w8_mma), 2 weight copies "
+                                   "rotated"},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": 8000.0, "unit": "GB/s",
                          "frac": round(gbs / 8000.0, 4), "traffic": None,
                          "kernel": "k_rows_gemv<true,1,64,2>", "bytes_per_launch": nbytes},

@@ -707,6 +707,29 @@ int rows_by_geo(RowsGeo g, const uint16_t* x, const void* w, const float* scale,
   }
 }
 
+// int8 weights and 2..16 rows per launch: k_rows_w8_mma, the rows' products on
+// the matrix core (x staged in LDS, at most kW8MmaLds bytes per workgroup)
+constexpr int kW8MmaLds = 64 * 1024;
+int w8_mma_rows(int M, int K) {
+  if (M < 2 || K % 64) return 0;
+  return std::min(16, kW8MmaLds / (2 * K + 16));
+}
+
+int rows_w8_mma(const uint16_t* x, const void* w, const float* scale, int M, int K, int O,
+                uint16_t* y, int nr, hipStream_t s) {
+  const int groups = (O + 15) / 16;
+  for (int m0 = 0; m0 < M; m0 += nr) {
+    const int mr = std::min(nr, M - m0);
+    const size_t lds = (size_t)mr * (2 * K + 16);
+    const int per_cu = (int)std::max<size_t>(1, std::min<size_t>(8, 160 * 1024 / lds));
+    const int blocks = std::min((groups + 3) / 4, per_cu * device_cus());
+    hipLaunchKernelGGL(esc::k_rows_w8_mma, dim3(blocks), dim3(256), lds, s, x + (size_t)m0 * K,
+                       static_cast<const int8_t*>(w), scale, mr, K, O, y + (size_t)m0 * O, O);
+    if (int rc = launched("k_rows_w8_mma")) return rc;
+  }
+  return ESC_OK;
+}
+
 template <bool Q8>
 int rows_gemv(const uint16_t* x, const void* w, const float* scale, int M, int K, int O,
               uint16_t* y, hipStream_t s) {
@@ -714,6 +737,9 @@ int rows_gemv(const uint16_t* x, const void* w, const float* scale, int M, int K
   const int chunks = K / cw;
   ESC_REQUIRE(K > 0 && K % cw == 0 && chunks >= 8 && chunks <= 64 * kRowsMaxCpl,
               "K=%d: need a multiple of %d in [%d, %d]", K, cw, 8 * cw, 64 * kRowsMaxCpl * cw);
+  if constexpr (Q8) {
+    if (const int nr = w8_mma_rows(M, K); nr >= 2) return rows_w8_mma(x, w, scale, M, K, O, y, nr, s);
+  }
   const RowsGeo g = rows_geo(chunks);
   const int nr_max = rows_nr_max(Q8, g.cpl);
   for (int m0 = 0; m0 < M; m0 += nr_max) {

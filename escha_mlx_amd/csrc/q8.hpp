@@ -164,6 +164,78 @@ __global__ __launch_bounds__(256) void k_rows_gemv(const uint16_t* __restrict__ 
   }
 }
 
+// w8a16 GEMV for 2..16 rows of x on the matrix core: y[m][o] = f16(sum_k
+// x[m][k] * wf[o][k]), wf = f16(f32(w8) * scale[o]) (the contract rounding, as
+// k_rows_gemv).  A wave owns 16 output channels at a time and walks all of K in
+// steps of 64: lane l reads 16 int8 of channel o0 + l % 16 at k0 + 16 (l / 16),
+// converts them, and the two halves are the A operands of two
+// v_mfma_f32_16x16x32_f16 (A slot 8g + t <-> k0 + 16g + t, second half +8);
+// the B operands are the same k of token l % 16 from x staged in LDS (rows at a
+// 16-byte-padded pitch, so the 16 tokens of a lane group hit different banks).
+// Every product of a channel lands in one accumulator: no lane reduction.  D
+// lane l: token l % 16, channels o0 + 4 (l / 16) + r.  K a multiple of 64;
+// dynamic LDS = M x (2K + 16) bytes; grid: any; block 256.
+__global__ __launch_bounds__(256) void k_rows_w8_mma(const uint16_t* __restrict__ x,
+                                                     const int8_t* __restrict__ w8,
+                                                     const float* __restrict__ scale, int M,
+                                                     int K, int O, uint16_t* __restrict__ y,
+                                                     int ldy) {
+  extern __shared__ uint4 s_xm[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int pitch = K / 8 + 1;  // 16-byte units per staged row
+  for (int i = threadIdx.x; i < M * (K / 8); i += 256) {
+    const int r = i / (K / 8), c = i % (K / 8);
+    s_xm[r * pitch + c] = *reinterpret_cast<const uint4*>(x + (size_t)r * K + 8 * c);
+  }
+  __syncthreads();
+  const int j = lane & 15, g = lane >> 4;
+  const uint4* xb = s_xm + (size_t)min(j, M - 1) * pitch + 2 * g;  // token j, k0 + 16g
+  const int ngroups = (O + 15) / 16, nwaves = gridDim.x * 4;
+  for (int grp = blockIdx.x * 4 + wave; grp < ngroups; grp += nwaves) {
+    const int oc = min(grp * 16 + j, O - 1);  // in-bounds reads for a partial last group
+    const float s = scale[oc], ms = -128.f * s;
+    const uint4* wr = reinterpret_cast<const uint4*>(w8 + (size_t)oc * K + 16 * g);
+    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    auto step = [&](const uint4 wc, int k0) {
+      u32x4_t a0, a1;
+      uint32_t p0, p1;
+      w8_to_f16x4(wc.x, s, ms, p0, p1);
+      a0[0] = p0;
+      a0[1] = p1;
+      w8_to_f16x4(wc.y, s, ms, p0, p1);
+      a0[2] = p0;
+      a0[3] = p1;
+      w8_to_f16x4(wc.z, s, ms, p0, p1);
+      a1[0] = p0;
+      a1[1] = p1;
+      w8_to_f16x4(wc.w, s, ms, p0, p1);
+      a1[2] = p0;
+      a1[3] = p1;
+      const uint4 b0 = xb[k0 / 8], b1 = xb[k0 / 8 + 1];
+      acc = mma16(a0, __builtin_bit_cast(u32x4_t, b0), acc);
+      acc = mma16(a1, __builtin_bit_cast(u32x4_t, b1), acc);
+    };
+    // two 64-k steps per iteration, the next two requested before these are used
+    uint4 n0 = wr[0], n1 = wr[K > 64 ? 4 : 0];
+    for (int k0 = 0; k0 < K; k0 += 128) {
+      const uint4 c0 = n0, c1 = n1;
+      if (k0 + 128 < K) {
+        n0 = wr[(k0 + 128) / 16];
+        n1 = wr[(k0 + 192 < K ? k0 + 192 : k0 + 128) / 16];
+      }
+      step(c0, k0);
+      if (k0 + 64 < K) step(c1, k0 + 64);
+    }
+    if (j < M) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = grp * 16 + 4 * g + r;
+        if (o < O) y[(size_t)j * ldy + o] = __builtin_bit_cast(uint16_t, to_f16(acc[r]));
+      }
+    }
+  }
+}
+
 // Embedding rows of an int8 table (escha_mlx/quant.py:253-266 under the w8a16
 // contract): out[t][k] = f16(f32(w8[ids[t]][k]) * f32(scale[ids[t]])), the
 // same rounding as the GEMV's weights.  An id outside [0, N) yields a row of
