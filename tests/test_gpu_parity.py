@@ -173,6 +173,22 @@ def test_gemm_rows_bit_identical_to_per_row(R_):
     assert np.array_equal(mid[:m].view(np.uint32), per_row.view(np.uint32))
 
 
+@pytest.mark.parametrize("m", [1, 63, 64, 65, 256, 1000, 1025, 2500])
+@pytest.mark.parametrize("E,R_", [(8, 2), (256, 8), (256, 3)])
+def test_build_groups_matches_oracle(m, E, R_):
+    """Stable expert grouping across waves and 1024-row chunks (rows of one
+    expert keep their order) against the oracle's brute-force model."""
+    from escha_mlx_amd import moe
+    rng = np.random.default_rng(m * 7 + E + R_)
+    re = rng.integers(0, E, size=m).astype(np.int32)
+    re[: m // 3] = E - 1  # skew: one expert owns a third of the rows
+    ng = moe.n_groups_bound(m, E, R_)
+    rows_idx, group_expert = moe.build_groups(torch.from_numpy(re).to(DEV), E, R_, ng)
+    ri, ge = R.build_groups(re, E, R_, ng)
+    assert np.array_equal(rows_idx.cpu().numpy(), ri)
+    assert np.array_equal(group_expert.cpu().numpy(), ge)
+
+
 @pytest.mark.parametrize("R_", [1, 2, 4, 8, 16])
 @pytest.mark.parametrize("m", [1, 5, 17])
 def test_dense_rows_bit_identical_to_gemv(R_, m):
