@@ -146,7 +146,6 @@ __device__ __forceinline__ ItemCode<K, NKT> load_item(const uint32_t* __restrict
   return c;
 }
 
-// Decode + multiply the item (inputs: 8 f16-pair words per kt in s_x) and
 // The item kernels keep their inputs in LDS as the decode's input pairs:
 // per kt, word i (= xpair_index(r), r in {0,1,4,5,8,9,12,13}) holds
 // [x(r+2) | x(r)], so the decode reads them as they are (no per-step
@@ -159,6 +158,7 @@ __device__ __forceinline__ uint32_t paired_word(uint32_t w) {
                            : __builtin_amdgcn_perm(w, nb, 0x05040100u);
 }
 
+// Decode + multiply the item (inputs: 8 f16-pair words per kt in s_x) and
 // publish its 256 float32 column partials to dst (device-coherent stores when
 // COH, for a consumer in the same launch; plain stores when the only consumer
 // runs in a later launch).
