@@ -894,21 +894,28 @@ constexpr int kSmallItemsBelow = 0;
 // kt per item of the many-layer two-launch path (gate_up, down)
 // (measured on MI355X: 32 kt per item for either kernel is no faster)
 constexpr int kKtaLayers = 16, kKtbLayers = 16;
-// kt per item of one token-layer (latency-bound)
+// kt per item of one token-layer (latency-bound); with I == 512 the down
+// items are 128-column blocks over all 32 kt (k_moe_down_blocks)
 constexpr int kKtaSingle = 16, kKtbSingle = 16;
+constexpr int kKtbBlocks = 32;
+// waves per gate_up / block down item of one token-layer, and per block
+// down item of many token-layers
+constexpr int kGateUpWavesSingle = 16, kDownBlockWavesSingle = 16;
+constexpr int kDownBlockWavesLayers = 4;
 
 FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput) {
   const bool large = throughput && L * T * top_k * (I / 128) * std::max(1, H / 256) >= kSmallItemsBelow;
   const bool layers = large && L > 1;
   const int kta = layers ? kKtaLayers : large ? kKtaSingle : 8;
-  const int ktb = layers ? kKtbLayers : large ? kKtbSingle : 4;
+  const bool blocks = large && I == 16 * kKtbBlocks;
+  const int ktb = blocks ? kKtbBlocks : layers ? kKtbLayers : large ? kKtbSingle : 4;
   FusedPlan f;
   f.L = L;
   f.M = T * top_k;
   f.NB = I / 128;
   f.NKC = std::max(1, H / (16 * kta));
   f.NKB = std::max(1, I / (16 * ktb));
-  f.NCP = H / 256;
+  f.NCP = ktb == kKtbBlocks ? H / 128 : H / 256;
   f.nA = f.M * f.NB * f.NKC;
   f.nB = f.M * f.NCP * f.NKB;
   f.grid = throughput ? std::min(L * std::max(f.nA, f.nB), 1024)
@@ -972,11 +979,22 @@ int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
     if (p.L > 1) {
       hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, kKtaLayers, true>), ga, blk, 0, s, p);
       if (int rc = launched("k_moe_gate_up_items")) return rc;
+      if (ktb == kKtbBlocks) {
+        hipLaunchKernelGGL((esc::k_moe_down_blocks<KG, KD, true, kDownBlockWavesLayers>), gb,
+                           dim3(64 * kDownBlockWavesLayers), 0, s, p);
+        return launched("k_moe_down_blocks");
+      }
       hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, kKtbLayers, true>), gb, blk, 0, s, p);
       return launched("k_moe_down_items");
     }
-    hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, kKtaSingle, false>), ga, blk, 0, s, p);
+    hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, kKtaSingle, false, kGateUpWavesSingle>), ga,
+                       dim3(64 * kGateUpWavesSingle), 0, s, p);
     if (int rc = launched("k_moe_gate_up_items")) return rc;
+    if (ktb == kKtbBlocks) {
+      hipLaunchKernelGGL((esc::k_moe_down_blocks<KG, KD, false, kDownBlockWavesSingle>), gb,
+                         dim3(64 * kDownBlockWavesSingle), 0, s, p);
+      return launched("k_moe_down_blocks");
+    }
     hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, kKtbSingle, false>), gb, blk, 0, s, p);
     return launched("k_moe_down_items");
   } else {

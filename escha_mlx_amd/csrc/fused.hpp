@@ -86,14 +86,14 @@ struct FusedMoe {
   uint16_t* xh2; // [L][M][I]   down inputs (two-launch path)
   int* cntA;     // [L][M*NB]  published gate_up items per (row, h-block)
   int* claimA;   // [L][nA]
-  int* cntB;     // [L][T*NCP] finished down items per (token, column pair)
+  int* cntB;     // [L][T*NCP] finished down items per (token, column pair or block)
   int* done;     // [1]
   int* err;      // [1] sticky: a spin bound was hit
   int L, T, top_k, H, I;
   int NB;   // I / 128        h-blocks
   int NKC;  // H / (16*KTA)   gate_up items per (row, h-block), <= 62
   int NKB;  // I / (16*KTB)   down items per (row, column pair)
-  int NCP;  // H / 256        column pairs
+  int NCP;  // H / 256        column pairs (H / 128 column blocks: k_moe_down_blocks)
   int nA, nB;  // items per layer
   __device__ __forceinline__ const MoeLayer& layer(int l) const { return layers ? layers[l] : l0; }
 };
@@ -114,33 +114,34 @@ __device__ __forceinline__ void col_owner(int c, int& q, int& ci) {
   }
 }
 
-// One item = 16 tiles x NKT kt of one stream.  Waves split the tiles into
-// 16/TPW groups and the kt range among the WPG waves of a group; each lane
-// holds its NSTEP kt-steps of code in VGPRs.
-template <int K, int NKT>
+// One item = 16 tiles x NKT kt of one stream, run by NW waves.  Waves split
+// the tiles into 16/TPW groups and the kt range among the WPG waves of a
+// group; each lane holds its NSTEP kt-steps of code in VGPRs.
+template <int K, int NKT, int NW = 4>
 struct ItemGeo {
   static constexpr int NG = 16 / Geo<K>::TPW;
-  static constexpr int WPG = 4 / NG;
+  static constexpr int WPG = NW / NG;
   static constexpr int NSTEP = NKT / WPG;
+  static_assert(NW % NG == 0 && NKT % WPG == 0, "item does not split over its waves");
 };
 
-template <int K, int NKT>
+template <int K, int NKT, int NW = 4>
 struct ItemCode {
-  LaneWords<K> w[ItemGeo<K, NKT>::NSTEP];
+  LaneWords<K> w[ItemGeo<K, NKT, NW>::NSTEP];
 };
 
-template <int K, int NKT, typename NtFn>
-__device__ __forceinline__ ItemCode<K, NKT> load_item(const uint32_t* __restrict__ code_e, int TN,
-                                                      int kt_base, NtFn nt_of) {
+template <int K, int NKT, int NW = 4, typename NtFn>
+__device__ __forceinline__ ItemCode<K, NKT, NW> load_item(const uint32_t* __restrict__ code_e,
+                                                          int TN, int kt_base, NtFn nt_of) {
   using G = Geo<K>;
-  using IG = ItemGeo<K, NKT>;
+  using IG = ItemGeo<K, NKT, NW>;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = wave / IG::WPG, wi = wave % IG::WPG;
   const int q = lane % G::LPT, i = lane / G::LPT;
   const size_t kstride = (size_t)TN * (8 * K);
   const uint32_t* lp = code_e + (size_t)nt_of(g * G::TPW + i) * (8 * K) + q * G::WPL +
                        (size_t)(kt_base + wi * IG::NSTEP) * kstride;
-  ItemCode<K, NKT> c;
+  ItemCode<K, NKT, NW> c;
 #pragma unroll
   for (int k = 0; k < IG::NSTEP; ++k) c.w[k] = load_lane_words<K>(lp + (size_t)k * kstride);
   return c;
@@ -158,15 +159,13 @@ __device__ __forceinline__ uint32_t paired_word(uint32_t w) {
                            : __builtin_amdgcn_perm(w, nb, 0x05040100u);
 }
 
-// Decode + multiply the item (inputs: 8 f16-pair words per kt in s_x) and
-// publish its 256 float32 column partials to dst (device-coherent stores when
-// COH, for a consumer in the same launch; plain stores when the only consumer
-// runs in a later launch).
-template <int K, int NKT, bool WAIT = true, bool COH = true, bool STORE = true>
-__device__ __forceinline__ float compute_item(const ItemCode<K, NKT>& code, const uint32_t* s_x,
-                                              float (*s_red)[64][4], float* __restrict__ dst) {
+// Decode + multiply the item (inputs: 8 f16-pair words per kt in s_x); each
+// wave leaves its lanes' column partials in s_red[wave].
+template <int K, int NKT, int NW = 4>
+__device__ __forceinline__ void item_to_lds(const ItemCode<K, NKT, NW>& code, const uint32_t* s_x,
+                                            float (*s_red)[64][4]) {
   using G = Geo<K>;
-  using IG = ItemGeo<K, NKT>;
+  using IG = ItemGeo<K, NKT, NW>;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wi = wave % IG::WPG;
   const int q = lane % G::LPT, i = lane / G::LPT;
@@ -185,36 +184,56 @@ __device__ __forceinline__ float compute_item(const ItemCode<K, NKT>& code, cons
   }
 #pragma unroll
   for (int c = 0; c < G::NCOL; ++c) s_red[wave][lane][c] = acc[c];
-  __syncthreads();
-  {
-    const int j = threadIdx.x, it = j >> 4, c = j & 15;
-    const int gg = it / G::TPW, ii = it % G::TPW;
-    int qq, ci;
-    col_owner<K>(c, qq, ci);
-    float v = 0.f;
+}
+
+// Column c (0..255) of an item after item_to_lds and a barrier: its wave
+// partials summed in wave order.
+template <int K, int NW = 4>
+__device__ __forceinline__ float item_col(const float (*s_red)[64][4], int c) {
+  using G = Geo<K>;
+  constexpr int WPG = NW / (16 / G::TPW);
+  const int it = c >> 4, gg = it / G::TPW, ii = it % G::TPW;
+  int qq, ci;
+  col_owner<K>(c & 15, qq, ci);
+  float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < IG::WPG; ++w) v = v + s_red[gg * IG::WPG + w][ii * G::LPT + qq][ci];
+  for (int w = 0; w < WPG; ++w) v = v + s_red[gg * WPG + w][ii * G::LPT + qq][ci];
+  return v;
+}
+
+// Decode + multiply an item and publish its 256 float32 column partials to
+// dst (device-coherent stores when COH, for a consumer in the same launch;
+// plain stores when the only consumer runs in a later launch).  Thread j < 256
+// returns column j.
+template <int K, int NKT, bool WAIT = true, bool COH = true, bool STORE = true, int NW = 4>
+__device__ __forceinline__ float compute_item(const ItemCode<K, NKT, NW>& code, const uint32_t* s_x,
+                                              float (*s_red)[64][4], float* __restrict__ dst) {
+  item_to_lds<K, NKT, NW>(code, s_x, s_red);
+  __syncthreads();
+  const int j = threadIdx.x;
+  float v = 0.f;
+  if (NW == 4 || j < 256) {
+    v = item_col<K, NW>(s_red, j);
     if constexpr (STORE) {
       if constexpr (COH)
         st_coherent(dst + j, v);
       else
         dst[j] = v;
     }
-    if constexpr (WAIT) {
-      wait_vm();
-      __syncthreads();
-    }
-    return v;
   }
+  if constexpr (WAIT) {
+    wait_vm();
+    __syncthreads();
+  }
+  return v;
 }
 
-
-template <int K, int KTA>
-__device__ __forceinline__ ItemCode<K, KTA> load_gate_up(const FusedMoe& p, int l, int a) {
+template <int K, int KTA, int NW = 4>
+__device__ __forceinline__ ItemCode<K, KTA, NW> load_gate_up(const FusedMoe& p, int l, int a) {
   const MoeLayer& L = p.layer(l);
   const int kc = a % p.NKC, rb = a / p.NKC, b = rb % p.NB, r = rb / p.NB;
   const int TK = p.H / 16, TN = 2 * p.I / 16, half_tn = p.I / 16;
-  return load_item<K, KTA>(L.gu_code + (size_t)L.ids[r] * TK * TN * (8 * K), TN, KTA * kc,
+  return load_item<K, KTA, NW>(L.gu_code + (size_t)L.ids[r] * TK * TN * (8 * K), TN, KTA * kc,
                            [&](int it) { return it < 8 ? 8 * b + it : half_tn + 8 * b + (it - 8); });
 }
 
@@ -235,8 +254,8 @@ __device__ __forceinline__ void publish_gate_up(const FusedMoe& p, int l, int a)
 
 // gate_up item a of layer l with its code already in flight: transform the
 // item's 16*KTA inputs (one wave per 128-block), decode + multiply, publish.
-template <int K, int KTA, bool PUBLISH = true, bool COH = true>
-__device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, KTA>& code,
+template <int K, int KTA, bool PUBLISH = true, bool COH = true, int NW = 4>
+__device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, KTA, NW>& code,
                             uint32_t* s_x, float (*s_red)[64][4]) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const MoeLayer& L = p.layer(l);
@@ -252,7 +271,8 @@ __device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, K
     s_x[64 * wave + lane] = paired_word(pack2(to_f16(v0 * kRS), to_f16(v1 * kRS)));
   }
   __syncthreads();
-  compute_item<K, KTA, PUBLISH, COH>(code, s_x, s_red, p.partA + ((size_t)l * p.nA + a) * 256);
+  compute_item<K, KTA, PUBLISH, COH, true, NW>(code, s_x, s_red,
+                                              p.partA + ((size_t)l * p.nA + a) * 256);
   if (PUBLISH && threadIdx.x == 0) publish_gate_up(p, l, a);
 }
 
@@ -451,16 +471,16 @@ __device__ __forceinline__ int xcd_item(int b, int n) {
 // token-layer, latency-bound) the partials go out with plain stores and each
 // down item derives its own inputs, which keeps the counter round trip off
 // the critical path.
-template <int KG, int KTA, bool PREH>
-__global__ __launch_bounds__(kFusedThreads, 4) void k_moe_gate_up_items(FusedMoe p) {
-  __shared__ float s_red[4][64][4];
+template <int KG, int KTA, bool PREH, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void k_moe_gate_up_items(FusedMoe p) {
+  __shared__ float s_red[NW][64][4];
   __shared__ uint32_t s_x[256];
   __shared__ int s_last;
   const int tid = threadIdx.x;
   const int g = xcd_item(blockIdx.x, gridDim.x);
   const int l = g / p.nA, a = g % p.nA;
-  const auto code = load_gate_up<KG, KTA>(p, l, a);
-  run_gate_up<KG, KTA, false, PREH>(p, l, a, code, s_x, s_red);
+  const auto code = load_gate_up<KG, KTA, NW>(p, l, a);
+  run_gate_up<KG, KTA, false, PREH, NW>(p, l, a, code, s_x, s_red);
   if constexpr (PREH) {
     wait_vm();  // this wave's partial stores have completed
     __syncthreads();
@@ -512,6 +532,153 @@ __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_down_items(FusedMoe p)
   }
   __syncthreads();
   if (s_flag) combine_tile(p, l, t, cp, s_d);
+}
+
+// Down items of one token-layer with I == 512 (k_moe_down_blocks): item
+// (row r, column block hb) covers output columns [128hb, 128hb+128) -- 8
+// tiles, one block of the output transform -- over all 32 kt, so no split-K
+// sum crosses blocks.  A K=2 wave-step spans 16 tile slots: slot i takes tile
+// i % 8 at kt 2s + i / 8 (two kt per step); a K=3 step spans the 8 tiles at one
+// kt.  NW waves split the steps.
+template <int K, int NW>
+struct BlockItem {
+  static constexpr int KPS = Geo<K>::TPW / 8;  // kt per wave-step
+  static constexpr int NSTEP = 32 / (KPS * NW);
+  static_assert(NSTEP * KPS * NW == 32, "32 kt do not split over the waves");
+};
+
+template <int K, int NW>
+struct BlockCode {
+  LaneWords<K> w[BlockItem<K, NW>::NSTEP];
+};
+
+template <int K, int NW>
+__device__ __forceinline__ BlockCode<K, NW> load_block_item(const uint32_t* __restrict__ code_e,
+                                                            int TN, int hb) {
+  using G = Geo<K>;
+  using BI = BlockItem<K, NW>;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int q = lane % G::LPT, i = lane / G::LPT;
+  const size_t kstride = (size_t)TN * (8 * K);
+  const int kt0 = BI::KPS * wave * BI::NSTEP + i / 8;
+  const uint32_t* lp = code_e + (size_t)(8 * hb + i % 8) * (8 * K) + q * G::WPL + kt0 * kstride;
+  BlockCode<K, NW> c;
+#pragma unroll
+  for (int k = 0; k < BI::NSTEP; ++k)
+    c.w[k] = load_lane_words<K>(lp + (size_t)(k * BI::KPS) * kstride);
+  return c;
+}
+
+// Decode + multiply the block item (inputs: all 32 kt of paired words in
+// s_x); each wave leaves its lanes' column partials in s_red[wave].
+template <int K, int NW>
+__device__ __forceinline__ void block_item_to_lds(const BlockCode<K, NW>& code,
+                                                  const uint32_t* s_x, float (*s_red)[64][4]) {
+  using G = Geo<K>;
+  using BI = BlockItem<K, NW>;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int q = lane % G::LPT, i = lane / G::LPT;
+  const int src = i * G::LPT + (q + G::LPT - 1) % G::LPT;
+  float acc[G::NCOL];
+#pragma unroll
+  for (int c = 0; c < G::NCOL; ++c) acc[c] = 0.f;
+#pragma unroll
+  for (int k = 0; k < BI::NSTEP; ++k) {
+    const int kl = BI::KPS * (wave * BI::NSTEP + k) + i / 8;
+    uint32_t xp[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xp[j] = s_x[8 * kl + j];
+    const uint32_t wprev = __shfl(code.w[k].w[G::WPL - 1], src);
+    fast_tile_packed<K>(code.w[k], wprev, xp, acc);
+  }
+#pragma unroll
+  for (int c = 0; c < G::NCOL; ++c) s_red[wave][lane][c] = acc[c];
+}
+
+// Column c (0..127) of a block item after block_item_to_lds and a barrier:
+// summed over the waves in order, each wave's kt slots in order.
+template <int K, int NW>
+__device__ __forceinline__ float block_item_col(const float (*s_red)[64][4], int c) {
+  using G = Geo<K>;
+  int qq, ci;
+  col_owner<K>(c & 15, qq, ci);
+  const int tile = c >> 4;
+  float v = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+#pragma unroll
+    for (int h = 0; h < BlockItem<K, NW>::KPS; ++h)
+      v = v + s_red[w][(tile + 8 * h) * G::LPT + qq][ci];
+  return v;
+}
+
+// One item per block (plan: NCP = H / 128 column blocks, NKB = 1).  The item
+// takes the row's 512 down inputs (4 waves, one h-block each: derived from the
+// gate_up partials, or read ready-made from xh2 when PREH), decodes and
+// multiplies, sums its waves, applies the down output transform and rounds
+// its 128 columns to f16 itself; the last of a (token, hb)'s top_k items to
+// finish gathers their f16 rows and combines them in slot order (f16(score)
+// weights, float32 sum, one f16 rounding).  The f16 row of item bi takes
+// 256 bytes of partB at float offset 64 bi.
+template <int KG, int KD, bool PREH, int NW>
+__global__ __launch_bounds__(64 * NW) void k_moe_down_blocks(FusedMoe p) {
+  static_assert(NW >= 4, "one wave per h-block");
+  __shared__ float s_red[NW][64][4];
+  __shared__ uint32_t s_x[256];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int g = xcd_item(blockIdx.x, gridDim.x);
+  const int l = g / p.nB, bi = g % p.nB;
+  const int hb = bi % p.NCP, r = bi / p.NCP, t = r / p.top_k;
+  const MoeLayer& L = p.layer(l);
+  const int e = L.ids[r];
+  const int TN = p.H / 16;
+  const auto code = load_block_item<KD, NW>(L.dn_code + (size_t)e * (p.I / 16) * TN * (8 * KD), TN, hb);
+  if (wave < 4) {
+    if constexpr (PREH)
+      s_x[64 * wave + lane] = reinterpret_cast<const uint32_t*>(
+          p.xh2 + ((size_t)l * p.T * p.top_k + r) * p.I + 128 * wave)[lane];
+    else
+      s_x[64 * wave + lane] = h_pair<false>(p, l, r, wave);
+  }
+  __syncthreads();
+  block_item_to_lds<KD, NW>(code, s_x, s_red);
+  __syncthreads();
+  uint32_t* rows = reinterpret_cast<uint32_t*>(p.partB + (size_t)l * p.nB * 256);
+  if (wave == 0) {
+    float v0 = block_item_col<KD, NW>(s_red, 2 * lane);
+    float v1 = block_item_col<KD, NW>(s_red, 2 * lane + 1);
+    h128_wave(v0, v1);
+    const float* ro = L.dn_rout + (size_t)e * p.H + 128 * hb + 2 * lane;
+    const uint32_t d = pack2(to_f16((v0 * kRS) * ro[0]), to_f16((v1 * kRS) * ro[1]));
+    __hip_atomic_store(rows + (size_t)bi * 64 + lane, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_vm();
+    int last = 0;
+    if (lane == 0) {
+      int* c = &p.cntB[(size_t)l * p.T * p.NCP + t * p.NCP + hb];
+      last = add_relaxed(c, 1) == p.top_k - 1;
+      if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (__shfl(last, 0)) {
+      float a0 = 0.f, a1 = 0.f;
+      for (int s0 = 0; s0 < p.top_k; s0 += 8) {
+        uint32_t d8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (s0 + j < p.top_k)
+            d8[j] = __hip_atomic_load(rows + (size_t)((t * p.top_k + s0 + j) * p.NCP + hb) * 64 + lane,
+                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (s0 + j < p.top_k) {
+            const float w = (float)(half_t)L.scores[t * p.top_k + s0 + j];
+            a0 = a0 + (float)__builtin_bit_cast(half_t, (uint16_t)d8[j]) * w;
+            a1 = a1 + (float)__builtin_bit_cast(half_t, (uint16_t)(d8[j] >> 16)) * w;
+          }
+      }
+      reinterpret_cast<uint32_t*>(L.y + (size_t)t * p.H + 128 * hb)[lane] =
+          pack2((half_t)a0, (half_t)a1);
+    }
+  }
 }
 
 template <int KG, int KD, int KTA, int KTB, bool PRE>

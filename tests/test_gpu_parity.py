@@ -461,12 +461,14 @@ def test_moe_one_launch_status_and_reuse(monkeypatch):
     assert ops().moe_status(ws, 1, k, H, I) == 0
 
 
-def test_moe_layers_one_launch_vs_oracle():
+@pytest.mark.parametrize("K_gu,K_dn,I", [(2, 2, 512), (2, 3, 512), (3, 2, 1024)])
+def test_moe_layers_one_launch_vs_oracle(K_gu, K_dn, I):
     """Independent token-layers in one launch (throughput mode): every layer's
-    output against the oracle, bit-identical across repeated launches."""
-    E, H, I, k, T, L = 32, 1024, 512, 8, 1, 3
+    output against the oracle, bit-identical across repeated launches (I = 512
+    takes the 128-column block down items, I = 1024 the split-K ones)."""
+    E, H, k, T, L = 32, 1024, 8, 1, 3
     o = ops()
-    cases = [_moe_case(E, H, I, 2, 2, T, k, 40 + l) for l in range(L)]
+    cases = [_moe_case(E, H, I, K_gu, K_dn, T, k, 40 + l) for l in range(L)]
     dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
     lays, keep = [], []
     for c in cases:
@@ -478,15 +480,15 @@ def test_moe_layers_one_launch_vs_oracle():
         lays.append(lay)
     table = o.moe_layers_table(lays, DEV)
     ws = torch.zeros(o.moe_layers_workspace(L, T, k, H, I), dtype=torch.uint8, device=DEV)
-    o.moe_expert_path_layers(table, T, k, E, H, I, 2, 2, ws=ws)
+    o.moe_expert_path_layers(table, T, k, E, H, I, K_gu, K_dn, ws=ws)
     first = [bits16(l["y"]).copy() for l in lays]
     for c, lay in zip(cases, lays):
         ids_np, sc_np = lay["ids"].cpu().numpy(), lay["scores"].cpu().numpy()
-        want = _oracle_moe(c, ids_np, sc_np, E, H, I, 2, 2, np.unique(ids_np)).astype(np.float32)
+        want = _oracle_moe(c, ids_np, sc_np, E, H, I, K_gu, K_dn, np.unique(ids_np)).astype(np.float32)
         got = lay["y"].cpu().numpy().astype(np.float32)
         assert np.abs(got - want).max() / np.abs(want).max() < 5e-3
     for _ in range(3):
-        o.moe_expert_path_layers(table, T, k, E, H, I, 2, 2, ws=ws)
+        o.moe_expert_path_layers(table, T, k, E, H, I, K_gu, K_dn, ws=ws)
         for f, lay in zip(first, lays):
             assert np.array_equal(bits16(lay["y"]), f)
 
@@ -514,6 +516,27 @@ def test_moe_config3_shape_fused_vs_exact(monkeypatch):
     want = _oracle_moe(c, ids_np, sc_np, E, H, I, 2, 2, np.unique(ids_np)).astype(np.float32)
     assert np.abs(y_ex.astype(np.float32) - want).max() / np.abs(want).max() < 1e-3
     assert np.abs(y_fast - want).max() / np.abs(want).max() < 5e-3
+
+
+@pytest.mark.parametrize("K_gu,K_dn,T,k", [(2, 3, 2, 8), (3, 2, 3, 4), (2, 2, 1, 10)])
+def test_moe_whole_row_down_items_vs_oracle(K_gu, K_dn, T, k, monkeypatch):
+    """I == 512, one token-layer: the down leg runs one item per (row, column
+    pair) over all 512 inputs and combines f16 rows in slot order (top_k
+    below, at and above one round of 8 slots; 2- and 3-bit down codes);
+    repeat calls on one workspace agree bit-for-bit."""
+    E, H, I = 32, 1024, 512
+    c = _moe_case(E, H, I, K_gu, K_dn, T, k, 300 + 10 * K_dn + k)
+    blk = _block(c, E, k, K_gu, K_dn, monkeypatch, exact=False)
+    ids, sc = ops().route_topk(torch.from_numpy(c["logits"]).to(DEV), k)
+    x = torch.from_numpy(c["x"]).to(DEV)
+    y = blk(x, ids, sc)
+    ids_np, sc_np = ids.cpu().numpy(), sc.cpu().numpy()
+    want = _oracle_moe(c, ids_np, sc_np, E, H, I, K_gu, K_dn, np.unique(ids_np)).astype(np.float32)
+    got = y.cpu().numpy().astype(np.float32)
+    assert np.abs(got - want).max() / np.abs(want).max() < 5e-3
+    first = bits16(y)
+    for _ in range(3):
+        assert np.array_equal(bits16(blk(x, ids, sc)), first)
 
 
 # ---------------------------------------------------------------- dense module
