@@ -48,7 +48,7 @@ BYTES_TOKEN_LAYER = TOP_K * (BYTES_GU + BYTES_DN)   # 6,291,456
 HBM_PEAK_GBS = 8000.0
 ROUTE_SETS = 4
 COPY_BYTES = 1 << 30                   # counter calibration copy
-KERNELS = ("k_moe_gate_up_items", "k_moe_down_items")
+KERNELS = ("k_moe_gate_up_items", "k_moe_down_blocks")
 
 
 def parse():
@@ -675,7 +675,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                          "traffic_detail": traffic_detail,
-                         "kernel": "k_moe_gate_up_items<2,16,true> + k_moe_down_items<2,2,16,true> "
+                         "kernel": "k_moe_gate_up_items<2,16,true,4> + k_moe_down_blocks<2,2,true,4> "
                                    "(one esc_moe_expert_path_layers call)",
                          "bytes_per_launch": bytes_call,
                          "avg_launch_us": round(ms * 1e3, 2)},

@@ -17,6 +17,9 @@
 //     256-column) tile sums every slot's partials in fixed order, transforms
 //     them and combines the slots in slot order (f16(score) weights, float32
 //     sum, one f16 rounding).  No float atomics: the result is deterministic.
+//   With I == 512 the two-launch path uses block down items instead
+//   (k_moe_down_blocks): one per (row, 128-column block) over all 512 inputs,
+//   each finishing its own output transform, so only f16 rows are combined.
 //
 // Two item sizes: small items (KTA=8, KTB=4) spread one token-layer over the
 // whole GPU for latency; large items (KTA=16, KTB=16) cut the partial traffic
