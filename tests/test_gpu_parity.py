@@ -461,7 +461,7 @@ def test_moe_one_launch_status_and_reuse(monkeypatch):
     assert ops().moe_status(ws, 1, k, H, I) == 0
 
 
-@pytest.mark.parametrize("K_gu,K_dn,I", [(2, 2, 512), (2, 3, 512), (3, 2, 1024)])
+@pytest.mark.parametrize("K_gu,K_dn,I", [(2, 2, 512), (2, 3, 512), (3, 3, 512), (3, 2, 1024)])
 def test_moe_layers_one_launch_vs_oracle(K_gu, K_dn, I):
     """Independent token-layers in one launch (throughput mode): every layer's
     output against the oracle, bit-identical across repeated launches (I = 512
