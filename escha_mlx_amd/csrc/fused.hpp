@@ -636,6 +636,15 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down_blocks(FusedMoe p) {
   const int e = L.ids[r];
   const int TN = p.H / 16;
   const auto code = load_block_item<KD, NW>(L.dn_code + (size_t)e * (p.I / 16) * TN * (8 * KD), TN, hb);
+  // wave 0's tail inputs, requested now so that no load waits behind the
+  // barriers: its two output scales and the f16-rounded score of slot `lane`
+  float ro0 = 0.f, ro1 = 0.f, score = 0.f;
+  if (wave == 0) {
+    const float* ro = L.dn_rout + (size_t)e * p.H + 128 * hb + 2 * lane;
+    ro0 = ro[0];
+    ro1 = ro[1];
+    if (lane < p.top_k) score = (float)(half_t)L.scores[t * p.top_k + lane];
+  }
   if (wave < 4) {
     if constexpr (PREH)
       s_x[64 * wave + lane] = reinterpret_cast<const uint32_t*>(
@@ -651,8 +660,7 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down_blocks(FusedMoe p) {
     float v0 = block_item_col<KD, NW>(s_red, 2 * lane);
     float v1 = block_item_col<KD, NW>(s_red, 2 * lane + 1);
     h128_wave(v0, v1);
-    const float* ro = L.dn_rout + (size_t)e * p.H + 128 * hb + 2 * lane;
-    const uint32_t d = pack2(to_f16((v0 * kRS) * ro[0]), to_f16((v1 * kRS) * ro[1]));
+    const uint32_t d = pack2(to_f16((v0 * kRS) * ro0), to_f16((v1 * kRS) * ro1));
     __hip_atomic_store(rows + (size_t)bi * 64 + lane, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wait_vm();
     int last = 0;
@@ -673,7 +681,7 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down_blocks(FusedMoe p) {
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           if (s0 + j < p.top_k) {
-            const float w = (float)(half_t)L.scores[t * p.top_k + s0 + j];
+            const float w = __shfl(score, s0 + j);
             a0 = a0 + (float)__builtin_bit_cast(half_t, (uint16_t)d8[j]) * w;
             a1 = a1 + (float)__builtin_bit_cast(half_t, (uint16_t)(d8[j] >> 16)) * w;
           }
