@@ -887,10 +887,6 @@ bool fused_eligible(int T, int top_k, int H, int I) {
          I % 128 == 0;
 }
 
-// Items per layer of the large (KTA=16) size; below kSmallItemsBelow of them
-// in total the two-launch path uses the small size to fill the GPU.
-constexpr int kSmallItemsBelow = 0;
-
 // kt per item of the many-layer two-launch path (gate_up, down)
 // (measured on MI355X: 32 kt per item for either kernel is no faster)
 constexpr int kKtaLayers = 16, kKtbLayers = 16;
@@ -904,7 +900,9 @@ constexpr int kGateUpWavesSingle = 16, kDownBlockWavesSingle = 16;
 constexpr int kDownBlockWavesLayers = 4;
 
 FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput) {
-  const bool large = throughput && L * T * top_k * (I / 128) * std::max(1, H / 256) >= kSmallItemsBelow;
+  // the two-launch path (throughput) uses the large items; the one-launch
+  // path the small ones (KTA = 8, KTB = 4), which spread one token-layer wide
+  const bool large = throughput;
   const bool layers = large && L > 1;
   const int kta = layers ? kKtaLayers : large ? kKtaSingle : 8;
   const bool blocks = large && I == 16 * kKtbBlocks;
@@ -963,19 +961,12 @@ template <int KG, int KD, bool TP>
 int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
   if constexpr (TP) {
     // two launches: every gate_up item, then every down item (grid unused);
-    // small items when there are few layers, large ones otherwise; the down
-    // inputs are precomputed once per (row, h-block) for multi-layer calls
+    // the down inputs are precomputed once per (row, h-block) for
+    // multi-layer calls
     (void)grid;
     const dim3 ga(p.L * p.nA), gb(p.L * p.nB), blk(esc::kFusedThreads);
-    // the plan's item sizes: small (below kSmallItemsBelow items), many
-    // layers, or one token-layer
-    const int kta = p.H / (16 * p.NKC), ktb = p.I / (16 * p.NKB);
-    if (kta == 8 && ktb == 4) {
-      hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, 8, false>), ga, blk, 0, s, p);
-      if (int rc = launched("k_moe_gate_up_items")) return rc;
-      hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, 4, false>), gb, blk, 0, s, p);
-      return launched("k_moe_down_items");
-    }
+    // the plan's down item size: whole-input blocks (I == 512) or split-K
+    const int ktb = p.I / (16 * p.NKB);
     if (p.L > 1) {
       hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, kKtaLayers, true>), ga, blk, 0, s, p);
       if (int rc = launched("k_moe_gate_up_items")) return rc;
