@@ -519,11 +519,12 @@ def test_moe_config3_shape_fused_vs_exact(monkeypatch):
 
 
 @pytest.mark.parametrize("K_gu,K_dn,T,k", [(2, 3, 2, 8), (3, 2, 3, 4), (2, 2, 1, 10)])
-def test_moe_whole_row_down_items_vs_oracle(K_gu, K_dn, T, k, monkeypatch):
-    """I == 512, one token-layer: the down leg runs one item per (row, column
-    pair) over all 512 inputs and combines f16 rows in slot order (top_k
-    below, at and above one round of 8 slots; 2- and 3-bit down codes);
-    repeat calls on one workspace agree bit-for-bit."""
+def test_moe_block_down_items_vs_oracle(K_gu, K_dn, T, k, monkeypatch):
+    """I == 512, one token-layer: the down leg runs one item per (row,
+    128-column block) over all 512 inputs, and the last slot of each (token,
+    block) combines the f16 rows in slot order (top_k below, at and above one
+    round of 8 slots; 2- and 3-bit codes); repeat calls on one workspace
+    agree bit-for-bit (the counters return to zero)."""
     E, H, I = 32, 1024, 512
     c = _moe_case(E, H, I, K_gu, K_dn, T, k, 300 + 10 * K_dn + k)
     blk = _block(c, E, k, K_gu, K_dn, monkeypatch, exact=False)
