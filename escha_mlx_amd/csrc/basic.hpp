@@ -226,10 +226,11 @@ __global__ __launch_bounds__(64) void k_route_topk(const float* __restrict__ log
 // each expert padded to a multiple of R, padding slots = m (zero sink row),
 // groups past the end = expert -1.  Integer only, one block, deterministic.
 // Shared memory holds per-expert counts; E <= 4096.
-__global__ __launch_bounds__(1024) void k_build_groups(const int* __restrict__ row_expert, int m,
-                                                       int E, int R, int n_groups,
-                                                       int* __restrict__ rows_idx,
-                                                       int* __restrict__ group_expert) {
+// The body runs in one block of 1024 threads (k_build_groups, or block 0 of
+// k_moe_prep).
+__device__ void build_groups_block(const int* __restrict__ row_expert, int m, int E, int R,
+                                   int n_groups, int* __restrict__ rows_idx,
+                                   int* __restrict__ group_expert) {
   __shared__ int s_cnt[4096];    // rows per expert, then rows placed so far
   __shared__ int s_start[4096];  // first padded slot of each expert
   __shared__ int s_e[1024];      // one chunk of row_expert
@@ -290,6 +291,13 @@ __global__ __launch_bounds__(1024) void k_build_groups(const int* __restrict__ r
     if (r < m) atomicAdd(&s_cnt[e], 1);
     __syncthreads();
   }
+}
+
+__global__ __launch_bounds__(1024) void k_build_groups(const int* __restrict__ row_expert, int m,
+                                                       int E, int R, int n_groups,
+                                                       int* __restrict__ rows_idx,
+                                                       int* __restrict__ group_expert) {
+  build_groups_block(row_expert, m, E, R, n_groups, rows_idx, group_expert);
 }
 
 }  // namespace esc

@@ -817,6 +817,13 @@ namespace {
 constexpr int kMoeGroupRows = 8;
 int moe_group_rows(int M, int E) { return M >= E ? kMoeGroupRows : 0; }
 
+int moe_input(const uint16_t* x, const int32_t* ids, int top_k, const float* rin, int H, float rs,
+              uint16_t* xh, int M, hipStream_t s) {
+  hipLaunchKernelGGL(esc::k_moe_input, dim3(H / 128, M), dim3(64), 0, s, x, ids, top_k, rin, H, rs,
+                     xh);
+  return launched("k_moe_input");
+}
+
 struct MoePlan {
   int M, S1, S2, R, n_groups;
   size_t off_xh, off_p1, off_xh2, off_p2, off_rows, off_gexp, total;
@@ -1079,18 +1086,19 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
   float* p2 = reinterpret_cast<float*>(w + p.off_p2);
   hipStream_t s = S(stream);
   const float rs = esc::kRS;
-  hipLaunchKernelGGL(esc::k_moe_input, dim3(H / 128, p.M), dim3(64), 0, s, x, ids, top_k, gu_rin,
-                     H, rs, xh);
-  if (int rc = launched("k_moe_input")) return rc;
   int* rows = reinterpret_cast<int*>(w + p.off_rows);
   int* gexp = reinterpret_cast<int*>(w + p.off_gexp);
   if (p.R) {
-    hipLaunchKernelGGL(esc::k_build_groups, dim3(1), dim3(1024), 0, s, ids, p.M, E, p.R,
-                       p.n_groups, rows, gexp);
-    if (int rc = launched("k_build_groups")) return rc;
+    // input transform and expert grouping in one launch
+    const int waves = H / 128 * p.M;
+    hipLaunchKernelGGL(esc::k_moe_prep, dim3(1 + (waves + 15) / 16), dim3(1024), 0, s, x, ids,
+                       top_k, gu_rin, H, rs, xh, p.M, E, p.R, p.n_groups, rows, gexp);
+    if (int rc = launched("k_moe_prep")) return rc;
     if (int rc = group_rows(K_gu, use_lut, p.R, xh, gu_code, rows, gexp, p.n_groups, p.M, H / 16,
                             2 * I / 16, p.S1, p1, s))
       return rc;
+  } else if (int rc = moe_input(x, ids, top_k, gu_rin, H, rs, xh, p.M, s)) {
+    return rc;
   } else if (int rc = by_k_lut<FastF>(K_gu, use_lut, xh, gu_code, ids, p.M, H / 16, 2 * I / 16,
                                       p.S1, p1, s)) {
     return rc;

@@ -8,12 +8,13 @@
 
 namespace esc {
 
-// xh[row] = f16(H128(f32(x[row / k]) * rin[ids[row]]) * RS).  grid (H/128, T*k), block 64.
-__global__ __launch_bounds__(64) void k_moe_input(const uint16_t* __restrict__ x,
-                                                  const int* __restrict__ ids, int top_k,
-                                                  const float* __restrict__ rin, int H, float rs,
-                                                  uint16_t* __restrict__ xh) {
-  const int blk = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+// xh[row] = f16(H128(f32(x[row / k]) * rin[ids[row]]) * RS), 128-block blk
+// of one row, by one wave.
+__device__ __forceinline__ void moe_input_wave(const uint16_t* __restrict__ x,
+                                               const int* __restrict__ ids, int top_k,
+                                               const float* __restrict__ rin, int H, float rs,
+                                               uint16_t* __restrict__ xh, int blk, int row) {
+  const int lane = threadIdx.x & 63;
   const int tok = row / top_k, e = ids[row];
   const int c = blk * 128 + 2 * lane;
   const uint16_t* xr = x + (size_t)tok * H + c;
@@ -24,6 +25,32 @@ __global__ __launch_bounds__(64) void k_moe_input(const uint16_t* __restrict__ x
   uint16_t* o = xh + (size_t)row * H + c;
   o[0] = __builtin_bit_cast(uint16_t, to_f16(v0 * rs));
   o[1] = __builtin_bit_cast(uint16_t, to_f16(v1 * rs));
+}
+
+// grid (H/128, T*k), block 64.
+__global__ __launch_bounds__(64) void k_moe_input(const uint16_t* __restrict__ x,
+                                                  const int* __restrict__ ids, int top_k,
+                                                  const float* __restrict__ rin, int H, float rs,
+                                                  uint16_t* __restrict__ xh) {
+  moe_input_wave(x, ids, top_k, rin, H, rs, xh, blockIdx.x, blockIdx.y);
+}
+
+// The chain's two independent first steps in one launch: block 0 groups the
+// routed rows by expert (build_groups_block); every other block runs 16 of
+// the (128-block, row) input transforms, one per wave.  grid
+// 1 + ceil(H/128 * m / 16), block 1024.
+__global__ __launch_bounds__(1024) void k_moe_prep(const uint16_t* __restrict__ x,
+                                                   const int* __restrict__ ids, int top_k,
+                                                   const float* __restrict__ rin, int H, float rs,
+                                                   uint16_t* __restrict__ xh, int m, int E, int R,
+                                                   int n_groups, int* __restrict__ rows_idx,
+                                                   int* __restrict__ group_expert) {
+  if (blockIdx.x == 0) {
+    build_groups_block(ids, m, E, R, n_groups, rows_idx, group_expert);
+    return;
+  }
+  const int nhb = H / 128, w = (blockIdx.x - 1) * 16 + (threadIdx.x >> 6);
+  if (w < nhb * m) moe_input_wave(x, ids, top_k, rin, H, rs, xh, w % nhb, w / nhb);
 }
 
 // h = f16(f16(silu(g)) * u) with silu(g) = g / (1 + exp(-g)) in float32
