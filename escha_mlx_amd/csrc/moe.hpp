@@ -138,19 +138,26 @@ __global__ __launch_bounds__(64) void k_moe_combine(const float* __restrict__ pa
       rows[j] = s0 + j < top_k ? tok * top_k + s0 + j : -1;
       cols[j] = c;
     }
+    // every slot's output scales and weight are requested before the
+    // partial sums, so the slots' expert-dependent loads overlap
+    float2 ro[8];
+    float w[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (rows[j] >= 0) {
+        ro[j] = *reinterpret_cast<const float2*>(dn_rout + (size_t)ids[rows[j]] * H + c);
+        w[j] = (float)(half_t)scores[rows[j]];
+      }
     float2 d[8];
     sum_splits<8>(part, S, M, H, rows, cols, d);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (rows[j] < 0) break;  // uniform
-      const int row = rows[j], e = ids[row];
       h128_wave(d[j].x, d[j].y);
-      const float* ro = dn_rout + (size_t)e * H;
-      const half_t d0 = to_f16((d[j].x * rs) * ro[c]);
-      const half_t d1 = to_f16((d[j].y * rs) * ro[c + 1]);
-      const float w = (float)(half_t)scores[row];
-      a0 = a0 + (float)d0 * w;
-      a1 = a1 + (float)d1 * w;
+      const half_t d0 = to_f16((d[j].x * rs) * ro[j].x);
+      const half_t d1 = to_f16((d[j].y * rs) * ro[j].y);
+      a0 = a0 + (float)d0 * w[j];
+      a1 = a1 + (float)d1 * w[j];
     }
   }
   y[(size_t)tok * H + c] = __builtin_bit_cast(uint16_t, (half_t)a0);
