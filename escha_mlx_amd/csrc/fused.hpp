@@ -2,7 +2,8 @@
 // EschaSparseMoeBlock._expert_path, escha_mlx/models/qwen3_5_moe.py:207-253),
 // for one token-layer or for a list of independent token-layers.
 //
-// Work is split into two kinds of items, each one block of 4 waves:
+// Work is split into two kinds of items, each one block (4 waves; 16 in the
+// two-launch path for one token-layer, where latency rules):
 //   gate_up item (l, r, b, kc): layer l, row r, output columns
 //     gate[128b, 128b+128) and up[I+128b, I+128b+128), input rows
 //     [16*KTA*kc, 16*KTA*(kc+1)).  The block input-transforms its own inputs of
