@@ -202,22 +202,32 @@ __device__ __forceinline__ void fast_tile_packed(const LaneWords<K>& lw, uint32_
 // R-row variant of fast_tile_packed: every state pair is decoded once (hash,
 // or two table reads from LDS into the two halves) and multiplied into R
 // rows' accumulators.  xp[r] are row r's input pairs (x_pairs).
+// Step pairs of every 8 that the table-decode GEMV reads from the table in
+// LDS; the others are hashed (the table is the hash's image, so the weights
+// are the same either way).  Measured on MI355X (config 2, 5120^2 K=2 at
+// batch 1): 4 of 8 beats 2, 6 and all 8.
+constexpr int kTablePairs = 4;
+
 template <int K, bool LUT, int R>
 __device__ __forceinline__ void fast_tile_rows(const LaneWords<K>& lw, uint32_t wprev,
                                                const uint32_t (*xp)[8], const uint16_t* lut,
                                                float (*acc)[Geo<K>::NCOL]) {
   using G = Geo<K>;
   const uint32_t clo = kClo, chi = kChi;
+  int pair = 0;
 #pragma unroll
   for (int u = 0; u < G::SPL; ++u) {
     if ((u >> 3) & 1) continue;  // u+8 handled with u
+    // table path: kTablePairs of every 8 pairs from the table, the rest by
+    // hash (bit-identical), so the LDS and the VALU share the decode
+    const bool from_lut = LUT && (pair++ & 7) < kTablePairs;
     uint32_t w2;
     if constexpr (K == 2) {
       const int rel = 2 * (u + 1) - 16;
       const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
       const uint32_t hi = a < 0 ? wprev : lw.w[a];
       const uint32_t p = off == 0 ? hi : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 32 - off);
-      if constexpr (LUT)
+      if (from_lut)
         w2 = (uint32_t)lut[p & 0xFFFFu] | ((uint32_t)lut[p >> 16] << 16);
       else
         w2 = halves_sum2(mask_xor(hash_x<false>(p, clo, chi)), mask_xor(hash_x<true>(p, clo, chi)));
@@ -232,7 +242,7 @@ __device__ __forceinline__ void fast_tile_rows(const LaneWords<K>& lw, uint32_t 
         s2[h] = off <= 16 ? hi >> (16 - off)
                           : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 48 - off);
       }
-      if constexpr (LUT)
+      if (from_lut)
         w2 = (uint32_t)lut[s2[0] & 0xFFFFu] | ((uint32_t)lut[s2[1] & 0xFFFFu] << 16);
       else
         w2 = halves_sum2(mask_xor(hash_x<false>(s2[0], clo, chi)),
@@ -299,10 +309,12 @@ __device__ __forceinline__ u32x4_t mma_a_operand(const LaneWords<K>& lw, uint32_
 #pragma unroll
   for (int m = 0; m < 4; m += 2) {
     const int ua = mma_step<K>(m, 2 * P, ci), ub = mma_step<K>(m, 2 * P + 1, ci);
+    // table path: half the words from the table, half by hash (as kTablePairs)
+    const bool from_lut = LUT && m == 0;
     if constexpr (K == 2) {
       // one window per v gives the steps of m (high half) and m + 1 (low half)
       const uint32_t pa = window2(lw, wprev, ua), pb = window2(lw, wprev, ub);
-      if constexpr (LUT) {
+      if (from_lut) {
         a[m] = (uint32_t)lut[pa >> 16] | ((uint32_t)lut[pb >> 16] << 16);
         a[m + 1] = (uint32_t)lut[pa & 0xFFFFu] | ((uint32_t)lut[pb & 0xFFFFu] << 16);
       } else {
@@ -313,7 +325,7 @@ __device__ __forceinline__ u32x4_t mma_a_operand(const LaneWords<K>& lw, uint32_
     } else {
       const uint32_t sa0 = state3(lw, wprev, ua), sb0 = state3(lw, wprev, ub);
       const uint32_t sa1 = state3(lw, wprev, ua + 8), sb1 = state3(lw, wprev, ub + 8);
-      if constexpr (LUT) {
+      if (from_lut) {
         a[m] = (uint32_t)lut[sa0 & 0xFFFFu] | ((uint32_t)lut[sb0 & 0xFFFFu] << 16);
         a[m + 1] = (uint32_t)lut[sa1 & 0xFFFFu] | ((uint32_t)lut[sb1 & 0xFFFFu] << 16);
       } else {
