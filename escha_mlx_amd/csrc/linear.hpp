@@ -157,6 +157,19 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
       }
     }
   }
+  // this wave's output scales and bias for the finishing passes (every pass
+  // of a wave transforms the same 128-column block, wave % kBlocks), requested
+  // now so that the last split does not wait on them after the counter
+  const int colw = ntg * kCols + 128 * (wave % kBlocks) + 2 * lane;
+  float ro0 = 0.f, ro1 = 0.f, bs0 = 0.f, bs1 = 0.f;
+  if (colw < OC) {
+    ro0 = rout[colw];
+    ro1 = rout[colw + 1];
+    if (bias) {
+      bs0 = (float)__builtin_bit_cast(half_t, bias[colw]);
+      bs1 = (float)__builtin_bit_cast(half_t, bias[colw + 1]);
+    }
+  }
   wait_vm();
   __syncthreads();
   // 3. the last split of (row group, column group) finishes the columns
@@ -202,11 +215,11 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
       float v0 = s_sum[rr][128 * b + 2 * lane];
       float v1 = s_sum[rr][128 * b + 2 * lane + 1];
       h128_wave(v0, v1);
-      half_t y0 = to_f16((v0 * rs) * rout[col]);
-      half_t y1 = to_f16((v1 * rs) * rout[col + 1]);
+      half_t y0 = to_f16((v0 * rs) * ro0);  // col == colw
+      half_t y1 = to_f16((v1 * rs) * ro1);
       if (bias) {
-        y0 = to_f16((float)y0 + (float)__builtin_bit_cast(half_t, bias[col]));
-        y1 = to_f16((float)y1 + (float)__builtin_bit_cast(half_t, bias[col + 1]));
+        y0 = to_f16((float)y0 + bs0);
+        y1 = to_f16((float)y1 + bs1);
       }
       uint16_t* yr = y + (size_t)(row0 + r) * OC + col;
       yr[0] = __builtin_bit_cast(uint16_t, y0);
