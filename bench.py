@@ -441,7 +441,7 @@ def bench_dense(args, torch, ops, cfg):
             per[f"M{M}_layer_us"] = round(t_layer * 1e3, 2)
             per[f"M{M}_layer_gbs"] = round(total_b / (t_layer * 1e-3) / 1e9, 1)
             per[f"M{M}_tok_s_per_layer"] = round(M / (t_layer * 1e-3), 1)
-        # the headline line: the whole layer replayed as one HIP graph, k and v as
+        # this line's value: the whole layer replayed as one HIP graph, k and v as
         # one pair launch (the per-projection graphs' sum is M1_layer_gbs)
         us_layer = per["M1_layer_graph_kv_pair_us"]
         res.update(metric="coded-weight GB/s of one dense decoder layer (q,k,v,o K2 LUT, up/down "
