@@ -217,10 +217,13 @@ LinearPlan linear_plan(int M, int K, int IC, int OC, bool lut) {
       if (p.groups * p.row_groups * S >= target) break;
     }
     p.KS = 8 * (nb / p.S);
-    // counters first, at an offset that does not depend on the split count:
-    // one zero-filled workspace serves the table and the hash plan alike
+    // counters first, sized for the most row groups either plan of this M
+    // has (the table plan's 8-row groups), so that neither plan's partials
+    // start inside the other's counters: one zero-filled workspace serves the
+    // table and the hash plan alike
+    const int rg_max = (M + kLinearSmallRowsLut - 1) / kLinearSmallRowsLut;
     p.off_cnt = 0;
-    p.off_part = al((size_t)p.groups * p.row_groups * 4);
+    p.off_part = al((size_t)p.groups * std::max(p.row_groups, rg_max) * 4);
     p.total = p.off_part + al((size_t)p.S * M * OC * 4);
   } else {
     p.off_xh = 0;
@@ -930,7 +933,7 @@ FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput) {
   f.off_pb = al((size_t)L * f.nA * 256 * 4);
   f.off_xh2 = f.off_pb + al((size_t)L * f.nB * 256 * 4);
   f.off_int = f.off_xh2 + al((size_t)L * f.M * I * 2);
-  f.n_int = L * (f.M * f.NB + f.nA + T * f.NCP) + 2;
+  f.n_int = L * (f.M * f.NB + f.nA + T * f.NCP) + 3;
   f.total = f.off_int + al((size_t)f.n_int * 4);
   return f;
 }
@@ -950,6 +953,7 @@ esc::FusedMoe fused_args(const FusedPlan& f, void* ws, int T, int top_k, int H, 
   p.cntB = p.claimA + (size_t)f.L * f.nA;
   p.done = p.cntB + (size_t)f.L * T * f.NCP;
   p.err = p.done + 1;
+  p.status = p.done + 2;
   p.L = f.L;
   p.T = T;
   p.top_k = top_k;
@@ -1032,11 +1036,13 @@ int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int
   if (!fused_eligible(T, top_k, H, I) || throughput_ok(H, I)) return ESC_OK;
   const FusedPlan f = fused_plan(1, T, top_k, H, I, false);
   ESC_REQUIRE(ws_bytes >= f.total, "workspace smaller than the plan");
-  const int32_t* err = reinterpret_cast<const int32_t*>(static_cast<const char*>(ws) + f.off_int) +
-                       (f.n_int - 1);
-  if (int rc = hip_check(hipMemcpyAsync(host_flag, err, 4, hipMemcpyDeviceToHost, S(stream)),
+  // the status slot (the last integer): read, then cleared for the next read
+  int32_t* st = reinterpret_cast<int32_t*>(static_cast<char*>(const_cast<void*>(ws)) + f.off_int) +
+                (f.n_int - 1);
+  if (int rc = hip_check(hipMemcpyAsync(host_flag, st, 4, hipMemcpyDeviceToHost, S(stream)),
                          "hipMemcpyAsync"))
     return rc;
+  if (int rc = hip_check(hipMemsetAsync(st, 0, 4, S(stream)), "hipMemsetAsync")) return rc;
   return hip_check(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
 }
 

@@ -39,9 +39,12 @@
 // gate_up item is claimed (integer CAS) by the block that runs it; a down item
 // whose inputs are not ready claims and runs the missing gate_up items itself,
 // and otherwise waits only on items already claimed by running blocks, which
-// never wait.  A bounded spin (err flag) is a last safety net.  The last block
-// to finish resets every counter, so the integer workspace is zero again for
-// the next call (it must be zero before the first).
+// never wait.  A bounded spin is a last safety net: a down item that gives up
+// computes on NaN inputs (so its outputs are NaN, never stale values), raises
+// the call's err flag (every other waiting block then gives up too) and the
+// status flag that esc_moe_status reports.  The last block to finish resets
+// every counter and the call's err flag, so the integer workspace is zero
+// again for the next call (it must be zero before the first).
 #pragma once
 
 #include "moe.hpp"
@@ -92,7 +95,8 @@ struct FusedMoe {
   int* claimA;   // [L][nA]
   int* cntB;     // [L][T*NCP] finished down items per (token, column pair or block)
   int* done;     // [1]
-  int* err;      // [1] sticky: a spin bound was hit
+  int* err;      // [1] a spin bound was hit in this call (reset by the last block)
+  int* status;   // [1] a spin bound was hit since the host last read it
   int L, T, top_k, H, I;
   int NB;   // I / 128        h-blocks
   int NKC;  // H / (16*KTA)   gate_up items per (row, h-block), <= 62
@@ -750,7 +754,12 @@ __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_fused(FusedMoe p) {
       ok = ok && st != kTimeout;
     }
     if (!ok) {
-      if (tid == 0) atomicOr(p.err, 1);
+      // inputs never became ready: NaN inputs make this item's outputs NaN
+      if ((tid >> 6) < kHB) s_x[tid] = 0x7E007E00u;
+      if (tid == 0) {
+        atomicOr(p.err, 1);
+        atomicOr(p.status, 1);
+      }
     } else if ((tid >> 6) < kHB) {
       down_inputs(p, l, r, hb0 + (tid >> 6), s_x + 64 * (tid >> 6));
     }
@@ -778,7 +787,10 @@ __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_fused(FusedMoe p) {
     for (int i = tid; i < nA_all; i += kFusedThreads) p.claimA[i] = 0;
     for (int i = tid; i < p.L * p.T * p.NCP; i += kFusedThreads) p.cntB[i] = 0;
     __syncthreads();
-    if (tid == 0) *p.done = 0;
+    if (tid == 0) {
+      *p.err = 0;
+      *p.done = 0;
+    }
   }
 }
 

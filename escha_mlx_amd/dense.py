@@ -56,11 +56,8 @@ def fold_scales(rin, rout, s_in=None, s_out=None):
 
 
 def apply_bias() -> bool:
-    """ESCHA_MLX_BIAS=1 applies the exported correction (default off, dense.py:107-132)."""
-    v = __import__("os").environ.get("ESCHA_MLX_BIAS", "0")
-    if v not in ("0", "1", ""):
-        raise ValueError(f"ESCHA_MLX_BIAS must be 0 or 1, got {v!r}")
-    return v == "1"
+    """ESCHA_MLX_BIAS on applies the exported correction (default off, dense.py:107-132)."""
+    return envs.parse_bool("ESCHA_MLX_BIAS", False)
 
 
 def dense_block_r(m: int, pin: int | None = None) -> int:
@@ -136,6 +133,8 @@ class EschaLinear(torch.nn.Module):
         self._exact = envs.use_exact()
         self._block_r_pin = envs.dense_block_r_pin()
         self._mat = envs.dense_mat()
+        self._fused_had = envs.fused_had()
+        envs.kt_block()  # validated like the reference's; no code tiles are staged here
         self._ws = {}  # zero-filled one-launch workspaces per (rows, device)
         self._pair_ws = {}  # the same for project_pair with this linear first
 
@@ -157,7 +156,7 @@ class EschaLinear(torch.nn.Module):
         shape = x.shape
         rows = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
         m = rows.shape[0]
-        if (not self._exact and self._block_r_pin is None
+        if (not self._exact and self._block_r_pin is None and self._fused_had
                 and (m < ops.LINEAR_SMALL_ROWS or self._mat)):
             # the whole linear in esc_linear (one launch below 16 rows)
             y = ops.linear(rows, w.code, w.rin, w.rout, w.K, w.IC, w.OC, bias=self.bias,
@@ -167,6 +166,12 @@ class EschaLinear(torch.nn.Module):
         r = dense_block_r(m, self._block_r_pin)
         if self._mat and r == DENSE_MAT_R:
             y = ops.scaled_had_out(ops.dense_gemm_mat(xh, w.code, w.K, w.IC, w.OC), w.rout, None)
+        elif not self._fused_had:
+            # ESCHA_MLX_FUSED_HAD off: the output transform is its own launch
+            # after the GEMV (escha_mlx/dense.py:287-298, 346-356)
+            mid = (ops.dense_gemm_rows(xh, w.code, w.K, w.IC, w.OC, r, lut=self._lut) if r > 1
+                   else ops.dense_gemv(xh, w.code, w.K, w.IC, w.OC, lut=self._lut))
+            y = ops.scaled_had_out(mid, w.rout, None)
         elif m > 1 and r <= 8 and not self._exact:
             y = ops.dense_gemm_rows_fast_out(xh, w.code, w.rout, w.K, w.IC, w.OC, max(r, 2),
                                              lut=self._lut)
@@ -201,6 +206,7 @@ def project_pair(first: EschaLinear, second: EschaLinear, x: torch.Tensor):
     compatible = (
         w0.IC == w1.IC == rows.shape[-1]
         and first._lut == second._lut
+        and first._fused_had and second._fused_had
         and not (first._exact or second._exact)
         and first._block_r_pin is None and second._block_r_pin is None
         and (m < ops.LINEAR_SMALL_ROWS or (first._mat and second._mat))

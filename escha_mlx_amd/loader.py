@@ -40,7 +40,7 @@ from pathlib import Path
 import numpy as np
 import torch
 
-from . import dense, moe, quant
+from . import dense, envs, moe, quant
 
 #: quant_method values this runtime loads (loader.py:29-34).
 QUANT_METHODS = frozenset({"escha", "eschamoe"})
@@ -86,10 +86,7 @@ def _dropped(name: str) -> bool:
 def use_last_logit() -> bool:
     """ESCHA_MLX_LAST_LOGIT (default 1): the head sees the final position only
     (loader.py:135-138)."""
-    v = os.environ.get("ESCHA_MLX_LAST_LOGIT", "1")
-    if v not in ("0", "1", ""):
-        raise ValueError(f"ESCHA_MLX_LAST_LOGIT must be 0 or 1, got {v!r}")
-    return v != "0"
+    return envs.parse_bool("ESCHA_MLX_LAST_LOGIT", True)
 
 
 def q8_group() -> int:

@@ -12,9 +12,10 @@ Two execution paths with the same rounding points:
   * fused (default) — ``esc_moe_expert_path``: decode fused into split-K
     GEMVs, transforms / swiglu / combine fused into their epilogues; GEMV
     sums reassociated (tolerance contract), decode bit-exact.
-  * exact (ESCHA_HIP_EXACT=1) — the reference kernel chain with the
-    reference accumulation order (bit-reproducible against the oracle),
-    row-blocked by the reference's R policy.
+  * exact (ESCHA_HIP_EXACT=1, and ESCHA_MLX_FUSED_HAD=0) — the reference
+    kernel chain with the reference accumulation order (bit-reproducible
+    against the oracle), row-blocked by the reference's R policy; every
+    transform is its own launch.
 """
 from __future__ import annotations
 
@@ -104,7 +105,9 @@ class EschaMoEExperts(torch.nn.Module):
         self._inter = dn.IC
         self._lut = envs.use_lut()
         self._exact = envs.use_exact()
+        self._fused_had = envs.fused_had()
         self._block_r = envs.block_r_pin()
+        envs.kt_block()  # validated like the reference's; no code tiles are staged here
         self._ws = {}
 
     def _rows(self, t: int, ids: torch.Tensor):
@@ -140,7 +143,9 @@ class EschaMoEExperts(torch.nn.Module):
         x = x.to(torch.float16).contiguous()
         ids = ids.to(torch.int32).contiguous()
         scores = scores.to(torch.float32).contiguous()
-        if self._exact:
+        if self._exact or not self._fused_had:
+            # ESCHA_MLX_FUSED_HAD off: every transform is its own launch around
+            # the GEMVs (models/qwen3_5_moe.py:103-122), the staged chain
             return self._forward_exact(x, ids, scores)
         t, h = x.shape
         # one zero-initialised workspace per token count: the one-launch path

@@ -427,7 +427,8 @@ def q8_embed(ids: torch.Tensor, w8: torch.Tensor, scale: torch.Tensor) -> torch.
 
 
 def moe_status(ws: torch.Tensor, T: int, top_k: int, H: int, I: int) -> int:
-    """1 if a one-launch expert path using ``ws`` ever hit its bounded wait (synchronises)."""
+    """1 if a one-launch expert path using ``ws`` hit its bounded wait since the
+    previous call (reading clears the flag; synchronises)."""
     flag = ctypes.c_int32(0)
     _lib.call("esc_moe_status", _ptr(ws), ws.numel(), T, top_k, H, I, ctypes.byref(flag), _stream())
     return int(flag.value)

@@ -261,10 +261,12 @@ int esc_moe_expert_path_layers(const esc_moe_layer* layers, int L, int T, int to
                                int I, int K_gu, int K_dn, void* ws, size_t ws_bytes,
                                void* stream);
 
-/* Diagnostic: *host_flag = 1 if the one-launch expert path run with this
- * workspace ever hit its bounded wait (never expected: the kernel's work
- * claiming guarantees progress).  Synchronises the stream.  No counterpart in
- * the reference (its expert path has no cross-workgroup hand-off). */
+/* Diagnostic: *host_flag = 1 if a one-launch expert path run with this
+ * workspace hit its bounded wait since the previous esc_moe_status call on it
+ * (never expected: the kernel's work claiming guarantees progress; the
+ * outputs of an item that gave up are NaN, never stale values).  Reading
+ * clears the flag.  Synchronises the stream.  No counterpart in the reference
+ * (its expert path has no cross-workgroup hand-off). */
 int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int I,
                    int32_t* host_flag, void* stream);
 

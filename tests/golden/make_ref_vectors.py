@@ -15,6 +15,7 @@ the resulting ``ref_vectors.npz`` and never the reference.
 from __future__ import annotations
 
 import importlib.util
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -24,6 +25,8 @@ OUT = Path(__file__).parent / "ref_vectors.npz"
 
 
 def _load_ref():
+    # no bytecode cache: nothing may be written under the read-only reference tree
+    sys.dont_write_bytecode = True
     spec = importlib.util.spec_from_file_location("escha_ref_for_vectors", REF)
     mod = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mod)

@@ -137,6 +137,10 @@ def _weight(K=2, ic=128, oc=128, **kw):
                              device="cpu", **kw)
 
 
+def _linear():
+    return dense.EschaLinear(_weight())
+
+
 def test_weight_infers_K_and_folds_scales():
     w = _weight(K=3, s_in=np.full(128, 0.5, np.float32), s_out=np.full(128, 2.0, np.float32))
     assert w.K == 3 and w.IC == 128 and w.OC == 128
@@ -176,12 +180,109 @@ def test_weight_scale_shape_guard():
 
 
 def test_env_validation(monkeypatch):
-    monkeypatch.setenv("ESCHA_MLX_LUT", "yes")
+    monkeypatch.setenv("ESCHA_MLX_LUT", "maybe")
     with pytest.raises(ValueError, match="ESCHA_MLX_LUT"):
         envs.use_lut()
     monkeypatch.setenv("ESCHA_MLX_DENSE_BLOCK_R", "3")
     with pytest.raises(ValueError, match="ESCHA_MLX_DENSE_BLOCK_R"):
         envs.dense_block_r_pin()
+
+
+@pytest.mark.parametrize("raw,want", [("1", True), ("true", True), (" Yes ", True), ("ON", True),
+                                      ("0", False), ("False", False), ("no", False),
+                                      (" off", False), ("", None)])
+@pytest.mark.parametrize("name,fn,default", [
+    ("ESCHA_MLX_LUT", envs.use_lut, False), ("ESCHA_MLX_FUSED_HAD", envs.fused_had, True),
+    ("ESCHA_HIP_EXACT", envs.use_exact, False), ("ESCHA_MLX_DENSE_MAT", envs.dense_mat, True),
+    ("ESCHA_MLX_BIAS", dense.apply_bias, False)])
+def test_bool_knobs_take_reference_spellings(monkeypatch, name, fn, default, raw, want):
+    """Every boolean knob accepts the reference's spellings, blanks and case
+    ignored (escha_mlx/envs.py:89-95); empty means the default."""
+    monkeypatch.setenv(name, raw)
+    assert fn() is (default if want is None else want)
+
+
+def test_last_logit_knob_spellings(monkeypatch):
+    from escha_mlx_amd import loader
+    monkeypatch.setenv("ESCHA_MLX_LAST_LOGIT", "false")
+    assert loader.use_last_logit() is False
+    monkeypatch.setenv("ESCHA_MLX_LAST_LOGIT", " TRUE ")
+    assert loader.use_last_logit() is True
+    monkeypatch.setenv("ESCHA_MLX_LAST_LOGIT", "2")
+    with pytest.raises(ValueError, match="ESCHA_MLX_LAST_LOGIT"):
+        loader.use_last_logit()
+
+
+@pytest.mark.parametrize("raw", ["1", "2", "4", "8", "16", "32"])
+def test_kt_block_accepted(monkeypatch, raw):
+    monkeypatch.setenv("ESCHA_MLX_KT_BLOCK", raw)
+    assert envs.kt_block() == int(raw)
+
+
+@pytest.mark.parametrize("raw", ["0", "3", "64", "-4", "four"])
+def test_kt_block_rejected(monkeypatch, raw):
+    """The reference's rule (escha_mlx/envs.py:117-121): a power of two up to 32."""
+    monkeypatch.setenv("ESCHA_MLX_KT_BLOCK", raw)
+    with pytest.raises(ValueError, match="ESCHA_MLX_KT_BLOCK"):
+        envs.kt_block()
+
+
+def test_modules_validate_kt_block_and_latch_fused_had(monkeypatch):
+    """Both knobs are read when a module is built: KT_BLOCK is validated,
+    FUSED_HAD is latched (off routes the forward through separate transform
+    launches)."""
+    ex = moe.EschaExperts(np.zeros((2, 8, 16, 32), np.int16), np.ones((2, 128)),
+                          np.ones((2, 256)), device="cpu")
+    dn = moe.EschaExperts(np.zeros((2, 8, 8, 32), np.int16), np.ones((2, 128)),
+                          np.ones((2, 128)), device="cpu")
+    monkeypatch.setenv("ESCHA_MLX_KT_BLOCK", "5")
+    with pytest.raises(ValueError, match="ESCHA_MLX_KT_BLOCK"):
+        moe.EschaMoEExperts(ex, dn, 2, 1)
+    with pytest.raises(ValueError, match="ESCHA_MLX_KT_BLOCK"):
+        _linear()
+    monkeypatch.setenv("ESCHA_MLX_KT_BLOCK", "8")
+    monkeypatch.setenv("ESCHA_MLX_FUSED_HAD", "off")
+    assert moe.EschaMoEExperts(ex, dn, 2, 1)._fused_had is False
+    assert _linear()._fused_had is False
+    monkeypatch.delenv("ESCHA_MLX_FUSED_HAD")
+    assert moe.EschaMoEExperts(ex, dn, 2, 1)._fused_had is True
+
+
+# atomic read-modify-write calls in the HIP sources
+_RMW = re.compile(r"\b(atomic(?:Add|Sub|Or|And|Xor|Max|Min|Exch|CAS|Inc|Dec)\w*|unsafeAtomic\w+|"
+                  r"safeAtomic\w+|__hip_atomic_(?:fetch_\w+|exchange|compare_exchange_\w+)|"
+                  r"__builtin_amdgcn_\w*atomic\w*|__builtin_amdgcn_\w*fadd\w*|"
+                  r"__atomic_\w+)\s*\(")
+
+
+def test_no_float_atomics_in_kernels():
+    """Determinism guard (as the reference's tests/test_moe_determinism.py:138):
+    every float sum in the kernels has a fixed order, so no atomic
+    read-modify-write may touch a float.  Each RMW call site is listed with its
+    integer target; a new one must be added here deliberately, after checking
+    that its operand is an integer."""
+    allowed = {
+        ("basic.hpp", "atomicAdd(&s_cnt[row_expert[r]], 1)"),   # int LDS expert counts
+        ("basic.hpp", "atomicAdd(&s_cnt[e], 1)"),
+        ("fused.hpp", "__hip_atomic_fetch_add(p, v,"),          # add_relaxed(int* p, int v)
+        ("fused.hpp", "__hip_atomic_compare_exchange_strong(p, &expected, 1,"),  # claim(int* p)
+        ("fused.hpp", "atomicOr(p.err, 1)"),                      # int flags
+        ("fused.hpp", "atomicOr(p.status, 1)"),
+    }
+    csrc = Path(ops.__file__).resolve().parent / "csrc"
+    found = set()
+    for f in sorted(csrc.glob("*.hpp")) + sorted(csrc.glob("*.hip")):
+        for line in f.read_text().splitlines():
+            code = line.split("//", 1)[0]
+            for m in _RMW.finditer(code):
+                site = code[m.start():].strip()
+                hit = [a for a in allowed if a[0] == f.name and site.startswith(a[1])]
+                assert hit, f"{f.name}: unlisted atomic read-modify-write: {site}"
+                found.add(hit[0])
+    assert found == allowed, f"listed atomics no longer present: {allowed - found}"
+    # the signatures that make the wrapped atomics integer-only
+    fused = (csrc / "fused.hpp").read_text()
+    assert "int add_relaxed(int* p, int v)" in fused and "bool claim(int* p)" in fused
 
 
 def test_experts_container_validation():

@@ -11,7 +11,10 @@ largest projections are checked directly, not only through smaller stand-ins:
   K=2 5120 x 5120): sampled rows within 1e-3 of the mean |f64| (the matrix
   GEMM's bar), the whole output bit-identical run to run;
 * config 4's MoE layer at batch 32 (E=256, H=2048, I=512, top-8, K=2, 256
-  routed rows): against the oracle's routed block (5e-3 of the max).
+  routed rows): against the oracle's routed block (5e-3 of the max);
+* config 3's headline call (esc_moe_expert_path_layers, several independent
+  token-layers at E=256, H=2048, I=512, top-8, K=2): every layer against the
+  oracle's routed block (5e-3 of the max).
 """
 from __future__ import annotations
 
@@ -108,3 +111,39 @@ def test_config4_moe_batch32_full_size_vs_oracle(monkeypatch):
     print(f"config 4: {len(np.unique(ids_np))} distinct experts, max|diff|/max|oracle| = {err:.2e}")
     assert err < 5e-3, err
     assert torch.equal(blk(x, ids, sc), y)
+
+
+def test_config3_layers_call_full_shape_vs_oracle():
+    """The headline call itself: esc_moe_expert_path_layers at config 3's shape
+    (E=256, H=2048, I=512, top-8, K=2 gate_up and down, one token per layer)
+    over L=5 independent token-layers, every layer's output against the
+    oracle's routed block (5e-3 of the max), then bit-identical on repeat
+    calls with the same workspace (its counters return to zero)."""
+    E, H, I, k, T, L = 256, 2048, 512, 8, 1, 5
+    o = ops()
+    cases = [_moe_case(E, H, I, 2, 2, T, k, 700 + l) for l in range(L)]
+    lays = []
+    for c in cases:
+        ids, sc = o.route_topk(_dev(c["logits"]), k)
+        lays.append({"x": _dev(c["x"]), "ids": ids, "scores": sc,
+                     "gu_code": _dev(c["gu_code"].view(np.int32)), "gu_rin": _dev(c["gu_rin"]),
+                     "gu_rout": _dev(c["gu_rout"]), "dn_code": _dev(c["dn_code"].view(np.int32)),
+                     "dn_rin": _dev(c["dn_rin"]), "dn_rout": _dev(c["dn_rout"]),
+                     "y": torch.empty((T, H), dtype=torch.float16, device=DEV)})
+    table = o.moe_layers_table(lays, DEV)
+    ws = torch.zeros(o.moe_layers_workspace(L, T, k, H, I), dtype=torch.uint8, device=DEV)
+    o.moe_expert_path_layers(table, T, k, E, H, I, 2, 2, ws=ws)
+    first = [lay["y"].clone() for lay in lays]
+    worst = 0.0
+    for c, lay in zip(cases, lays):
+        ids_np, sc_np = lay["ids"].cpu().numpy(), lay["scores"].cpu().numpy()
+        want = _oracle_moe(c, ids_np, sc_np, E, H, I, 2, 2, np.unique(ids_np)).astype(np.float32)
+        got = lay["y"].cpu().numpy().astype(np.float32)
+        err = np.abs(got - want).max() / np.abs(want).max()
+        worst = max(worst, err)
+        assert err < 5e-3, err
+    print(f"config 3 layers call, L={L}: max|diff|/max|oracle| = {worst:.2e}")
+    for _ in range(2):
+        o.moe_expert_path_layers(table, T, k, E, H, I, 2, 2, ws=ws)
+        for f, lay in zip(first, lays):
+            assert torch.equal(lay["y"], f)

@@ -121,6 +121,24 @@ def test_linear_workspace_shared_by_table_and_hash_calls():
             assert torch.equal(ops().linear(*args, lut=lut, ws=ws), first[lut]), lut
 
 
+def test_linear_workspace_shared_two_row_groups():
+    """9-15 rows: the table plan has two 8-row groups per column group, the hash
+    plan one group of all rows.  With more than 32 column groups (K=2, OC >
+    8192) the hash plan's partials would start inside the table plan's second
+    counter block unless the counter region is sized for both; alternating
+    table and hash calls on one workspace must stay bit-identical."""
+    rng = np.random.default_rng(12)
+    K, ic, oc, m = 2, 5120, 12288, 12
+    u32, rin, rout = _proj(rng, ic, oc, K)
+    x = rng.standard_normal((m, ic)).astype(np.float16)
+    ws = torch.zeros(max(ops().linear_workspace(m, K, ic, oc), 4), dtype=torch.uint8, device=DEV)
+    args = (_dev(x), _code(u32), _dev(rin), _dev(rout), K, ic, oc)
+    fresh = {lut: ops().linear(*args, lut=lut, ws=torch.zeros_like(ws)) for lut in (True, False)}
+    for _ in range(3):
+        for lut in (False, True, False, True):
+            assert torch.equal(ops().linear(*args, lut=lut, ws=ws), fresh[lut]), lut
+
+
 def test_module_default_uses_one_launch_linear(monkeypatch):
     """EschaLinear below 16 rows defaults to esc_linear; within tolerance of the
     order-exact module (ESCHA_HIP_EXACT=1), bias included."""

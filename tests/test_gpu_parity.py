@@ -171,6 +171,11 @@ def test_gemm_rows_bit_identical_to_per_row(R_):
     xh_pad = torch.cat([d_xh, torch.zeros((1, IC), dtype=torch.float16, device=DEV)])
     mid = ops().moe_gemm_rows(xh_pad, d_code, rows_idx, group_expert, K, IC, OC, R_, m).cpu().numpy()
     assert np.array_equal(mid[:m].view(np.uint32), per_row.view(np.uint32))
+    # and directly against the oracle's kernel-order GEMV, row by row
+    w = {e: R.reconstruct(codes[e], IC, OC, K) for e in np.unique(re)}
+    for r in range(m):
+        want = R.gemv_ordered(xh[r:r + 1], w[re[r]])[0]
+        assert np.array_equal(mid[r].view(np.uint32), want.view(np.uint32)), r
 
 
 @pytest.mark.parametrize("m", [1, 63, 64, 65, 256, 1000, 1025, 2500])
@@ -447,9 +452,10 @@ def test_moe_multi_launch_path_vs_oracle(E, T, K_gu, K_dn, H, monkeypatch):
 
 
 def test_moe_one_launch_status_and_reuse(monkeypatch):
-    """The one-launch path never hits its bounded wait and leaves its counters
-    zero: repeated calls on one workspace agree bit-for-bit."""
-    E, H, I, k = 256, 2048, 512, 8
+    """The one persistent launch (k_moe_fused: H or I not a multiple of 512)
+    never hits its bounded wait and leaves its counters zero: repeated calls on
+    one workspace agree bit-for-bit and the status flag stays clear."""
+    E, H, I, k = 64, 512, 256, 8
     c = _moe_case(E, H, I, 2, 2, 1, k, 12)
     blk = _block(c, E, k, 2, 2, monkeypatch, exact=False)
     ids, sc = ops().route_topk(torch.from_numpy(c["logits"]).to(DEV), k)
