@@ -57,6 +57,9 @@ SIGNATURES = {
     "esc_moe_block_out": (_I, [_P, _P, _P, _I, _I, _P, _P]),
     "esc_q8_embed": (_I, [_P, _I, _P, _P, _I, _I, _P, _P]),
     "esc_moe_expert_path_workspace": (_Z, [_I, _I, _I, _I, _I]),
+    "esc_moe_expert_path_static_max": (_Z, []),
+    "esc_moe_expert_path_static": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _P,
+                                        _P, _I, _I, _P, _P]),
     "esc_moe_status": (_I, [_P, _Z, _I, _I, _I, _I, _P, _P]),
     "esc_moe_layers_workspace": (_Z, [_I, _I, _I, _I, _I]),
     "esc_moe_expert_path_layers": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),

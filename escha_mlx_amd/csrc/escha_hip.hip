@@ -63,6 +63,15 @@ int ensure_lut() {
   return ESC_OK;
 }
 
+bool lut_ready() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  return g_lut_ready[dev];
+}
+
+int ensure_scratch(void** out);
+
 int check_proj(int K, int IC, int OC) {
   ESC_REQUIRE(K == 2 || K == 3, "escha code implies K=%d; this runtime implements K in [2, 3]", K);
   ESC_REQUIRE(IC > 0 && OC > 0 && IC % 128 == 0 && OC % 128 == 0,
@@ -344,7 +353,11 @@ int esc_version(void) { return 100; }
 
 const char* esc_last_error(void) { return g_err.c_str(); }
 
-int esc_init(void) { return ensure_lut(); }
+int esc_init(void) {
+  if (int rc = ensure_lut()) return rc;
+  void* ptr = nullptr;
+  return ensure_scratch(&ptr);
+}
 
 int esc_decode_tiles(const uint32_t* code, int K, int IC, int OC, int use_lut, uint16_t* w,
                      void* stream) {
@@ -831,7 +844,9 @@ struct MoePlan {
   int M, S1, S2, R, n_groups;
   size_t off_xh, off_p1, off_xh2, off_p2, off_rows, off_gexp, total;
 };
-MoePlan moe_plan(int T, int top_k, int E, int H, int I, int K_gu, int K_dn) {
+// base: bytes at the start of the workspace left to the caller (the
+// no-allocation variant keeps its counters there).
+MoePlan moe_plan(int T, int top_k, int E, int H, int I, int K_gu, int K_dn, size_t base = 0) {
   MoePlan p;
   p.M = T * top_k;
   p.R = E <= 4096 ? moe_group_rows(p.M, E) : 0;
@@ -843,7 +858,7 @@ MoePlan moe_plan(int T, int top_k, int E, int H, int I, int K_gu, int K_dn) {
   p.S1 = fast_splits(K_gu, eff, H / 16, 2 * I / 16);
   p.S2 = fast_splits(K_dn, eff, I / 16, H / 16);
   auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
-  p.off_xh = 0;
+  p.off_xh = al(base);
   p.off_p1 = al(p.off_xh + (size_t)p.M * H * 2);
   p.off_xh2 = al(p.off_p1 + (size_t)p.S1 * p.M * 2 * I * 4);
   p.off_p2 = al(p.off_xh2 + (size_t)p.M * I * 2);
@@ -909,7 +924,12 @@ constexpr int kKtbBlocks = 32;
 constexpr int kGateUpWavesSingle = 16, kDownBlockWavesSingle = 16;
 constexpr int kDownBlockWavesLayers = 4;
 
-FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput) {
+// int_region > 0: the integer counters sit at offset 0 in a region of that
+// many bytes and the float data after it, so calls of different shapes on one
+// workspace never find another call's floats where their counters are (the
+// no-allocation variant; the caller checks n_int * 4 <= int_region).
+FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput,
+                     size_t int_region = 0) {
   // the two-launch path (throughput) uses the large items; the one-launch
   // path the small ones (KTA = 8, KTB = 4), which spread one token-layer wide
   const bool large = throughput;
@@ -929,12 +949,13 @@ FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput) {
   f.grid = throughput ? std::min(L * std::max(f.nA, f.nB), 1024)
                       : std::min(std::max(f.nA, f.nB), 2048);
   auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
-  f.off_pa = 0;
-  f.off_pb = al((size_t)L * f.nA * 256 * 4);
-  f.off_xh2 = f.off_pb + al((size_t)L * f.nB * 256 * 4);
-  f.off_int = f.off_xh2 + al((size_t)L * f.M * I * 2);
   f.n_int = L * (f.M * f.NB + f.nA + T * f.NCP) + 3;
-  f.total = f.off_int + al((size_t)f.n_int * 4);
+  f.off_pa = al(int_region);
+  f.off_pb = f.off_pa + al((size_t)L * f.nA * 256 * 4);
+  f.off_xh2 = f.off_pb + al((size_t)L * f.nB * 256 * 4);
+  const size_t end = f.off_xh2 + al((size_t)L * f.M * I * 2);
+  f.off_int = int_region ? 0 : end;
+  f.total = int_region ? end : end + al((size_t)f.n_int * 4);
   return f;
 }
 
@@ -1046,12 +1067,16 @@ int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int
   return hip_check(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
 }
 
-int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, int T,
-                        int top_k, int E, int H, int I, const uint32_t* gu_code,
-                        const float* gu_rin, const float* gu_rout, int K_gu,
-                        const uint32_t* dn_code, const float* dn_rin, const float* dn_rout,
-                        int K_dn, int use_lut, uint16_t* y, void* ws, size_t ws_bytes,
-                        void* stream) {
+}  // extern "C"
+
+namespace {
+// The expert path on a given workspace; int_region > 0 puts every counter in
+// a fixed region at its start (see fused_plan).
+int moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, int T, int top_k,
+                    int E, int H, int I, const uint32_t* gu_code, const float* gu_rin,
+                    const float* gu_rout, int K_gu, const uint32_t* dn_code, const float* dn_rin,
+                    const float* dn_rout, int K_dn, int use_lut, uint16_t* y, void* ws,
+                    size_t ws_bytes, size_t int_region, void* stream) {
   ESC_REQUIRE(x && ids && scores && gu_code && gu_rin && gu_rout && dn_code && dn_rin && dn_rout &&
                   y,
               "null pointer");
@@ -1060,27 +1085,24 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
   if (int rc = check_proj(K_dn, I, H)) return rc;
   ESC_REQUIRE(T >= 0, "negative token count");
   if (T == 0) return ESC_OK;
-  if (fused_eligible(T, top_k, H, I) && throughput_ok(H, I)) {
-    // two launches (gate_up items, down items + combine): measured faster
-    // than the single persistent launch for one token-layer on gfx950
-    const FusedPlan f = fused_plan(1, T, top_k, H, I, true);
-    if (!ws || ws_bytes < f.total)
-      return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, f.total);
-    esc::FusedMoe p = fused_args(f, ws, T, top_k, H, I);
-    p.l0 = esc::MoeLayer{x, ids, scores, gu_code, gu_rin, gu_rout, dn_code, dn_rin, dn_rout, y};
-    p.layers = nullptr;
-    return launch_fused<true>(p, K_gu, K_dn, f.grid, S(stream));
-  }
   if (fused_eligible(T, top_k, H, I)) {
-    const FusedPlan f = fused_plan(1, T, top_k, H, I, false);
+    // throughput_ok: two launches (gate_up items, down items + combine),
+    // measured faster than the single persistent launch for one token-layer
+    // on gfx950; otherwise the single persistent launch
+    const bool two = throughput_ok(H, I);
+    const FusedPlan f = fused_plan(1, T, top_k, H, I, two, int_region);
+    if (int_region && (size_t)f.n_int * 4 > int_region)
+      return fail(ESC_ENOSPACE, "%d counters exceed the %zu-byte counter region", f.n_int,
+                  int_region);
     if (!ws || ws_bytes < f.total)
       return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, f.total);
     esc::FusedMoe p = fused_args(f, ws, T, top_k, H, I);
     p.l0 = esc::MoeLayer{x, ids, scores, gu_code, gu_rin, gu_rout, dn_code, dn_rin, dn_rout, y};
     p.layers = nullptr;
-    return launch_fused<false>(p, K_gu, K_dn, f.grid, S(stream));
+    return two ? launch_fused<true>(p, K_gu, K_dn, f.grid, S(stream))
+               : launch_fused<false>(p, K_gu, K_dn, f.grid, S(stream));
   }
-  const MoePlan p = moe_plan(T, top_k, E, H, I, K_gu, K_dn);
+  const MoePlan p = moe_plan(T, top_k, E, H, I, K_gu, K_dn, int_region);
   if (!ws || ws_bytes < p.total)
     return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, p.total);
   if (use_lut)
@@ -1123,6 +1145,79 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
   hipLaunchKernelGGL(esc::k_moe_combine, dim3(H / 128, T), dim3(64), 0, s, p2, p.S2, p.M, H, ids,
                      scores, top_k, dn_rout, rs, y);
   return launched("k_moe_combine");
+}
+
+// ---- the expert path without allocation: a file-scope device scratch array
+// Its counters sit in the first kStaticIntBytes (zeroed once per device at
+// set-up, left zero by every call), the float data after them.
+constexpr size_t kStaticScratchBytes = size_t(4) << 20;
+constexpr size_t kStaticIntBytes = size_t(128) << 10;
+}  // namespace
+
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+// Device address of `scratch` per device (the symbol's host-side name is not
+// a device address): looked up once per device, with that device current,
+// and its counter region zeroed by a fill kernel.
+void* g_scratch_ptr[kMaxDevices];
+
+__global__ void k_zero_words(uint32_t* p, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+int ensure_scratch(void** out) {
+  int dev = 0;
+  if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return fail(ESC_EINVAL, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (int rc = hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress"))
+      return rc;
+    if (!ptr) return fail(ESC_EHIP, "hipGetSymbolAddress returned a null scratch address");
+    hipLaunchKernelGGL(k_zero_words, dim3(64), dim3(256), 0, 0, static_cast<uint32_t*>(ptr),
+                       kStaticIntBytes / 4);
+    if (int rc = launched("k_zero_words")) return rc;
+    if (int rc = hip_check(hipDeviceSynchronize(), "scratch set-up sync")) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ESC_OK;
+}
+}  // namespace
+
+extern "C" {
+int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, int T,
+                        int top_k, int E, int H, int I, const uint32_t* gu_code,
+                        const float* gu_rin, const float* gu_rout, int K_gu,
+                        const uint32_t* dn_code, const float* dn_rin, const float* dn_rout,
+                        int K_dn, int use_lut, uint16_t* y, void* ws, size_t ws_bytes,
+                        void* stream) {
+  return moe_expert_path(x, ids, scores, T, top_k, E, H, I, gu_code, gu_rin, gu_rout, K_gu,
+                         dn_code, dn_rin, dn_rout, K_dn, use_lut, y, ws, ws_bytes, 0, stream);
+}
+
+size_t esc_moe_expert_path_static_max(void) { return kStaticScratchBytes; }
+
+int esc_moe_expert_path_static(const uint16_t* x, const int32_t* ids, const float* scores, int T,
+                               int top_k, int E, int H, int I, const uint32_t* gu_code,
+                               const float* gu_rin, const float* gu_rout, int K_gu,
+                               const uint32_t* dn_code, const float* dn_rin,
+                               const float* dn_rout, int K_dn, int use_lut, uint16_t* y,
+                               void* stream) {
+  ESC_REQUIRE(T >= 0 && top_k >= 1 && H > 0 && I > 0, "bad sizes T=%d top_k=%d H=%d I=%d", T,
+              top_k, H, I);
+  if (T == 0) return ESC_OK;
+  // the table, when asked for, is built by esc_init (a kernel, no allocation)
+  ESC_REQUIRE(!use_lut || lut_ready(), "use_lut needs esc_init() on this device first");
+  void* ptr = nullptr;
+  if (int rc = ensure_scratch(&ptr)) return rc;
+  return moe_expert_path(x, ids, scores, T, top_k, E, H, I, gu_code, gu_rin, gu_rout, K_gu,
+                         dn_code, dn_rin, dn_rout, K_dn, use_lut, y, ptr, kStaticScratchBytes,
+                         kStaticIntBytes, stream);
 }
 
 size_t esc_moe_layers_workspace(int L, int T, int top_k, int H, int I) {

@@ -337,6 +337,32 @@ def moe_expert_path(x, ids, scores, gu_code, gu_rin, gu_rout, K_gu, dn_code, dn_
     return y
 
 
+def moe_expert_path_static_max() -> int:
+    """Bytes of the device scratch array esc_moe_expert_path_static uses."""
+    return int(_lib.load().esc_moe_expert_path_static_max())
+
+
+def moe_expert_path_static(x, ids, scores, gu_code, gu_rin, gu_rout, K_gu, dn_code, dn_rin,
+                           dn_rout, K_dn, out, lut=None):
+    """moe_expert_path with no allocation in the call: scratch from the
+    library's device array, output into the caller's ``out`` [T, H] f16.
+    Calls that overlap on one GPU race (they share the array)."""
+    _dev(x, ids, scores, gu_code, gu_rin, gu_rout, dn_code, dn_rin, dn_rout, out)
+    t, h = x.shape
+    k = ids.shape[1]
+    E = gu_code.shape[0]
+    I = gu_rout.shape[1] // 2
+    if ids.dtype != torch.int32 or scores.dtype != torch.float32:
+        raise ValueError("ids must be int32 and scores float32")
+    if out.dtype != torch.float16 or tuple(out.shape) != (t, h) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous float16 [{t}, {h}] tensor")
+    _lib.call("esc_moe_expert_path_static", _ptr(x), _ptr(ids), _ptr(scores), t, k, E, h, I,
+              _ptr(_as_u32(gu_code)), _ptr(gu_rin), _ptr(gu_rout), K_gu,
+              _ptr(_as_u32(dn_code)), _ptr(dn_rin), _ptr(dn_rout), K_dn, _lut_flag(lut),
+              _ptr(out), _stream())
+    return out
+
+
 def swiglu(gu16: torch.Tensor) -> torch.Tensor:
     """f16 [m, 2I] -> f16 [m, I]: f16(f16(silu(g)) * u), gate = first half (ref.py:296-301)."""
     _dev(gu16)

@@ -233,6 +233,27 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
                         int K_dn, int use_lut, uint16_t* y, void* ws, size_t ws_bytes,
                         void* stream);
 
+/* esc_moe_expert_path without allocation: the same computation and outputs
+ * (the same kernels), with its scratch (partials, counters, down inputs) in a
+ * file-scope device array of esc_moe_expert_path_static_max() bytes (4 MiB)
+ * that each GPU holds until the process ends, instead of a caller workspace.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The call itself allocates nothing: the array's device address
+ * is looked up and its counter region zeroed by esc_init() (or by the first
+ * call on a device).  Shapes whose plan needs more scratch are rejected with
+ * ESC_ENOSPACE (T * top_k <= 64 rows at H = 2048, I = 512 fit).  Every call
+ * on a GPU shares that GPU's array: calls that overlap on one GPU (concurrent
+ * streams, threads) race and must be serialised by the caller.  use_lut needs
+ * esc_init() on the device first. */
+size_t esc_moe_expert_path_static_max(void);
+int esc_moe_expert_path_static(const uint16_t* x, const int32_t* ids, const float* scores, int T,
+                               int top_k, int E, int H, int I, const uint32_t* gu_code,
+                               const float* gu_rin, const float* gu_rout, int K_gu,
+                               const uint32_t* dn_code, const float* dn_rin,
+                               const float* dn_rout, int K_dn, int use_lut, uint16_t* y,
+                               void* stream);
+
 /* One token-layer of routed experts for esc_moe_expert_path_layers (device
  * pointers; the same tensors esc_moe_expert_path takes). */
 typedef struct {

@@ -1,0 +1,120 @@
+"""esc_moe_expert_path_static (the expert path with its scratch in the
+library's device array, no allocation in the call) against esc_moe_expert_path
+(caller workspace), through the C-ABI.
+
+Both run the same kernels on the same inputs, so their outputs must be
+bit-identical.  The static array keeps the previous call's contents: the calls
+run in a row with shapes that shrink (and a shape of the other kernel path in
+between), so a counter left where another shape keeps data would show.  The
+order-exact chain and the oracle pin the regular entry point elsewhere; here
+the expert path's output is also held to the oracle at one shape.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref_np as R
+
+from .conftest import has_gpu
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not has_gpu(), reason="needs a ROCm GPU")]
+
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    print(f"\n[gpu case] {request.node.nodeid}", flush=True)
+    yield
+    torch.cuda.synchronize()
+
+
+def _case(E, H, I, T, k, seed):
+    rng = np.random.default_rng(seed)
+    u32 = lambda *s: rng.integers(0, 2**32, size=s, dtype=np.uint64).astype(np.uint32)
+    c = dict(gu_code=u32(E, H // 16, 2 * I // 16, 16), dn_code=u32(E, I // 16, H // 16, 16),
+             gu_rin=rng.choice([-1.0, 1.0], (E, H)).astype(np.float32),
+             dn_rin=rng.choice([-1.0, 1.0], (E, I)).astype(np.float32),
+             gu_rout=(rng.choice([-1.0, 1.0], (E, 2 * I)) * rng.uniform(0.5, 1.5, (E, 2 * I))
+                      * 4e-2).astype(np.float32),
+             dn_rout=(rng.choice([-1.0, 1.0], (E, H)) * rng.uniform(0.5, 1.5, (E, H))
+                      * 4e-2).astype(np.float32),
+             x=rng.standard_normal((T, H)).astype(np.float16),
+             logits=rng.standard_normal((T, E)).astype(np.float32))
+    return c
+
+
+def _device(c, k):
+    from escha_mlx_amd import ops
+    d = {n: torch.from_numpy(np.ascontiguousarray(v)).to(DEV) for n, v in c.items()}
+    d["gu_code"] = d["gu_code"].view(torch.int32)
+    d["dn_code"] = d["dn_code"].view(torch.int32)
+    d["ids"], d["scores"] = ops.route_topk(d["logits"], k)
+    return d
+
+
+def _both(d, K=2):
+    """(static entry point's output, regular entry point's output)."""
+    from escha_mlx_amd import ops
+    args = (d["x"], d["ids"], d["scores"], d["gu_code"], d["gu_rin"], d["gu_rout"], K,
+            d["dn_code"], d["dn_rin"], d["dn_rout"], K)
+    y_s = torch.full(tuple(d["x"].shape), float("nan"), dtype=torch.float16, device=DEV)
+    ops.moe_expert_path_static(*args, out=y_s)
+    y_r = ops.moe_expert_path(*args)
+    return y_s, y_r
+
+
+def test_static_expert_path_equals_workspace_path_in_a_row():
+    """Two calls in a row at config 3's expert shape (E=256, H=2048, I=512,
+    top-8, K=2), the second with fewer tokens, then a shape of the one
+    persistent launch, then the first shape again: each bit-identical to the
+    workspace entry point."""
+    from escha_mlx_amd import ops
+    k = 8
+    big = _device(_case(256, 2048, 512, 4, k, 901), k)
+    small = _device(_case(256, 2048, 512, 1, k, 902), k)
+    other = _device(_case(64, 512, 256, 2, k, 903), k)
+    for name, d in (("T=4", big), ("T=1", small), ("persistent T=2", other), ("T=4 again", big),
+                    ("T=1 again", small)):
+        y_s, y_r = _both(d)
+        torch.cuda.synchronize()
+        assert not torch.isnan(y_s.float()).any(), name
+        assert torch.equal(y_s.view(torch.int16), y_r.view(torch.int16)), name
+
+
+def test_static_expert_path_vs_oracle():
+    """The static call's output at T=1 against the oracle's routed block."""
+    E, H, I, k = 256, 2048, 512, 8
+    c = _case(E, H, I, 1, k, 904)
+    d = _device(c, k)
+    y_s, _ = _both(d)
+    ids, sc = d["ids"].cpu().numpy(), d["scores"].cpu().numpy()
+    w_gu = np.zeros((E, H, 2 * I), np.float16)
+    w_dn = np.zeros((E, I, H), np.float16)
+    for e in np.unique(ids):
+        w_gu[e] = R.reconstruct(c["gu_code"][e], H, 2 * I, 2)
+        w_dn[e] = R.reconstruct(c["dn_code"][e], I, H, 2)
+    want = R.moe_routed(c["x"], ids, sc, {"w": w_gu, "rin": c["gu_rin"], "rout": c["gu_rout"]},
+                        {"w": w_dn, "rin": c["dn_rin"], "rout": c["dn_rout"]}, 2, 2,
+                        ordered=True).astype(np.float32)
+    got = y_s.cpu().numpy().astype(np.float32)
+    assert np.abs(got - want).max() / np.abs(want).max() < 5e-3
+
+
+def test_static_expert_path_rejects_oversize():
+    """A shape whose plan needs more than the array holds is refused with a
+    clear error and leaves the array usable."""
+    from escha_mlx_amd import ops
+    k = 8
+    huge = _device(_case(256, 2048, 512, 48, k, 905), k)
+    y = torch.empty((48, 2048), dtype=torch.float16, device=DEV)
+    with pytest.raises(ValueError, match="workspace|counter region"):
+        ops.moe_expert_path_static(huge["x"], huge["ids"], huge["scores"], huge["gu_code"],
+                                   huge["gu_rin"], huge["gu_rout"], 2, huge["dn_code"],
+                                   huge["dn_rin"], huge["dn_rout"], 2, out=y)
+    small = _device(_case(256, 2048, 512, 1, k, 906), k)
+    y_s, y_r = _both(small)
+    assert torch.equal(y_s.view(torch.int16), y_r.view(torch.int16))
+    assert ops.moe_expert_path_static_max() == 4 << 20
