@@ -11,8 +11,9 @@ every step reads its experts cold.
 
 Two measurements, both one token per layer (batch 1):
   sustained (the `value`): the 40 token-layers are independent and go to the
-      GPU as ONE esc_moe_expert_path_layers call (two kernels: every gate_up
-      item, then every down item); steady-state coded-weight throughput.
+      GPU as ONE esc_moe_expert_path_layers call (three kernels: every gate_up
+      item, every down item, the slot combine; the decode takes 4 of every 8
+      step pairs from a table in LDS); steady-state coded-weight throughput.
   chained (`tok_s`): a decode step -- layer l's output is layer l+1's input --
       as 40 calls of the drop-in esc_moe_expert_path; tok/s = 1 / step.
 Inputs are resident in HBM before timing starts; HIP events on the launch stream.
@@ -48,8 +49,9 @@ BYTES_TOKEN_LAYER = TOP_K * (BYTES_GU + BYTES_DN)   # 6,291,456
 HBM_PEAK_GBS = 8000.0
 ROUTE_SETS = 4
 COPY_BYTES = 1 << 30                   # counter calibration copy
-KERNELS = ("k_moe_gate_up_items", "k_moe_down_blocks")
-SUSTAINED_KERNELS = "k_moe_gate_up_items<2,16,true,4> + k_moe_down_blocks<2,2,true,4>"
+KERNELS = ("k_moe_layers_gu", "k_moe_layers_dn", "k_moe_layers_combine")
+SUSTAINED_KERNELS = ("k_moe_layers_gu + k_moe_layers_dn + k_moe_layers_combine "
+                     "(table-assisted decode, 4 of 8 step pairs from LDS)")
 
 
 def parse():
@@ -66,9 +68,10 @@ def parse():
     ap.add_argument("--probe", action="store_true",
                     help="run the calibration copy and two sustained calls (config 6: two head "
                          "calls), untimed, as the PMC target")
-    ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5, 6], default=3,
+    ap.add_argument("--config", choices=["1", "2", "3", "4", "5", "6", "ceiling"], default="3",
                     help="BASELINE config; 3 (the headline metric) by default; 6 is not a "
-                         "BASELINE config: the w8a16 vocabulary-head GEMV around the MoE block")
+                         "BASELINE config: the w8a16 vocabulary-head GEMV around the MoE block; "
+                         "'ceiling': the decode-rate probe (hash, table and mixes)")
     return ap.parse_args()
 
 
@@ -629,8 +632,50 @@ def run_q8_head(args):
     return res
 
 
+def bench_ceiling(args, torch, ops):
+    """The decode-rate ceiling: esc_decode_probe streams cold K=2 code (1 GiB at
+    16 waves per CU) through the expert GEMVs' decode + dot2 loop, with nt of
+    every 8 step pairs from the table in LDS and the rest by hash."""
+    dev = "cuda:0"
+    stream = torch.cuda.current_stream()
+    steps = 256
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    words = max(ops.decode_probe_words(steps, w) for w in (16, 32))
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    code = torch.randint(-2**31, 2**31 - 1, (words,), generator=g, device=dev, dtype=torch.int32)
+    out = torch.empty(words // (4 * steps), dtype=torch.float32, device=dev)
+    rows, hash16 = [], None
+    cases = [(0, 32, 1), (0, 32, 2)] + [(nt, 16, pf) for nt in (0, 2, 3, 4, 5, 6, 8)
+                                         for pf in (1, 2, 3)]
+    for nt, wpc, pf in cases:
+        ms = timed(torch, lambda i: ops.decode_probe(code, steps, nt, wpc, out, pf), 5, 2, stream)
+        weights = cus * wpc * steps * 4096
+        row = {"table_pairs_of_8": nt, "waves_per_cu": wpc, "prefetch_steps": pf,
+               "us": round(ms * 1e3, 1), "coded_tbs": round(weights / 4 / (ms * 1e-3) / 1e12, 3),
+               "weights_per_cu_clk_2p4ghz": round(weights / (ms * 1e-3) / cus / 2.4e9, 2)}
+        if wpc == 16:
+            # the table is the hash's image and the pairs are summed in the
+            # same order: every mix gives the hash path's outputs bit-for-bit
+            if nt == 0 and pf == 1:
+                hash16 = out.clone()
+            else:
+                row["bit_identical_to_hash"] = bool(torch.equal(out, hash16))
+        rows.append(row)
+    best = max(rows, key=lambda r: r["coded_tbs"])
+    return {"metric": "decode-rate ceiling: coded TB/s of the K=2 decode + dot2 loop alone",
+            "value": best["coded_tbs"], "unit": "TB/s", "n_gpus": 1, "steps": 5, "warmup": 2,
+            "ms_per_step": best["us"] / 1e3, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "u32 codes -> f16 weights (hash / table), f32 dot2",
+            "data": "synthetic: uniform-random code, 1 GiB per 16 waves per CU (cold)",
+            "config": {"workload": "esc_decode_probe: persistent workgroups of 1024 threads, "
+                                   f"{steps} wave-steps (1 KiB) per wave, fixed inputs"},
+            "rows": rows, "best": best}
+
+
 def main():
     args = parse()
+    args.config = int(args.config) if args.config != "ceiling" else "ceiling"
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus N>1 is not supported "
                                    "(the sharding design is described, not built)"}))
@@ -646,7 +691,9 @@ def main():
         from escha_mlx_amd import ops
         torch.cuda.set_device(0)
         ops.init()
-        if args.config == 4:
+        if args.config == "ceiling":
+            res = bench_ceiling(args, torch, ops)
+        elif args.config == 4:
             res = bench_c4(args, torch, ops)
         else:
             res = bench_dense(args, torch, ops, args.config)

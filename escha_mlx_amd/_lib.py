@@ -58,6 +58,8 @@ SIGNATURES = {
     "esc_q8_embed": (_I, [_P, _I, _P, _P, _I, _I, _P, _P]),
     "esc_moe_expert_path_workspace": (_Z, [_I, _I, _I, _I, _I]),
     "esc_moe_expert_path_static_max": (_Z, []),
+    "esc_decode_probe_words": (_Z, [_I, _I]),
+    "esc_decode_probe": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "esc_moe_expert_path_static": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _P,
                                         _P, _I, _I, _P, _P]),
     "esc_moe_status": (_I, [_P, _Z, _I, _I, _I, _I, _P, _P]),

@@ -16,6 +16,8 @@
 #include "mfma.hpp"
 #include "linear.hpp"
 #include "q8.hpp"
+#include "probe.hpp"
+#include "layers.hpp"
 
 namespace {
 
@@ -1033,6 +1035,101 @@ int launch_fused(const esc::FusedMoe& p, int K_gu, int K_dn, int grid, hipStream
     return K_dn == 2 ? launch_fused_k<2, 2, TP>(p, grid, s) : launch_fused_k<2, 3, TP>(p, grid, s);
   return K_dn == 2 ? launch_fused_k<3, 2, TP>(p, grid, s) : launch_fused_k<3, 3, TP>(p, grid, s);
 }
+
+// ---- many-layer calls: the table-assisted kernels (K=2 gate_up and down,
+// layers.hpp) or the item kernels above (any other K).  One workspace serves
+// both: the item kernels' counters at offset 0, the table-assisted kernels'
+// group counters after them, and each path's float data after both counter
+// regions, so calls of either path on one workspace never find the other's
+// floats where their counters are.
+struct LayersWs {
+  FusedPlan f;  // the item kernels' plan
+  size_t off_cnt_gu, off_cnt_dn, off_part, off_xh2, off_rows, total;
+};
+
+LayersWs layers_ws(int L, int T, int top_k, int H, int I) {
+  auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
+  LayersWs w;
+  const size_t M = (size_t)T * top_k, NB = I / 128, NKC = H / 128, NCP = H / 256;
+  w.off_cnt_gu = al((size_t)fused_plan(L, T, top_k, H, I, true).n_int * 4);
+  w.off_cnt_dn = w.off_cnt_gu + al(L * M * NB * 4);
+  const size_t ireg = w.off_cnt_dn + al(L * M * NCP * 4);
+  w.f = fused_plan(L, T, top_k, H, I, true, ireg);
+  // partials: at most one slot per item of a group (one item per wave)
+  w.off_part = ireg;
+  const size_t part = std::max(L * M * NB * NKC, L * M * NCP * esc::kDownEighths) * 1024;
+  w.off_xh2 = w.off_part + al(part);
+  w.off_rows = w.off_xh2 + al(L * M * I * 2);
+  w.total = std::max(w.f.total, w.off_rows + al(L * M * H * 2));
+  return w;
+}
+
+bool layers_table_ok(int K_gu, int K_dn, int I) {
+  return K_gu == 2 && K_dn == 2 && I <= esc::kLayersMaxI;
+}
+
+int launch_layers_table(const esc::MoeLayer* layers, const LayersWs& w, void* ws, int L, int T,
+                        int top_k, int H, int I, hipStream_t s) {
+  if (int rc = ensure_lut()) return rc;
+  static std::once_flag attr_once;
+  static hipError_t attr_err = hipSuccess;
+  std::call_once(attr_once, [] {
+    const void* kerns[] = {(const void*)esc::k_moe_layers_gu, (const void*)esc::k_moe_layers_dn<1>,
+                           (const void*)esc::k_moe_layers_dn<2>};
+    for (const void* k : kerns) {
+      const hipError_t e =
+          hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 65536 * 2);
+      if (e != hipSuccess) attr_err = e;
+    }
+  });
+  if (int rc = hip_check(attr_err, "hipFuncSetAttribute")) return rc;
+  esc::LayersMoe p{};
+  p.layers = layers;
+  p.ws = static_cast<char*>(ws);
+  p.off_part = w.off_part;
+  p.off_xh2 = w.off_xh2;
+  p.off_rows = w.off_rows;
+  p.L = L;
+  p.T = T;
+  p.top_k = top_k;
+  p.H = H;
+  p.I = I;
+  p.M = T * top_k;
+  p.NB = I / 128;
+  p.NKC = H / 128;
+  p.NHB = H / 128;
+  const int cus = device_cus();
+  const long na = (long)L * p.M * p.NB * p.NKC, nd = (long)L * p.M * (p.NHB / 2) * esc::kDownEighths;
+  ESC_REQUIRE(na < (1L << 30) && nd < (1L << 30), "too many items (%ld, %ld)", na, nd);
+  // one workgroup per CU, more when a wave would otherwise run more than
+  // kLayersMaxRange items (its items' pointers are staged in LDS); each
+  // wave runs P consecutive items, so a group of `size` items spans at most
+  // (size + P - 2) / P + 1 waves
+  auto plan = [&](long n, int size, int& grid) {
+    const long wg = esc::kLayersWaves;
+    grid = (int)std::max(std::min<long>(cus, (n + wg - 1) / wg),
+                         (n + wg * esc::kLayersMaxRange - 1) / (wg * esc::kLayersMaxRange));
+    p.P = (int)((n + wg * grid - 1) / (wg * grid));
+    p.maxc = std::min(size, (size + p.P - 2) / p.P + 1);
+  };
+  const dim3 blk(64 * esc::kLayersWaves);
+  const size_t lds = 65536 * 2;
+  int grid = 0;
+  plan(na, p.NKC, grid);
+  p.off_cnt = w.off_cnt_gu;
+  hipLaunchKernelGGL(esc::k_moe_layers_gu, dim3(grid), blk, lds, s, p);
+  if (int rc = launched("k_moe_layers_gu")) return rc;
+  plan(nd, esc::kDownEighths, grid);
+  p.off_cnt = w.off_cnt_dn;
+  // the down items' inputs: I/16 words, one or two registers per lane
+  if (I <= 1024)
+    hipLaunchKernelGGL(esc::k_moe_layers_dn<1>, dim3(grid), blk, lds, s, p);
+  else
+    hipLaunchKernelGGL(esc::k_moe_layers_dn<2>, dim3(grid), blk, lds, s, p);
+  if (int rc = launched("k_moe_layers_dn")) return rc;
+  hipLaunchKernelGGL(esc::k_moe_layers_combine, dim3((L * T * p.NHB + 3) / 4), dim3(256), 0, s, p);
+  return launched("k_moe_layers_combine");
+}
 }  // namespace
 
 extern "C" {
@@ -1223,7 +1320,7 @@ int esc_moe_expert_path_static(const uint16_t* x, const int32_t* ids, const floa
 size_t esc_moe_layers_workspace(int L, int T, int top_k, int H, int I) {
   if (L <= 0 || T <= 0 || top_k <= 0 || !fused_eligible(T, top_k, H, I) || !throughput_ok(H, I))
     return 0;
-  return fused_plan(L, T, top_k, H, I, true).total;
+  return layers_ws(L, T, top_k, H, I).total;
 }
 
 int esc_moe_expert_path_layers(const esc_moe_layer* layers, int L, int T, int top_k, int E, int H,
@@ -1240,12 +1337,61 @@ int esc_moe_expert_path_layers(const esc_moe_layer* layers, int L, int T, int to
               "512, H <= 7936 (got T=%d top_k=%d H=%d I=%d)",
               kFusedMaxRows, T, top_k, H, I);
   if (L == 0 || T == 0) return ESC_OK;
-  const FusedPlan f = fused_plan(L, T, top_k, H, I, true);
-  if (!ws || ws_bytes < f.total)
-    return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, f.total);
-  esc::FusedMoe p = fused_args(f, ws, T, top_k, H, I);
-  p.layers = reinterpret_cast<const esc::MoeLayer*>(layers);
-  return launch_fused<true>(p, K_gu, K_dn, f.grid, S(stream));
+  const LayersWs w = layers_ws(L, T, top_k, H, I);
+  if (!ws || ws_bytes < w.total)
+    return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, w.total);
+  const auto* lr = reinterpret_cast<const esc::MoeLayer*>(layers);
+  if (layers_table_ok(K_gu, K_dn, I))
+    return launch_layers_table(lr, w, ws, L, T, top_k, H, I, S(stream));
+  esc::FusedMoe p = fused_args(w.f, ws, T, top_k, H, I);
+  p.layers = lr;
+  return launch_fused<true>(p, K_gu, K_dn, w.f.grid, S(stream));
+}
+
+
+// ---- decode-rate probe (measurement only)
+size_t esc_decode_probe_words(int steps, int waves_per_cu) {
+  if (steps <= 0 || steps % 4 || (waves_per_cu != 16 && waves_per_cu != 32)) return 0;
+  return (size_t)device_cus() * waves_per_cu * steps * 64 * 4;
+}
+
+int esc_decode_probe(const uint32_t* code, int steps, int nt, int waves_per_cu, int prefetch,
+                     float* out, void* stream) {
+  ESC_REQUIRE(code && out, "null pointer");
+  ESC_REQUIRE(steps > 0 && steps % 4 == 0, "steps must be a positive multiple of 4");
+  ESC_REQUIRE(waves_per_cu == 16 || waves_per_cu == 32, "waves per CU must be 16 or 32");
+  ESC_REQUIRE(nt == 0 || waves_per_cu == 16, "the table (nt > 0) fits one workgroup per CU");
+  ESC_REQUIRE(prefetch >= 1 && prefetch <= 3, "prefetch depth must be 1, 2 or 3");
+  if (nt > 0)
+    if (int rc = ensure_lut()) return rc;
+  const dim3 grid(device_cus() * (waves_per_cu / 16)), blk(1024);
+  const size_t lds = nt > 0 ? 131072 : 0;
+  auto go = [&](auto kern) -> int {
+    if (lds)
+      if (int rc = hip_check(hipFuncSetAttribute((const void*)kern,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds),
+                             "hipFuncSetAttribute"))
+        return rc;
+    hipLaunchKernelGGL(kern, grid, blk, lds, S(stream), code, steps, out);
+    return launched("k_decode_probe");
+  };
+  auto by_pf = [&](auto k1, auto k2, auto k3) -> int {
+    return prefetch == 1 ? go(k1) : prefetch == 2 ? go(k2) : go(k3);
+  };
+#define ESC_PROBE(NT) \
+  by_pf(esc::k_decode_probe<NT, 1>, esc::k_decode_probe<NT, 2>, esc::k_decode_probe<NT, 3>)
+  switch (nt) {
+    case 0: return ESC_PROBE(0);
+    case 2: return ESC_PROBE(2);
+    case 3: return ESC_PROBE(3);
+    case 4: return ESC_PROBE(4);
+    case 5: return ESC_PROBE(5);
+    case 6: return ESC_PROBE(6);
+    case 8: return ESC_PROBE(8);
+  }
+#undef ESC_PROBE
+  return fail(ESC_EINVAL, "table pairs per 8 must be one of 0, 2, 3, 4, 5, 6, 8 (got %d)", nt);
 }
 
 }  // extern "C"

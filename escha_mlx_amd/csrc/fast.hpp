@@ -403,6 +403,80 @@ __device__ __forceinline__ void mma_store(const f32x4_t* acc, int g, float* dst)
   }
 }
 
+// The previous lane's word within each quad of lanes (a tile's 4 lanes).
+__device__ __forceinline__ uint32_t quad_prev_word(uint32_t w) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)w, (int)w, 0x93, 0xF, 0xF, false);  // [3,0,1,2]
+}
+
+// One f16 of the decode table in LDS at byte address addr (zero-extended).
+typedef __attribute__((address_space(3))) const uint16_t lds_u16_t;
+__device__ __forceinline__ uint32_t lds_u16(uint32_t addr) { return *(lds_u16_t*)(size_t)addr; }
+
+// K=2 tile decode with NT of every 8 step pairs from the 65,536-entry table
+// in LDS (at byte address tb) and the rest by hash (as fast_tile_packed).
+// Table pair: the two states' byte addresses come from v_mad_u32_u16 (the
+// state's half selected by op_sel, times 2, plus the table base), two
+// ds_read_u16 fetch the f16 values and one v_lshl_or_b32 packs them: 3 VALU
+// per pair against 8 for the hash, so the LDS pipe takes part of the decode.
+// (A d16 read into each half of one register would save the pack, but with
+// SRAM ECC on -- as on MI355X -- d16 loads zero the other half.)  The table
+// is the hash's image and the pairs are accumulated in step order, as in
+// fast_tile_packed: the result is bit-identical to it for every NT.  The
+// table pairs are the last NT of each 8 and their reads are issued first, so
+// their latency overlaps the group's hash pairs.
+template <int NT>
+__device__ __forceinline__ void fast_tile_mix(const LaneWords<2>& lw, uint32_t wprev,
+                                              const uint32_t* xp, float* acc, uint32_t tb) {
+  const uint32_t clo = kClo, chi = kChi;
+  // pair k (0..31) is step u = 16 (k / 8) + k % 8 with step u + 8; pairs
+  // k % 8 >= 8 - NT come from the table
+  auto step_of = [](int k) { return 16 * (k >> 3) + (k & 7); };
+  uint32_t tlo[32], thi[32];
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    if ((k & 7) < 8 - NT) continue;
+    const uint32_t p = window2(lw, wprev, step_of(k));
+    uint32_t a_lo, a_hi;
+    __asm__("v_mad_u32_u16 %0, %1, 2, %2" : "=v"(a_lo) : "v"(p), "v"(tb));
+    __asm__("v_mad_u32_u16 %0, %1, 2, %2 op_sel:[1,0,0,0]" : "=v"(a_hi) : "v"(p), "v"(tb));
+    tlo[k] = lds_u16(a_lo);  // step u + 8 (low half)
+    thi[k] = lds_u16(a_hi);  // step u (high half)
+  }
+  // every table read issued here, before the hash work: the hash reads its
+  // code words through this barrier (the compiler would otherwise hoist the
+  // hash above the reads, sink each read next to its use and wait on it at
+  // once)
+  LaneWords<2> lh = lw;
+  uint32_t wph = wprev;
+  if constexpr (NT > 0)
+    __asm__ volatile("" : "+v"(lh.w[0]), "+v"(lh.w[1]), "+v"(lh.w[2]), "+v"(lh.w[3]), "+v"(wph)
+                     :
+                     : "memory");
+  // every hash pair first (into registers), then the table values: their
+  // wait lands after all the hash work; the products are then accumulated
+  // in step order, as in fast_tile_packed
+  uint32_t hw[32];
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    if ((k & 7) >= 8 - NT) continue;
+    const uint32_t p = window2(lh, wph, step_of(k));
+    hw[k] = halves_sum2(mask_xor(hash_x<false>(p, clo, chi)), mask_xor(hash_x<true>(p, clo, chi)));
+    if constexpr (NT > 0) __asm__ volatile("" : "+v"(hw[k]));
+  }
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    const int u = step_of(k);
+    uint32_t w2;
+    if ((k & 7) < 8 - NT) {
+      w2 = hw[k];
+    } else {
+      __asm__ volatile("" : "+v"(tlo[k]), "+v"(thi[k]));
+      w2 = (thi[k] << 16) | tlo[k];
+    }
+    acc[Geo<2>::col_slot(u)] = dot2(xp[xpair_index(fast_row(u))], w2, acc[Geo<2>::col_slot(u)]);
+  }
+}
+
 // One wave's share of the split-K row-group GEMM on the matrix core: tiles
 // [tile0, tile0 + 16/LPT) of the stream at code_e over kt [z*KS, (z+1)*KS),
 // B column c = input row xr_c (the lane's row, xr), accumulated into acc.

@@ -363,6 +363,25 @@ def moe_expert_path_static(x, ids, scores, gu_code, gu_rin, gu_rout, K_gu, dn_co
     return out
 
 
+def decode_probe_words(steps: int, waves_per_cu: int) -> int:
+    """Code words esc_decode_probe streams for `steps` wave-steps per wave."""
+    return int(_lib.load().esc_decode_probe_words(steps, waves_per_cu))
+
+
+def decode_probe(code_u32: torch.Tensor, steps: int, nt: int, waves_per_cu: int,
+                 out: torch.Tensor, prefetch: int = 1) -> None:
+    """Measurement only: the K=2 decode + dot2 loop streamed over `code_u32`
+    with nt of every 8 step pairs from the table, `prefetch` wave-steps ahead
+    (esc_decode_probe)."""
+    _dev(code_u32, out)
+    need = decode_probe_words(steps, waves_per_cu)
+    lanes = need // (4 * steps) if need else 0  # one output per lane
+    if need == 0 or code_u32.numel() < need or out.numel() < lanes:
+        raise ValueError(f"probe needs {need} code words and {lanes} outputs")
+    _lib.call("esc_decode_probe", _ptr(code_u32), steps, nt, waves_per_cu, prefetch, _ptr(out),
+              _stream())
+
+
 def swiglu(gu16: torch.Tensor) -> torch.Tensor:
     """f16 [m, 2I] -> f16 [m, I]: f16(f16(silu(g)) * u), gate = first half (ref.py:296-301)."""
     _dev(gu16)

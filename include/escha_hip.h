@@ -291,6 +291,19 @@ int esc_moe_expert_path_layers(const esc_moe_layer* layers, int L, int T, int to
 int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int I,
                    int32_t* host_flag, void* stream);
 
+/* Decode-rate probe (measurement only; no counterpart in the reference): the
+ * K=2 decode + dot2 loop of the expert GEMVs streamed by persistent
+ * workgroups (waves_per_cu 16 or 32) over `code` (esc_decode_probe_words
+ * words: every wave reads `steps` wave-steps of 1 KiB, steps a multiple of
+ * 4, `prefetch` (1-3) steps ahead), with nt of every 8 step pairs decoded
+ * from the table in LDS (nt in 0, 2, 3, 4, 5, 6, 8; nt > 0 needs 16 waves
+ * per CU) and the rest by hash.  out: one float per lane (steps * 256 code
+ * words per 64 outputs), each lane's sum of x * w over its weights with
+ * fixed inputs x.  Bounds the rate of any kernel built on this decode. */
+size_t esc_decode_probe_words(int steps, int waves_per_cu);
+int esc_decode_probe(const uint32_t* code, int steps, int nt, int waves_per_cu, int prefetch,
+                     float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -499,6 +499,116 @@ def test_moe_layers_one_launch_vs_oracle(K_gu, K_dn, I):
             assert np.array_equal(bits16(lay["y"]), f)
 
 
+def test_decode_probe_vs_oracle_and_table_mix_bit_identical():
+    """esc_decode_probe (4 wave-steps per wave): every lane's sum of x * w
+    over its 256 decoded weights against the oracle's reconstruct of the same
+    tiles (float32 tolerance), and every table/hash mix (nt of 8 pairs from
+    the LDS table) and prefetch depth bit-identical to the hash-only decode."""
+    o = ops()
+    o.init()
+    steps = 4
+    words = o.decode_probe_words(steps, 16)
+    rng = np.random.default_rng(21)
+    u32 = rng.integers(0, 2**32, size=words, dtype=np.uint64).astype(np.uint32)
+    code = torch.from_numpy(u32.view(np.int32)).to(DEV)
+    outs = {}
+    for nt, pf in [(0, 1), (0, 3)] + [(nt, 2) for nt in (2, 3, 4, 5, 6, 8)]:
+        out = torch.full((words // (4 * steps),), float("nan"), dtype=torch.float32, device=DEV)
+        o.decode_probe(code, steps, nt, 16, out, pf)
+        outs[(nt, pf)] = out.cpu().numpy()
+    ref = outs[(0, 1)]
+    for key, v in outs.items():
+        assert np.array_equal(v.view(np.uint32), ref.view(np.uint32)), key
+    # the probe's fixed inputs: word j = f16 pair 0x3C00 ^ 0x10 j in both halves;
+    # word xpair_index(r) = 2 (r >> 2) | (r & 1) holds row r (low) and r + 2 (high)
+    xw = [(0x3C003C00 ^ (j * 0x00100010)) & 0xFFFFFFFF for j in range(8)]
+    x = np.zeros(16)
+    for r in (0, 1, 4, 5, 8, 9, 12, 13):
+        j = 2 * (r >> 2) | (r & 1)
+        x[r] = np.array([xw[j] & 0xFFFF], np.uint16).view(np.float16)[0]
+        x[r + 2] = np.array([xw[j] >> 16], np.uint16).view(np.float16)[0]
+    # wave g, step k, lane l: tile 16 (steps g + k) + l // 4, quarter l % 4
+    n_waves = 16
+    n_tiles = n_waves * steps * 16
+    w = R.reconstruct(u32[:n_tiles * 16].reshape(1, n_tiles, 16), 16, 16 * n_tiles,
+                      2).astype(np.float64)
+    got = ref[:n_waves * 64].astype(np.float64)
+    for g in range(n_waves):
+        for lane in range(64):
+            q = lane % 4
+            cols = [16 * (16 * (steps * g + k) + lane // 4) + 2 * q + (c & 1) + 8 * (c >> 1)
+                    for k in range(steps) for c in range(4)]
+            terms = x[:, None] * w[:, cols]
+            want = terms.sum()
+            assert abs(got[64 * g + lane] - want) <= 2e-5 * np.abs(terms).sum() + 1e-30, (g, lane)
+
+
+def _layers(o, cases, T, H):
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    lays = []
+    for c in cases:
+        ids, sc = o.route_topk(dv(c["logits"]), c["ids_k"])
+        lays.append({"x": dv(c["x"]), "ids": ids, "scores": sc, "gu_code": dcode(c["gu_code"]),
+                     "gu_rin": dv(c["gu_rin"]), "gu_rout": dv(c["gu_rout"]),
+                     "dn_code": dcode(c["dn_code"]), "dn_rin": dv(c["dn_rin"]),
+                     "dn_rout": dv(c["dn_rout"]),
+                     "y": torch.empty((T, H), dtype=torch.float16, device=DEV)})
+    return lays
+
+
+@pytest.mark.parametrize("E,H,I,T,k", [(32, 1024, 1024, 1, 8), (16, 1536, 512, 3, 6),
+                                       (24, 512, 2048, 2, 4), (48, 1024, 512, 4, 8)])
+def test_moe_layers_table_kernels_shapes(E, H, I, T, k):
+    """The table-assisted many-layer kernels (K=2 gate_up and down) away from
+    config 3's shape: several tokens per layer (the slot combine over top_k
+    rows, top_k not a multiple of 8), H = 1536 (12 gate_up items per (row,
+    h-block), so a group straddles two workgroups and its hand-off crosses
+    XCDs), I = 1024 and 2048 (2 and 4 down input words per lane).  Every
+    layer's output against the oracle, bit-identical on repeat calls."""
+    L = 3
+    o = ops()
+    cases = [dict(_moe_case(E, H, I, 2, 2, T, k, 60 + l), ids_k=k) for l in range(L)]
+    lays = _layers(o, cases, T, H)
+    table = o.moe_layers_table(lays, DEV)
+    ws = torch.zeros(o.moe_layers_workspace(L, T, k, H, I), dtype=torch.uint8, device=DEV)
+    o.moe_expert_path_layers(table, T, k, E, H, I, 2, 2, ws=ws)
+    first = [bits16(l["y"]).copy() for l in lays]
+    for c, lay in zip(cases, lays):
+        ids_np, sc_np = lay["ids"].cpu().numpy(), lay["scores"].cpu().numpy()
+        want = _oracle_moe(c, ids_np, sc_np, E, H, I, 2, 2, np.unique(ids_np)).astype(np.float32)
+        got = lay["y"].cpu().numpy().astype(np.float32)
+        assert np.abs(got - want).max() / np.abs(want).max() < 5e-3
+    for _ in range(2):
+        o.moe_expert_path_layers(table, T, k, E, H, I, 2, 2, ws=ws)
+        for f, lay in zip(first, lays):
+            assert np.array_equal(bits16(lay["y"]), f)
+
+
+def test_moe_layers_workspace_shared_by_both_kernel_families():
+    """K=2/2 calls run the table-assisted kernels, other K the item kernels;
+    alternating them on one workspace stays bit-identical to each on a fresh
+    workspace (each family's counters sit where the other writes no floats)."""
+    E, H, I, k, T, L = 32, 1024, 512, 8, 1, 2
+    o = ops()
+    runs = {}
+    for kk in ((2, 2), (3, 3)):
+        cases = [dict(_moe_case(E, H, I, kk[0], kk[1], T, k, 90 + l), ids_k=k) for l in range(L)]
+        lays = _layers(o, cases, T, H)
+        runs[kk] = (o.moe_layers_table(lays, DEV), lays)
+    nbytes = o.moe_layers_workspace(L, T, k, H, I)
+    fresh = {}
+    for kk, (table, lays) in runs.items():
+        o.moe_expert_path_layers(table, T, k, E, H, I, *kk, ws=torch.zeros(nbytes, dtype=torch.uint8,
+                                                                           device=DEV))
+        fresh[kk] = [bits16(l["y"]).copy() for l in lays]
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+    for kk in ((2, 2), (3, 3), (2, 2), (3, 3), (2, 2)):
+        table, lays = runs[kk]
+        o.moe_expert_path_layers(table, T, k, E, H, I, *kk, ws=ws)
+        for f, lay in zip(fresh[kk], lays):
+            assert np.array_equal(bits16(lay["y"]), f), kk
+
+
 def test_moe_fused_is_deterministic(monkeypatch):
     c = _moe_case(64, 512, 256, 2, 2, 2, 8, 77)
     blk = _block(c, 64, 8, 2, 2, monkeypatch, exact=False)
