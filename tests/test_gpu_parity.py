@@ -584,6 +584,42 @@ def test_moe_layers_table_kernels_shapes(E, H, I, T, k):
             assert np.array_equal(bits16(lay["y"]), f)
 
 
+def test_moe_layers_many_layers_grid_beyond_one_workgroup_per_cu():
+    """Beyond 8 items per wave on one workgroup per CU the item kernels run
+    more workgroups than CUs (each wave's item pointers are staged in LDS):
+    132 token-layers cycling 4 routed cases, every layer against its case's
+    oracle, then a 4-layer call (one item per wave) on the same workspace,
+    then the many-layer call again -- all within tolerance of the oracle, the
+    many-layer call repeatable bit-for-bit."""
+    E, H, I, k, T, Lc, L = 32, 1024, 512, 8, 1, 4, 132
+    o = ops()
+    cases = [dict(_moe_case(E, H, I, 2, 2, T, k, 120 + c), ids_k=k) for c in range(Lc)]
+    base = _layers(o, cases, T, H)
+    want = []
+    for c, lay in zip(cases, base):
+        ids_np, sc_np = lay["ids"].cpu().numpy(), lay["scores"].cpu().numpy()
+        want.append(_oracle_moe(c, ids_np, sc_np, E, H, I, 2, 2, np.unique(ids_np)).astype(np.float32))
+    lays = [dict(base[j % Lc], y=torch.empty((T, H), dtype=torch.float16, device=DEV))
+            for j in range(L)]
+    ws = torch.zeros(o.moe_layers_workspace(L, T, k, H, I), dtype=torch.uint8, device=DEV)
+    big, small = o.moe_layers_table(lays, DEV), o.moe_layers_table(base, DEV)
+
+    def check(ls, n):
+        for j, lay in enumerate(ls[:n]):
+            got = lay["y"].cpu().numpy().astype(np.float32)
+            w = want[j % Lc]
+            assert np.abs(got - w).max() / np.abs(w).max() < 5e-3, j
+
+    o.moe_expert_path_layers(big, T, k, E, H, I, 2, 2, ws=ws)
+    check(lays, L)
+    first = [bits16(l["y"]).copy() for l in lays]
+    o.moe_expert_path_layers(small, T, k, E, H, I, 2, 2, ws=ws)
+    check(base, Lc)
+    o.moe_expert_path_layers(big, T, k, E, H, I, 2, 2, ws=ws)
+    for f, lay in zip(first, lays):
+        assert np.array_equal(bits16(lay["y"]), f)
+
+
 def test_moe_layers_workspace_shared_by_both_kernel_families():
     """K=2/2 calls run the table-assisted kernels, other K the item kernels;
     alternating them on one workspace stays bit-identical to each on a fresh
