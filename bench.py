@@ -112,6 +112,16 @@ def route_sets(torch, layers):
     return routes
 
 
+def host_cpus():
+    """This box's host CPU facts beside every CPU baseline: its logical CPUs and
+    the BLAS library's default thread count (the baselines limit BLAS to one
+    thread)."""
+    from threadpoolctl import threadpool_info
+    blas = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
+    return {"cpu_count": os.cpu_count(), "blas_threads": 1,
+            "blas_threads_default": max(blas) if blas else None}
+
+
 def cpu_baseline(sample):
     """The NumPy oracle (decode + transforms + f32 matmul, no weight cache), one
     BLAS thread.  Returns the baseline record and the oracle's outputs, which
@@ -132,7 +142,7 @@ def cpu_baseline(sample):
             t_total += time.perf_counter() - t0
     per = t_total / len(sample)
     return {"value": round(BYTES_TOKEN_LAYER / per / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": "port",
+            **host_cpus(), "kind": "port",
             "sample": f"{len(sample)} token-layers of config 3 (distinct layer x routing pairs) "
                       f"through oracle/ref_np.py: vectorised decode of 8 experts x 2 legs, no "
                       f"cache, f32 matmul, 1 BLAS thread; {per * 1e3:.1f} ms per token-layer, "
@@ -246,10 +256,12 @@ def _counter_rows(path: Path):
     return per
 
 
-def measure_traffic(probe_args: list, kernels=KERNELS):
-    """HBM bytes per call of `kernels` (summed), from FETCH_SIZE and WRITE_SIZE
-    passes of rocprofv3 over `bench.py --probe <probe_args>`, each calibrated by
-    the 1 GiB copy the probe runs first.  Runs before this process touches the GPU."""
+def measure_traffic(probe_args: list, kernels=KERNELS, units: int = 2):
+    """HBM bytes per unit (one call / layer / step) of `kernels` (every dispatch
+    of those kernels summed, divided by the probe's `units`), from FETCH_SIZE
+    and WRITE_SIZE passes of rocprofv3 over `bench.py --probe <probe_args>`,
+    each calibrated by the 1 GiB copy the probe runs first.  Runs before this
+    process touches the GPU."""
     exe = shutil.which("rocprofv3")
     if exe is None:
         return None, "rocprofv3 not found"
@@ -271,7 +283,7 @@ def measure_traffic(probe_args: list, kernels=KERNELS):
                 vals = [v for k, vv in per.items() if kname in k for v in vv]
                 if not vals:
                     return None, f"no {kname} dispatch in the {ctr} pass"
-                res[(ctr, kname)] = (sum(vals) / len(vals)) * 1024.0 * factor
+                res[(ctr, kname)] = (sum(vals) / units) * 1024.0 * factor
             res[(ctr, "factor")] = factor
     total = sum(v for (c, k), v in res.items() if k != "factor")
     detail = {f"{c.split('_')[0].lower()}_{k}": (round(v, 4) if k == "factor" else int(v))
@@ -289,11 +301,20 @@ def calibration_copy(torch, dev):
 
 
 def probe(torch, args):
-    """Calibration copy, then two sustained calls (PMC target)."""
+    """Calibration copy, then two units of the config's workload, untimed (the
+    PMC target): config 3 two sustained calls, 1 two projection calls, 2 two
+    decoder layers at batch 1, 4 two layer-steps, 5 two module passes."""
     from escha_mlx_amd import ops
     dev = "cuda:0"
     ops.init()
     calibration_copy(torch, dev)
+    if args.config != 3:
+        units = {1: c1_unit, 2: c2_unit, 4: c4_unit, 5: c5_unit}[args.config](torch, ops)
+        for i in range(2):
+            units(i)
+        torch.cuda.synchronize()
+        print(f"probe: copy {COPY_BYTES} B, 2 units of config {args.config}", flush=True)
+        return
     layers = make_layers(torch, args.layers, dev)
     routes = route_sets(torch, layers)
     ws = torch.zeros(ops.moe_layers_workspace(args.layers, 1, TOP_K, H, I), dtype=torch.uint8,
@@ -401,41 +422,289 @@ def graph_time(torch, fns, steps: int, warmup: int, stream, name: str = ""):
     return timed(torch, lambda i: graphs[i % len(graphs)].replay(), steps, warmup, stream)
 
 
-def bench_dense(args, torch, ops, cfg):
+# ------------------------------------------------------- workload units
+# (one call / layer / step of each secondary config, shared by its timed
+# line and its PMC probe)
+
+C2_PROJS = [("q", 5120, 5120, 2, True), ("k", 5120, 5120, 2, True), ("v", 5120, 5120, 2, True),
+            ("o", 5120, 5120, 2, True), ("up", 5120, 17408, 3, False),
+            ("down", 17408, 5120, 3, False)]
+C2_BYTES = sum(ic * oc * K_ // 8 for _, ic, oc, K_, _ in C2_PROJS)
+TRAFFIC_KERNELS = {1: ("k_linear_small",), 2: ("k_linear_small", "k_linear_pair"),
+                   4: ("k_gemv_fast_rows", "k_moe_prep", "k_moe_mid", "k_moe_combine"),
+                   5: ("k_gemm_mma2", "k_input_transform")}
+
+
+def c1_setup(torch, copies):
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0)
+    P = _dense_proj(torch, 2048, 2048, 2, copies, g, "cuda:0")
+    x = torch.randn(1, 2048, generator=g, device="cuda:0").half()
+    return P, x
+
+
+def c1_unit(torch, ops):
+    P, x = c1_setup(torch, 2)
+    return lambda i: _linear(ops, P, x, i, False)
+
+
+def c2_setup(torch, copies):
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(1)
+    return {n: (_dense_proj(torch, ic, oc, K_, copies, g, "cuda:0"), lut)
+            for n, ic, oc, K_, lut in C2_PROJS}, g
+
+
+def c2_layer(ops, P, xs, i):
+    """One decoder layer's projections, k and v as one pair launch."""
+    pk, pv = P["k"][0], P["v"][0]
+    return (*_linear_pair(ops, pk, pv, xs["k"], i, True),
+            *(_linear(ops, P[n][0], xs[n], i, P[n][1]) for n in P if n not in ("k", "v")))
+
+
+def c2_unit(torch, ops):
+    P, g = c2_setup(torch, 2)
+    xs = {n: torch.randn(1, P[n][0]["ic"], generator=g, device="cuda:0").half() for n in P}
+    return lambda i: c2_layer(ops, P, xs, i)
+
+
+C4_T, C4_L = 32, 8
+
+
+def c4_setup(torch, ops, n_layers):
+    from escha_mlx_amd import moe
     dev = "cuda:0"
+    layers = make_layers(torch, n_layers, dev, seed=3)
     g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    recs = []
+    for Ld in layers:
+        logits = torch.randn(C4_T, E, generator=g, device=dev)
+        ids, scores = moe.route(logits, TOP_K)
+        x = torch.randn(C4_T, H, generator=g, device=dev).half()
+        recs.append(dict(Ld, ids=ids, scores=scores, x=x,
+                         y=torch.empty(C4_T, H, dtype=torch.float16, device=dev),
+                         distinct=int(torch.unique(ids).numel())))
+    ws = torch.zeros(ops.moe_expert_path_workspace(C4_T, TOP_K, E, H, I), dtype=torch.uint8,
+                     device=dev)
+
+    def step(i):
+        R_ = recs[i % len(recs)]
+        ops.moe_expert_path(R_["x"], R_["ids"], R_["scores"], R_["gu_code"], R_["gu_rin"],
+                            R_["gu_rout"], K, R_["dn_code"], R_["dn_rin"], R_["dn_rout"], K,
+                            ws=ws, out=R_["y"])
+    return recs, step
+
+
+def c4_unit(torch, ops):
+    return c4_setup(torch, ops, 2)[1]
+
+
+C5_M = 2048
+
+
+def c5_setup(torch):
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(4)
+    up = _dense_proj(torch, 5120, 17408, 3, 1, g, "cuda:0")
+    o = _dense_proj(torch, 5120, 5120, 2, 1, g, "cuda:0")
+    x = torch.randn(C5_M, 5120, generator=g, device="cuda:0").half()
+    return up, o, x
+
+
+def c5_unit(torch, ops):
+    up, o, x = c5_setup(torch)
+    return lambda i: (_linear(ops, up, x, i, False), _linear(ops, o, x, i, False))
+
+
+def roofline_block(bound, achieved, peak, unit, traffic, detail, kernel, **extra):
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic, "traffic_detail": detail,
+            "kernel": kernel, **extra}
+
+
+# ------------------------------------------------------- CPU baselines (oracle)
+
+def _np_proj(rng, ic, oc, K_):
+    """Uniform-random code words, +-1 signs (rin), +-U[0.5,1.5]e-2 per-row
+    scales (rout), both f16-valued."""
+    u32 = rng.integers(0, 2**32, size=(ic // 16, oc // 16, 8 * K_), dtype=np.uint64).astype(np.uint32)
+    rin = rng.choice([-1.0, 1.0], ic).astype(np.float16).astype(np.float32)
+    rout = (rng.choice([-1.0, 1.0], oc) * rng.uniform(0.5, 1.5, oc) * 1e-2).astype(
+        np.float16).astype(np.float32)
+    return u32, rin, rout
+
+
+def _timed_cpu(fn, seconds: float, min_reps: int = 1):
+    t, n, out = 0.0, 0, None
+    while n < min_reps or t < seconds:
+        t0 = time.perf_counter()
+        out = fn()
+        t += time.perf_counter() - t0
+        n += 1
+    return t / n, n, out
+
+
+def c1_cpu_and_parity(torch, ops, seconds: float = 8.0):
+    """Config 1 through the oracle on default_rng(0) inputs (decode + input
+    transform + f32 GEMV + output transform, one BLAS thread), repeated for
+    about `seconds`; the reference's literal per-tile reconstruct loop timed
+    once; and the GPU's esc_linear on the same inputs against the oracle."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import ref_np
+    ic = oc = 2048
+    rng = np.random.default_rng(0)
+    u32, rin, rout = _np_proj(rng, ic, oc, 2)
+    x = rng.standard_normal((1, ic)).astype(np.float16)
+    with threadpool_limits(limits=1):
+        per, n, y = _timed_cpu(lambda: ref_np.expert_linear(x, u32, rin, rout, 2), seconds, 3)
+        t0 = time.perf_counter()
+        w = ref_np.reconstruct_tiles(u32, ic, oc, 2)
+        y_loop = ref_np.expert_linear(x, u32, rin, rout, 2, w_bare=w)
+        t_loop = time.perf_counter() - t0
+    b = ic * oc * 2 // 8
+    dev = "cuda:0"
+    y_gpu = ops.linear(torch.from_numpy(x).to(dev), torch.from_numpy(u32.view(np.int32)).to(dev),
+                       torch.from_numpy(rin).to(dev), torch.from_numpy(rout).to(dev), 2, ic, oc,
+                       lut=False).cpu().numpy()
+    d = np.abs(y_gpu.astype(np.float64) - y.astype(np.float64))
+    ref_max = float(np.abs(y.astype(np.float64)).max())
+    cpu = {"value": round(b / per / 1e9, 4), "unit": "GB/s", "cores": 1, **host_cpus(),
+           "kind": "port",
+           "sample": f"the whole config (one 2048x2048 K2 projection, numpy.default_rng(0) "
+                     f"inputs) through oracle/ref_np.py expert_linear, {n} repetitions, "
+                     f"{per * 1e3:.1f} ms each",
+           "literal_reconstruct_loop": {
+               "seconds": round(t_loop, 3),
+               "gbs": round(b / t_loop / 1e9, 5),
+               "what": "oracle/ref_np.py reconstruct_tiles (the Python loop over the 16,384 "
+                       "tiles of escha_mlx/ref.py:126-134) + the same transforms and GEMV, "
+                       "timed once",
+               "same_output": bool(np.array_equal(y_loop.view(np.uint16), y.view(np.uint16)))}}
+    parity = {"max_abs_err": float(d.max()), "max_rel_err": round(float(d.max()) / ref_max, 6),
+              "tolerance": "max |diff| / max |oracle| < 2e-3 (split-K float32 sums)",
+              "checked": "esc_linear (hash decode) on the CPU baseline's inputs"}
+    return cpu, parity
+
+
+def c2_cpu(seconds: float = 0.0):
+    """Config 2's q (K2) and up (K3) projections at batch 1 through the oracle
+    (one BLAS thread), each once; GB/s over their coded bytes."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import ref_np
+    rng = np.random.default_rng(1)
+    total_b, total_t = 0, 0.0
+    with threadpool_limits(limits=1):
+        for ic, oc, K_ in ((5120, 5120, 2), (5120, 17408, 3)):
+            u32, rin, rout = _np_proj(rng, ic, oc, K_)
+            x = rng.standard_normal((1, ic)).astype(np.float16)
+            per, _, _ = _timed_cpu(lambda: ref_np.expert_linear(x, u32, rin, rout, K_), seconds)
+            total_b += ic * oc * K_ // 8
+            total_t += per
+    return {"value": round(total_b / total_t / 1e9, 4), "unit": "GB/s", "cores": 1,
+            **host_cpus(), "kind": "port",
+            "sample": f"q (5120x5120 K2) and up (5120->17408 K3) at batch 1 through "
+                      f"oracle/ref_np.py expert_linear, once each: {total_t:.2f} s for "
+                      f"{total_b} coded bytes"}
+
+
+def c4_cpu(recs, n_tokens: int = 4):
+    """Config 4's first layer-step, its first n_tokens tokens, through the
+    oracle's routed-expert path (decode of every distinct expert, no cache,
+    one BLAS thread); GB/s over those experts' coded bytes."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import ref_np
+    R_ = recs[0]
+    ids = R_["ids"][:n_tokens].cpu().numpy()
+    scores = R_["scores"][:n_tokens].cpu().numpy()
+    x = R_["x"][:n_tokens].cpu().numpy()
+    used = sorted({int(e) for e in ids.reshape(-1)})
+
+    def host(t, e):
+        a = t[e].cpu().numpy()
+        return a.view(np.uint32) if a.dtype == np.int32 else a
+    gu = {e: host(R_["gu_code"], e) for e in used}
+    dn = {e: host(R_["dn_code"], e) for e in used}
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        w_gu = {e: ref_np.reconstruct(gu[e], H, 2 * I, K) for e in used}
+        w_dn = {e: ref_np.reconstruct(dn[e], I, H, K) for e in used}
+        gup = {"w": w_gu, "rin": {e: host(R_["gu_rin"], e) for e in used},
+               "rout": {e: host(R_["gu_rout"], e) for e in used}}
+        dnp = {"w": w_dn, "rin": {e: host(R_["dn_rin"], e) for e in used},
+               "rout": {e: host(R_["dn_rout"], e) for e in used}}
+        ref_np.moe_routed(x, ids, scores, gup, dnp, K, K, ordered=False)
+        t = time.perf_counter() - t0
+    b = len(used) * (BYTES_GU + BYTES_DN)
+    return {"value": round(b / t / 1e9, 4), "unit": "GB/s", "cores": 1, **host_cpus(),
+            "kind": "port",
+            "sample": f"layer-step 0's first {n_tokens} tokens ({len(used)} distinct experts) "
+                      f"through oracle/ref_np.py moe_routed (decode every expert, f32 matmul): "
+                      f"{t:.2f} s"}
+
+
+def c5_cpu(rows: int = 32):
+    """Config 5's up (K3) and o (K2) projections for `rows` of the 2048 tokens
+    through the oracle (decode + transforms + f32 matmul, one BLAS thread)."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import ref_np
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((rows, 5120)).astype(np.float16)
+    t = 0.0
+    with threadpool_limits(limits=1):
+        for ic, oc, K_ in ((5120, 17408, 3), (5120, 5120, 2)):
+            u32, rin, rout = _np_proj(rng, ic, oc, K_)
+            t0 = time.perf_counter()
+            ref_np.expert_linear(x, u32, rin, rout, K_)
+            t += time.perf_counter() - t0
+    flop = 2 * rows * 5120 * (17408 + 5120)
+    return {"value": round(flop / t / 1e12, 6), "unit": "TFLOP/s", "cores": 1, **host_cpus(),
+            "kind": "port",
+            "sample": f"{rows} of the 2048 rows through up and o with oracle/ref_np.py "
+                      f"expert_linear (the decode is paid once per projection, as the GPU "
+                      f"pays it once per 128 rows): {t:.2f} s"}
+
+
+def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffic)")):
+    dev = "cuda:0"
     stream = torch.cuda.current_stream()
+    tr, tr_detail = traffic
     res = {"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "data": "synthetic: uniform-random code "
            "streams, +-1 rin, +-U[0.5,1.5]e-2 rout, x ~ N(0,1) f16"}
     if cfg == 1:
-        g.manual_seed(0)
-        P = _dense_proj(torch, 2048, 2048, 2, 1024, g, dev)   # 1 GiB of code, rotated
-        x = torch.randn(1, 2048, generator=g, device=dev).half()
+        P, x = c1_setup(torch, 512)   # 512 MiB of code, rotated
         ms_eager = timed(torch, lambda i: _linear(ops, P, x, i, False), args.steps * 50,
                          args.warmup, stream)
         fns = [lambda i=i: (_linear(ops, P, x, i, False),) for i in range(512)]
         ms_graph = graph_time(torch, fns, args.steps * 50, args.warmup, stream, "c1")
         ms = min(ms_graph, ms_eager)  # one launch per call: the graph adds its own replay cost
         b = 2048 * 2048 * 2 // 8
+        gbs = b / (ms * 1e-3) / 1e9
         res.update(metric="coded-weight GB/s, one 2048x2048 K2 projection at batch 1",
-                   value=round(b / (ms * 1e-3) / 1e9, 2), unit="GB/s", ms_per_step=round(ms, 5),
+                   value=round(gbs, 2), unit="GB/s", ms_per_step=round(ms, 5),
                    dtype="u32 codes -> f16 weights (hash), f32 accumulate",
                    config={"workload": "config 1: EschaLinear 2048x2048 K2 hash, M=1 (one "
                                        "esc_linear launch), 512 code copies rotated (512 MiB, "
                                        "cold); best of eager and HIP-graph replay"},
                    us_per_call=round(ms * 1e3, 3), eager_us_per_call=round(ms_eager * 1e3, 3),
-                   graph_us_per_call=round(ms_graph * 1e3, 3))
+                   graph_us_per_call=round(ms_graph * 1e3, 3),
+                   roofline=roofline_block(
+                       "hbm", gbs, HBM_PEAK_GBS, "GB/s", tr, tr_detail,
+                       "k_linear_small<2,false,1> (one launch per call; achieved over the "
+                       "call's time, launch included)", bytes_per_launch=b,
+                       avg_launch_us=round(ms * 1e3, 3)))
+        if not args.no_cpu:
+            res["cpu_baseline"], res["parity"] = c1_cpu_and_parity(torch, ops)
         return res
     if cfg == 2:
-        g.manual_seed(1)
         L = 8   # 8 layer copies x 93 MB = 745 MB rotated
-        projs = [("q", 5120, 5120, 2, True), ("k", 5120, 5120, 2, True), ("v", 5120, 5120, 2, True),
-                 ("o", 5120, 5120, 2, True), ("up", 5120, 17408, 3, False),
-                 ("down", 17408, 5120, 3, False)]
-        P = {n: (_dense_proj(torch, ic, oc, K, L, g, dev), lut) for n, ic, oc, K, lut in projs}
+        P, g = c2_setup(torch, L)
         per = {}
-        total_b = sum(ic * oc * K // 8 for _, ic, oc, K, _ in projs)
         for M in (1, 4):
             xs = {n: torch.randn(M, P[n][0]["ic"], generator=g, device=dev).half() for n in P}
             t_layer = 0.0
@@ -460,35 +729,36 @@ def bench_dense(args, torch, ops, cfg):
             fkv = [lambda i=i: _linear_pair(ops, pk, pv, xs["k"], i, True) for i in range(L)]
             per[f"M{M}_kv_pair_us"] = round(graph_time(torch, fkv, args.steps * 5, args.warmup,
                                                        stream, f"M{M} kv pair") * 1e3, 2)
-            rest = [n for n in P if n not in ("k", "v")]
-            flp = [lambda i=i: (*_linear_pair(ops, pk, pv, xs["k"], i, True),
-                                *(_linear(ops, P[n][0], xs[n], i, P[n][1]) for n in rest))
-                   for i in range(L)]
+            flp = [lambda i=i: c2_layer(ops, P, xs, i) for i in range(L)]
             per[f"M{M}_layer_graph_kv_pair_us"] = round(
                 graph_time(torch, flp, args.steps, args.warmup, stream, f"M{M} layer kv pair") * 1e3, 2)
             per[f"M{M}_layer_us"] = round(t_layer * 1e3, 2)
-            per[f"M{M}_layer_gbs"] = round(total_b / (t_layer * 1e-3) / 1e9, 1)
+            per[f"M{M}_layer_gbs"] = round(C2_BYTES / (t_layer * 1e-3) / 1e9, 1)
             per[f"M{M}_tok_s_per_layer"] = round(M / (t_layer * 1e-3), 1)
         # this line's value: the whole layer replayed as one HIP graph, k and v as
         # one pair launch (the per-projection graphs' sum is M1_layer_gbs)
         us_layer = per["M1_layer_graph_kv_pair_us"]
+        gbs = C2_BYTES / (us_layer * 1e-6) / 1e9
         res.update(metric="coded-weight GB/s of one dense decoder layer (q,k,v,o K2 LUT, up/down "
                           "K3) at batch 1",
-                   value=round(total_b / (us_layer * 1e-6) / 1e9, 1), unit="GB/s",
-                   ms_per_step=round(us_layer / 1e3, 5),
+                   value=round(gbs, 1), unit="GB/s", ms_per_step=round(us_layer / 1e3, 5),
                    dtype="u32 codes -> f16 weights (LUT q/k/v/o, hash up/down), f32 accumulate",
                    config={"workload": "config 2: 27B-class dense layer, 5120 hidden, M=1 and "
                                        "M=4, the layer's projections replayed as one HIP graph "
                                        "(k and v as one pair launch), 8 layer copies rotated "
                                        "(745 MB, cold)"},
-                   bytes_per_layer=total_b, **per)
+                   bytes_per_layer=C2_BYTES, **per,
+                   roofline=roofline_block(
+                       "hbm", gbs, HBM_PEAK_GBS, "GB/s", tr, tr_detail,
+                       "the layer's k_linear_small (q, o LUT; up, down hash) + k_linear_pair "
+                       "(k, v) launches at batch 1, one HIP graph", bytes_per_layer=C2_BYTES,
+                       avg_layer_us=us_layer))
+        if not args.no_cpu:
+            res["cpu_baseline"] = c2_cpu()
         return res
     if cfg == 5:
-        g.manual_seed(4)
-        M = 2048
-        up = _dense_proj(torch, 5120, 17408, 3, 1, g, dev)
-        o = _dense_proj(torch, 5120, 5120, 2, 1, g, dev)
-        x = torch.randn(M, 5120, generator=g, device=dev).half()
+        up, o, x = c5_setup(torch)
+        M = C5_M
         flop = 2 * M * 5120 * (17408 + 5120)
         xh_up = ops.scaled_had(x, up["rin"], None)
         xh_o = ops.scaled_had(x, o["rin"], None)
@@ -507,50 +777,42 @@ def bench_dense(args, torch, ops, cfg):
                                        "transform)"},
                    tok_s=round(M / (ms_mod * 1e-3), 1),
                    gemm_up_us=round(ms_gu * 1e3, 1), gemm_o_us=round(ms_go * 1e3, 1),
-                   roofline={"bound": "mfma", "achieved": round(tf_k, 1), "peak": 2500.0,
-                             "unit": "TFLOP/s", "frac": round(tf_k / 2500.0, 4), "traffic": None,
-                             "kernel": "k_gemm_mma2<3,8> + k_gemm_mma2<2,6> (row blocks per "
-                                       "workgroup chosen by the host for this shape)",
-                             "flop_per_launch_pair": flop})
+                   roofline=roofline_block(
+                       "mfma", tf_k, 2500.0, "TFLOP/s", tr, tr_detail,
+                       "k_gemm_mma2<3,8> + k_gemm_mma2<2,6> (row blocks per workgroup chosen "
+                       "by the host for this shape); traffic: HBM bytes per module pass (both "
+                       "projections, input transforms included)",
+                       flop_per_launch_pair=flop))
+        if not args.no_cpu:
+            res["cpu_baseline"] = c5_cpu()
         return res
     raise SystemExit(f"config {cfg}: not measured by this bench")
 
 
-def bench_c4(args, torch, ops):
+def bench_c4(args, torch, ops, traffic=(None, "not measured (--no-traffic)")):
     """Config 4: the MoE layer at 32 tokens (m = 256 routed rows)."""
-    from escha_mlx_amd import moe
-    dev = "cuda:0"
-    T, L = 32, 8
-    layers = make_layers(torch, L, dev, seed=3)
     stream = torch.cuda.current_stream()
-    g = torch.Generator(device=dev)
-    g.manual_seed(3)
-    recs = []
-    for Ld in layers:
-        logits = torch.randn(T, E, generator=g, device=dev)
-        ids, scores = moe.route(logits, TOP_K)
-        x = torch.randn(T, H, generator=g, device=dev).half()
-        recs.append(dict(Ld, ids=ids, scores=scores, x=x,
-                         y=torch.empty(T, H, dtype=torch.float16, device=dev),
-                         distinct=int(torch.unique(ids).numel())))
-    ws = torch.zeros(ops.moe_expert_path_workspace(T, TOP_K, E, H, I), dtype=torch.uint8, device=dev)
-
-    def step(i):
-        R_ = recs[i % L]
-        ops.moe_expert_path(R_["x"], R_["ids"], R_["scores"], R_["gu_code"], R_["gu_rin"],
-                            R_["gu_rout"], K, R_["dn_code"], R_["dn_rin"], R_["dn_rout"], K,
-                            ws=ws, out=R_["y"])
-    ms = timed(torch, step, args.steps * L, args.warmup, stream)
-    distinct = sum(r["distinct"] for r in recs) / L
+    recs, step = c4_setup(torch, ops, C4_L)
+    ms = timed(torch, step, args.steps * C4_L, args.warmup, stream)
+    distinct = sum(r["distinct"] for r in recs) / C4_L
     b = distinct * (BYTES_GU + BYTES_DN)
-    return {"metric": "coded-weight GB/s (distinct experts) + tok/s, MoE layer at batch 32",
-            "value": round(b / (ms * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
-            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "u32 codes -> f16 weights (hash), f32 accumulate",
-            "data": "synthetic, seeded logits [32,256] per layer, 8 layer stacks rotated",
-            "config": {"workload": "config 4: E=256, H=2048, I=512, top-8, T=32 (m=256 rows)"},
-            "distinct_experts_per_layer": distinct, "tok_s_per_layer": round(T / (ms * 1e-3), 1)}
+    gbs = b / (ms * 1e-3) / 1e9
+    res = {"metric": "coded-weight GB/s (distinct experts) + tok/s, MoE layer at batch 32",
+           "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "u32 codes -> f16 weights (hash), f32 accumulate",
+           "data": "synthetic, seeded logits [32,256] per layer, 8 layer stacks rotated",
+           "config": {"workload": "config 4: E=256, H=2048, I=512, top-8, T=32 (m=256 rows)"},
+           "distinct_experts_per_layer": distinct, "tok_s_per_layer": round(C4_T / (ms * 1e-3), 1),
+           "roofline": roofline_block(
+               "hbm", gbs, HBM_PEAK_GBS, "GB/s", traffic[0], traffic[1],
+               "k_moe_prep + k_gemv_fast_rows<2,false,8> (gate_up, down) + k_moe_mid + "
+               "k_moe_combine, one esc_moe_expert_path call per layer-step",
+               bytes_per_step=int(b), avg_step_us=round(ms * 1e3, 2))}
+    if not args.no_cpu:
+        res["cpu_baseline"] = c4_cpu(recs)
+    return res
 
 
 Q8_HEAD_O, Q8_HEAD_K = 248320, 2048
@@ -686,6 +948,14 @@ def main():
             print(json.dumps(res))
         return
     if args.config != 3:
+        traffic = (None, "not measured (--no-traffic)")
+        if args.probe:
+            import torch
+            torch.cuda.set_device(0)
+            probe(torch, args)
+            return
+        if args.config in TRAFFIC_KERNELS and not args.no_traffic:
+            traffic = measure_traffic(["--config", str(args.config)], TRAFFIC_KERNELS[args.config])
         import torch
 
         from escha_mlx_amd import ops
@@ -694,9 +964,9 @@ def main():
         if args.config == "ceiling":
             res = bench_ceiling(args, torch, ops)
         elif args.config == 4:
-            res = bench_c4(args, torch, ops)
+            res = bench_c4(args, torch, ops, traffic)
         else:
-            res = bench_dense(args, torch, ops, args.config)
+            res = bench_dense(args, torch, ops, args.config, traffic)
         print(json.dumps(res))
         return
     traffic, traffic_detail = None, "not measured (--no-traffic)"

@@ -152,6 +152,33 @@ def reconstruct(code: np.ndarray, ic: int, oc: int, K: int, lut: np.ndarray | No
     return out.reshape(tk, tn, 16, 16).transpose(0, 2, 1, 3).reshape(ic, oc)
 
 
+def decode_tile(words: np.ndarray, K: int, lut: np.ndarray | None = None) -> np.ndarray:
+    """One tile's 8K code words -> its 16x16 f16 block (escha_mlx/ref.py:114-123):
+    the tile's 256 trellis states through the value table, placed by the lane
+    map."""
+    lut = LUT if lut is None else lut
+    vals = lut[tile_states(np.asarray(words, dtype=np.uint32).reshape(1, 8 * K), K)[0]]
+    tile = np.zeros((16, 16), dtype=np.float16)
+    tile[_ROW, _COL] = vals
+    return tile
+
+
+def reconstruct_tiles(code: np.ndarray, ic: int, oc: int, K: int) -> np.ndarray:
+    """The reference's literal form of reconstruct: a Python loop over the
+    tiles (kt, nt), one decode_tile each (escha_mlx/ref.py:126-134).  Same
+    weights as reconstruct; kept as the CPU baseline's un-vectorised timing."""
+    tk, tn = ic // 16, oc // 16
+    if code.dtype == np.uint32:
+        words = code.reshape(tk, tn, 8 * K)
+    else:
+        words = code_words(code.reshape(tk * tn, 16 * K)).reshape(tk, tn, 8 * K)
+    out = np.zeros((ic, oc), dtype=np.float16)
+    for kt in range(tk):
+        for nt in range(tn):
+            out[16 * kt:16 * kt + 16, 16 * nt:16 * nt + 16] = decode_tile(words[kt, nt], K)
+    return out
+
+
 # ---------------------------------------------------------------- transforms
 
 def h128(x: np.ndarray) -> np.ndarray:

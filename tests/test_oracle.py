@@ -52,6 +52,18 @@ def test_reconstruct_bit_exact_vs_goldens(which, k2_golden, k3_golden):
     assert n_zero == meta["n_zero"]
 
 
+@pytest.mark.parametrize("K,ic,oc", [(2, 64, 96), (3, 48, 80)])
+def test_reconstruct_tiles_loop_equals_vectorised(K, ic, oc):
+    """The literal per-tile loop (the CPU baseline's form) decodes the same
+    weights as the golden-pinned vectorised reconstruct, int16 and u32 code."""
+    rng = np.random.default_rng(40 + K)
+    code = rng.integers(-32768, 32768, size=(ic // 16, oc // 16, 16 * K), dtype=np.int16)
+    want = R.reconstruct(code, ic, oc, K)
+    assert np.array_equal(R.reconstruct_tiles(code, ic, oc, K).view(np.uint16), want.view(np.uint16))
+    u32 = R.code_words(code.reshape(-1, 16 * K)).reshape(ic // 16, oc // 16, 8 * K)
+    assert np.array_equal(R.reconstruct_tiles(u32, ic, oc, K).view(np.uint16), want.view(np.uint16))
+
+
 def _brute_states(words: np.ndarray, K: int) -> np.ndarray:
     """Trellis states from an explicit MSB-first bit string (circular)."""
     bits = "".join(format(int(w), "032b") for w in words)
