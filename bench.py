@@ -66,8 +66,9 @@ def parse():
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 PMC passes")
     ap.add_argument("--only", choices=["both", "sustained", "chained"], default="both")
     ap.add_argument("--probe", action="store_true",
-                    help="run the calibration copy and two sustained calls (config 6: two head "
-                         "calls), untimed, as the PMC target")
+                    help="run the calibration copy and two units of the config's workload "
+                         "(config 3: two sustained calls; ceiling: one pass per decode "
+                         "variant), untimed, as the PMC target")
     ap.add_argument("--config", choices=["1", "2", "3", "4", "5", "6", "ceiling"], default="3",
                     help="BASELINE config; 3 (the headline metric) by default; 6 is not a "
                          "BASELINE config: the w8a16 vocabulary-head GEMV around the MoE block; "
@@ -308,6 +309,17 @@ def probe(torch, args):
     dev = "cuda:0"
     ops.init()
     calibration_copy(torch, dev)
+    if args.config == "ceiling":
+        # one cold 1 GiB pass per variant: hash only, then 4 of 8 pairs from the table
+        steps = 256
+        words = ops.decode_probe_words(steps, 16)
+        code = torch.randint(-2**31, 2**31 - 1, (words,), device=dev, dtype=torch.int32)
+        out = torch.empty(words // (4 * steps), dtype=torch.float32, device=dev)
+        for nt in (0, 4):
+            ops.decode_probe(code, steps, nt, 16, out, 1)
+            torch.cuda.synchronize()
+        print(f"probe: copy {COPY_BYTES} B, decode probe nt 0 and 4 over {4 * words} B", flush=True)
+        return
     if args.config != 3:
         units = {1: c1_unit, 2: c2_unit, 4: c4_unit, 5: c5_unit}[args.config](torch, ops)
         for i in range(2):
