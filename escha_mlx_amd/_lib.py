@@ -18,7 +18,7 @@ import torch  # noqa: F401  (loads the HIP runtime this library binds to)
 LIB_NAME = "libescha_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ESC_OK, ESC_EINVAL, ESC_EHIP, ESC_ENOSPACE = 0, -1, -2, -3
+ESC_OK, ESC_EINVAL, ESC_EHIP, ESC_ENOSPACE, ESC_ETIMEOUT = 0, -1, -2, -3, -4
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -63,6 +63,7 @@ SIGNATURES = {
     "esc_moe_expert_path_static": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _P,
                                         _P, _I, _I, _P, _P]),
     "esc_moe_status": (_I, [_P, _Z, _I, _I, _I, _I, _P, _P]),
+    "esc_moe_set_spin_limit": (_I, [_I]),
     "esc_moe_layers_workspace": (_Z, [_I, _I, _I, _I, _I]),
     "esc_moe_expert_path_layers": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
     "esc_moe_expert_path": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _P,
@@ -74,6 +75,11 @@ _lib = None
 
 class EschaHipError(RuntimeError):
     """A HIP runtime failure reported by libescha_hip."""
+
+
+class EschaWaitTimeout(EschaHipError):
+    """An earlier one-launch expert-path call on the device gave up a bounded
+    wait between workgroups; its outputs are NaN."""
 
 
 def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
@@ -104,6 +110,8 @@ def check(rc: int, what: str) -> None:
         raise ValueError(f"{what}: {msg}")
     if rc == ESC_ENOSPACE:
         raise ValueError(f"{what}: {msg}")
+    if rc == ESC_ETIMEOUT:
+        raise EschaWaitTimeout(f"{what}: {msg}")
     raise EschaHipError(f"{what}: {msg}")
 
 

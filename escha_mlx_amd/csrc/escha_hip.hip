@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -73,6 +74,58 @@ bool lut_ready() {
 }
 
 int ensure_scratch(void** out);
+// Device-wide bounded-wait flag of the single persistent expert launch
+// (k_moe_fused): one int per device in pinned, coherent host memory, set by a
+// workgroup that gave up a wait and read by the host with no synchronisation,
+// so a later call can report the failure.  Allocated at set-up (esc_init, or
+// the first esc_moe_expert_path call on the device); the allocation-free entry
+// point only uses it once it exists.
+int* g_wait_flag[kMaxDevices];
+int* g_wait_flag_dev[kMaxDevices];
+std::atomic<int> g_spin_limit{esc::kSpinLimit};
+
+int ensure_wait_flag() {
+  int dev = 0;
+  if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return fail(ESC_EINVAL, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  if (g_wait_flag[dev]) return ESC_OK;
+  void* h = nullptr;
+  if (int rc = hip_check(hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent),
+                         "hipHostMalloc"))
+    return rc;
+  void* d = nullptr;
+  if (int rc = hip_check(hipHostGetDevicePointer(&d, h, 0), "hipHostGetDevicePointer")) {
+    (void)hipHostFree(h);
+    return rc;
+  }
+  *static_cast<volatile int*>(h) = 0;
+  g_wait_flag_dev[dev] = static_cast<int*>(d);
+  g_wait_flag[dev] = static_cast<int*>(h);
+  return ESC_OK;
+}
+
+// Takes the device's flag: ESC_ETIMEOUT (flag cleared) if a single persistent
+// launch on this device gave up a wait since the last take; *dev_flag is the
+// flag's device address for the next launch (null before set-up).
+int take_wait_error(int** dev_flag) {
+  *dev_flag = nullptr;
+  int dev = 0;
+  if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return fail(ESC_EINVAL, "device index %d out of range", dev);
+  int* h = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_init_mu);
+    h = g_wait_flag[dev];
+    *dev_flag = g_wait_flag_dev[dev];
+  }
+  if (h && __atomic_exchange_n(h, 0, __ATOMIC_ACQ_REL) != 0)
+    return fail(ESC_ETIMEOUT,
+                "an earlier single-launch expert-path call on device %d gave up a bounded wait: "
+                "its outputs are NaN (this call did not run)",
+                dev);
+  return ESC_OK;
+}
 
 int check_proj(int K, int IC, int OC) {
   ESC_REQUIRE(K == 2 || K == 3, "escha code implies K=%d; this runtime implements K in [2, 3]", K);
@@ -357,6 +410,7 @@ const char* esc_last_error(void) { return g_err.c_str(); }
 
 int esc_init(void) {
   if (int rc = ensure_lut()) return rc;
+  if (int rc = ensure_wait_flag()) return rc;
   void* ptr = nullptr;
   return ensure_scratch(&ptr);
 }
@@ -977,6 +1031,8 @@ esc::FusedMoe fused_args(const FusedPlan& f, void* ws, int T, int top_k, int H, 
   p.done = p.cntB + (size_t)f.L * T * f.NCP;
   p.err = p.done + 1;
   p.status = p.done + 2;
+  p.host_err = nullptr;
+  p.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   p.L = f.L;
   p.T = T;
   p.top_k = top_k;
@@ -1161,7 +1217,17 @@ int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int
                          "hipMemcpyAsync"))
     return rc;
   if (int rc = hip_check(hipMemsetAsync(st, 0, 4, S(stream)), "hipMemsetAsync")) return rc;
-  return hip_check(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
+  if (int rc = hip_check(hipStreamSynchronize(S(stream)), "hipStreamSynchronize")) return rc;
+  // the device-wide flag records the same event: taken here too, so a later
+  // call does not report it again
+  int* unused = nullptr;
+  if (take_wait_error(&unused) == ESC_ETIMEOUT) *host_flag = 1;
+  return ESC_OK;
+}
+
+int esc_moe_set_spin_limit(int polls) {
+  g_spin_limit.store(polls < 0 ? esc::kSpinLimit : polls, std::memory_order_relaxed);
+  return ESC_OK;
 }
 
 }  // extern "C"
@@ -1196,8 +1262,10 @@ int moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, 
     esc::FusedMoe p = fused_args(f, ws, T, top_k, H, I);
     p.l0 = esc::MoeLayer{x, ids, scores, gu_code, gu_rin, gu_rout, dn_code, dn_rin, dn_rout, y};
     p.layers = nullptr;
-    return two ? launch_fused<true>(p, K_gu, K_dn, f.grid, S(stream))
-               : launch_fused<false>(p, K_gu, K_dn, f.grid, S(stream));
+    if (two) return launch_fused<true>(p, K_gu, K_dn, f.grid, S(stream));
+    // only the single persistent launch waits across workgroups
+    if (int rc = take_wait_error(&p.host_err)) return rc;
+    return launch_fused<false>(p, K_gu, K_dn, f.grid, S(stream));
   }
   const MoePlan p = moe_plan(T, top_k, E, H, I, K_gu, K_dn, int_region);
   if (!ws || ws_bytes < p.total)
@@ -1293,6 +1361,7 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
                         const uint32_t* dn_code, const float* dn_rin, const float* dn_rout,
                         int K_dn, int use_lut, uint16_t* y, void* ws, size_t ws_bytes,
                         void* stream) {
+  if (int rc = ensure_wait_flag()) return rc;
   return moe_expert_path(x, ids, scores, T, top_k, E, H, I, gu_code, gu_rin, gu_rout, K_gu,
                          dn_code, dn_rin, dn_rout, K_dn, use_lut, y, ws, ws_bytes, 0, stream);
 }

@@ -42,7 +42,9 @@
 // never wait.  A bounded spin is a last safety net: a down item that gives up
 // computes on NaN inputs (so its outputs are NaN, never stale values), raises
 // the call's err flag (every other waiting block then gives up too) and the
-// status flag that esc_moe_status reports.  The last block to finish resets
+// status flag that esc_moe_status reports, and sets a device-wide flag in
+// pinned host memory that the next expert-path call on the device returns as
+// ESC_ETIMEOUT (without a synchronisation).  The last block to finish resets
 // every counter and the call's err flag, so the integer workspace is zero
 // again for the next call (it must be zero before the first).
 #pragma once
@@ -97,6 +99,9 @@ struct FusedMoe {
   int* done;     // [1]
   int* err;      // [1] a spin bound was hit in this call (reset by the last block)
   int* status;   // [1] a spin bound was hit since the host last read it
+  int* host_err; // device-wide flag in pinned host memory: a spin bound was hit
+                 // (the next expert-path call on the device reports it)
+  int spin_limit;  // polls before a wait gives up (kSpinLimit; the host may lower it)
   int L, T, top_k, H, I;
   int NB;   // I / 128        h-blocks
   int NKC;  // H / (16*KTA)   gate_up items per (row, h-block), <= 62
@@ -411,7 +416,7 @@ __device__ int wait_gate_up(const FusedMoe& p, int l, int r, int kb, int* s_flag
     const int* cnt = &p.cntA[(size_t)l * p.T * p.top_k * p.NB + r * p.NB + kb];
     int* claims = p.claimA + (size_t)l * p.nA + abase;
     int st = kTimeout;
-    for (int spin = 0; spin < kSpinLimit; ++spin) {
+    for (int spin = 0; spin < p.spin_limit; ++spin) {
       // the counter every poll; the claim flags and the error flag only on
       // every 32nd (they change rarely, and each is a device-coherent load)
       const bool full = (spin & 31) == 0;
@@ -759,6 +764,7 @@ __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_fused(FusedMoe p) {
       if (tid == 0) {
         atomicOr(p.err, 1);
         atomicOr(p.status, 1);
+        if (p.host_err) __hip_atomic_store(p.host_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       }
     } else if ((tid >> 6) < kHB) {
       down_inputs(p, l, r, hb0 + (tid >> 6), s_x + 64 * (tid >> 6));

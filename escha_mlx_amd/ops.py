@@ -472,11 +472,18 @@ def q8_embed(ids: torch.Tensor, w8: torch.Tensor, scale: torch.Tensor) -> torch.
 
 
 def moe_status(ws: torch.Tensor, T: int, top_k: int, H: int, I: int) -> int:
-    """1 if a one-launch expert path using ``ws`` hit its bounded wait since the
-    previous call (reading clears the flag; synchronises)."""
+    """1 if a one-launch expert path using ``ws``, or any on this device, hit
+    its bounded wait since the flags were last read (reading clears them;
+    synchronises)."""
     flag = ctypes.c_int32(0)
     _lib.call("esc_moe_status", _ptr(ws), ws.numel(), T, top_k, H, I, ctypes.byref(flag), _stream())
     return int(flag.value)
+
+
+def set_moe_spin_limit(polls: int) -> None:
+    """Test hook: polls before a wait of the one-launch expert path gives up
+    (negative restores the default; 0 gives up at once)."""
+    _lib.call("esc_moe_set_spin_limit", int(polls))
 
 
 # one esc_moe_layer record: x, ids, scores, gu_code, gu_rin, gu_rout,

@@ -28,6 +28,8 @@ extern "C" {
 #define ESC_EINVAL (-1)   /* shape / K / pointer precondition violated */
 #define ESC_EHIP (-2)     /* the HIP runtime reported an error           */
 #define ESC_ENOSPACE (-3) /* workspace smaller than the *_workspace size */
+#define ESC_ETIMEOUT (-4) /* an earlier single-launch expert-path call on the
+                             device gave up a bounded wait (NaN outputs)    */
 
 /* ABI version (major*100 + minor). */
 int esc_version(void);
@@ -223,7 +225,12 @@ int esc_q8_embed(const int32_t* ids, int T, const int8_t* w8, const float* scale
  * Tolerance contract (reassociated GEMV sums; decode bit-exact).  ws:
  * esc_moe_expert_path_workspace bytes, zero-filled before its first use (the
  * counters it holds are left zero by every call); calls sharing one ws must
- * not overlap.
+ * not overlap.  Shapes that run as one persistent launch (H or I not a
+ * multiple of 512) hand work between workgroups with bounded waits: a
+ * workgroup that gives up writes NaN outputs and raises a device-wide flag,
+ * and the next call on the device that would take that launch returns
+ * ESC_ETIMEOUT without running (the flag is read without a synchronisation;
+ * esc_moe_status reads it at once).
  * Replaces EschaSparseMoeBlock._expert_path (escha_mlx/models/qwen3_5_moe.py:207-253). */
 size_t esc_moe_expert_path_workspace(int T, int top_k, int E, int H, int I);
 int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, int T,
@@ -283,13 +290,22 @@ int esc_moe_expert_path_layers(const esc_moe_layer* layers, int L, int T, int to
                                void* stream);
 
 /* Diagnostic: *host_flag = 1 if a one-launch expert path run with this
- * workspace hit its bounded wait since the previous esc_moe_status call on it
- * (never expected: the kernel's work claiming guarantees progress; the
- * outputs of an item that gave up are NaN, never stale values).  Reading
- * clears the flag.  Synchronises the stream.  No counterpart in the reference
- * (its expert path has no cross-workgroup hand-off). */
+ * workspace, or any such run on the current device, hit its bounded wait
+ * since the flags were last read (never expected: the kernel's work claiming
+ * guarantees progress; the outputs of an item that gave up are NaN, never
+ * stale values).  Reading clears both flags, so the next esc_moe_expert_path
+ * call does not also return ESC_ETIMEOUT for it.  Synchronises the stream.
+ * No counterpart in the reference (its expert path has no cross-workgroup
+ * hand-off). */
 int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int I,
                    int32_t* host_flag, void* stream);
+
+/* Test hook (no counterpart in the reference): the number of polls a wait of
+ * the one persistent expert launch makes before giving up, for every later
+ * call in the process; polls < 0 restores the default (2^18).  0 makes every
+ * wait give up at once, so the failure reporting can be tested with kernels
+ * that still run to their end. */
+int esc_moe_set_spin_limit(int polls);
 
 /* Decode-rate probe (measurement only; no counterpart in the reference): the
  * K=2 decode + dot2 loop of the expert GEMVs streamed by persistent

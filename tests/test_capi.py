@@ -268,6 +268,7 @@ def test_no_float_atomics_in_kernels():
         ("fused.hpp", "__hip_atomic_compare_exchange_strong(p, &expected, 1,"),  # claim(int* p)
         ("fused.hpp", "atomicOr(p.err, 1)"),                      # int flags
         ("fused.hpp", "atomicOr(p.status, 1)"),
+        ("escha_hip.hip", "__atomic_exchange_n(h, 0,"),           # host: int wait flag
     }
     csrc = Path(ops.__file__).resolve().parent / "csrc"
     found = set()

@@ -467,6 +467,42 @@ def test_moe_one_launch_status_and_reuse(monkeypatch):
     assert ops().moe_status(ws, 1, k, H, I) == 0
 
 
+def test_moe_one_launch_gave_up_wait_is_reported(monkeypatch):
+    """Failure reporting of the one persistent launch, forced from the host:
+    with a spin limit of 0 every down item's wait gives up at once (no wait
+    runs, so the kernel still reaches its end), its outputs are NaN, and the
+    next call on the device raises EschaWaitTimeout without running; the call
+    after that matches the good output bit-for-bit, and the workspace's own
+    flag still reads 1 once.  Read through esc_moe_status first instead, the
+    failure is reported once and no call raises."""
+    from escha_mlx_amd import _lib
+    E, H, I, k = 64, 512, 256, 8
+    c = _moe_case(E, H, I, 2, 2, 1, k, 13)
+    blk = _block(c, E, k, 2, 2, monkeypatch, exact=False)
+    ids, sc = ops().route_topk(torch.from_numpy(c["logits"]).to(DEV), k)
+    x = torch.from_numpy(c["x"]).to(DEV)
+    good = bits16(blk(x, ids, sc))
+    assert not np.isnan(good.view(np.float16)).any()
+    ws = blk._ws[(1, x.device)]
+    for via_status in (False, True):
+        ops().set_moe_spin_limit(0)
+        try:
+            bad = blk(x, ids, sc).float().cpu()
+        finally:
+            ops().set_moe_spin_limit(-1)
+        assert torch.isnan(bad).all()
+        if via_status:
+            assert ops().moe_status(ws, 1, k, H, I) == 1
+        else:
+            with pytest.raises(_lib.EschaWaitTimeout, match="bounded wait"):
+                blk(x, ids, sc)
+        assert np.array_equal(bits16(blk(x, ids, sc)), good)
+        # the workspace's own flag keeps the failure until esc_moe_status reads it
+        if not via_status:
+            assert ops().moe_status(ws, 1, k, H, I) == 1
+        assert ops().moe_status(ws, 1, k, H, I) == 0
+
+
 @pytest.mark.parametrize("K_gu,K_dn,I", [(2, 2, 512), (2, 3, 512), (3, 3, 512), (3, 2, 1024)])
 def test_moe_layers_one_launch_vs_oracle(K_gu, K_dn, I):
     """Independent token-layers in one launch (throughput mode): every layer's
