@@ -467,8 +467,28 @@ def c2_setup(torch, copies):
             for n, ic, oc, K_, lut in C2_PROJS}, g
 
 
+def _linear_multi(ops, Ps, x, i, lut):
+    """q, k and v of one input row on copy i: one esc_linear_multi launch."""
+    import torch
+    key = ("multi_ws", tuple(id(P) for P in Ps))
+    P0 = Ps[0]
+    if key not in P0:   # zero-filled once, before any graph capture
+        P0[key] = torch.zeros(max(ops.linear_multi_workspace(P0["K"], P0["ic"],
+                                                             [P["oc"] for P in Ps]), 4),
+                              dtype=torch.uint8, device=x.device)
+    sel = lambda P: (P["code"][i % len(P["code"])], P["rin"], P["rout"], P["K"], P["oc"], None)
+    return tuple(ops.linear_multi(x, [sel(P) for P in Ps], lut=lut, ws=P0[key]))
+
+
 def c2_layer(ops, P, xs, i):
-    """One decoder layer's projections, k and v as one pair launch."""
+    """One decoder layer's projections: at one row q, k and v (one input) as
+    one esc_linear_multi launch, then o, up and down; at several rows k and v
+    as one pair launch."""
+    if xs["q"].shape[0] == 1:
+        # one row: every projection with the table mix (k_proj_rows1; for up
+        # and down measured 23-25 us against 25-26 us by hash)
+        return (*_linear_multi(ops, [P["q"][0], P["k"][0], P["v"][0]], xs["q"], i, True),
+                *(_linear(ops, P[n][0], xs[n], i, True) for n in ("o", "up", "down")))
     pk, pv = P["k"][0], P["v"][0]
     return (*_linear_pair(ops, pk, pv, xs["k"], i, True),
             *(_linear(ops, P[n][0], xs[n], i, P[n][1]) for n in P if n not in ("k", "v")))
@@ -741,29 +761,36 @@ def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffi
             fkv = [lambda i=i: _linear_pair(ops, pk, pv, xs["k"], i, True) for i in range(L)]
             per[f"M{M}_kv_pair_us"] = round(graph_time(torch, fkv, args.steps * 5, args.warmup,
                                                        stream, f"M{M} kv pair") * 1e3, 2)
+            if M == 1:
+                pq = [P["q"][0], P["k"][0], P["v"][0]]
+                fm = [lambda i=i: _linear_multi(ops, pq, xs["q"], i, True) for i in range(L)]
+                per["M1_qkv_multi_us"] = round(graph_time(torch, fm, args.steps * 5, args.warmup,
+                                                          stream, "M1 qkv multi") * 1e3, 2)
             flp = [lambda i=i: c2_layer(ops, P, xs, i) for i in range(L)]
-            per[f"M{M}_layer_graph_kv_pair_us"] = round(
-                graph_time(torch, flp, args.steps, args.warmup, stream, f"M{M} layer kv pair") * 1e3, 2)
+            per[f"M{M}_layer_graph_fused_us"] = round(
+                graph_time(torch, flp, args.steps, args.warmup, stream, f"M{M} layer fused") * 1e3, 2)
             per[f"M{M}_layer_us"] = round(t_layer * 1e3, 2)
             per[f"M{M}_layer_gbs"] = round(C2_BYTES / (t_layer * 1e-3) / 1e9, 1)
             per[f"M{M}_tok_s_per_layer"] = round(M / (t_layer * 1e-3), 1)
-        # this line's value: the whole layer replayed as one HIP graph, k and v as
-        # one pair launch (the per-projection graphs' sum is M1_layer_gbs)
-        us_layer = per["M1_layer_graph_kv_pair_us"]
+        # this line's value: the whole layer replayed as one HIP graph, q, k and v
+        # as one launch (the per-projection graphs' sum is M1_layer_gbs)
+        us_layer = per["M1_layer_graph_fused_us"]
         gbs = C2_BYTES / (us_layer * 1e-6) / 1e9
         res.update(metric="coded-weight GB/s of one dense decoder layer (q,k,v,o K2 LUT, up/down "
                           "K3) at batch 1",
+                   # per-projection M1_* / M4_* lines: q, k, v, o with the table,
+                   # up and down by hash, each its own launch
                    value=round(gbs, 1), unit="GB/s", ms_per_step=round(us_layer / 1e3, 5),
-                   dtype="u32 codes -> f16 weights (LUT q/k/v/o, hash up/down), f32 accumulate",
+                   dtype="u32 codes -> f16 weights (table + hash mix), f32 accumulate",
                    config={"workload": "config 2: 27B-class dense layer, 5120 hidden, M=1 and "
                                        "M=4, the layer's projections replayed as one HIP graph "
-                                       "(k and v as one pair launch), 8 layer copies rotated "
-                                       "(745 MB, cold)"},
+                                       "(M=1: q, k, v as one launch; M=4: k and v as one pair "
+                                       "launch), 8 layer copies rotated (745 MB, cold)"},
                    bytes_per_layer=C2_BYTES, **per,
                    roofline=roofline_block(
                        "hbm", gbs, HBM_PEAK_GBS, "GB/s", tr, tr_detail,
-                       "the layer's k_linear_small (q, o LUT; up, down hash) + k_linear_pair "
-                       "(k, v) launches at batch 1, one HIP graph", bytes_per_layer=C2_BYTES,
+                       "the layer's four k_proj_rows1 launches at batch 1 (q+k+v, o, up, down; "
+                       "table + hash mix), one HIP graph", bytes_per_layer=C2_BYTES,
                        avg_layer_us=us_layer))
         if not args.no_cpu:
             res["cpu_baseline"] = c2_cpu()

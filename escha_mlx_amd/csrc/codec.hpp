@@ -99,4 +99,38 @@ __device__ __forceinline__ uint32_t step_state(WordFn w, int t) {
 // use it.  One copy per device, filled once by esc_init().
 __device__ uint16_t g_lut[65536];
 
+// Copying the table into LDS: 8,192 pieces of 16 bytes.  A load-then-store
+// loop waits one round trip to L2 per piece a thread copies; these issue
+// eight loads before the first store, so a workgroup of B threads (B dividing
+// 1024) waits 1024 / B round trips.
+constexpr int kTablePieces = 65536 / 8;
+__device__ __forceinline__ void copy_table(uint16_t* s_dst) {
+  const uint4* src = reinterpret_cast<const uint4*>(g_lut);
+  uint4* dst = reinterpret_cast<uint4*>(s_dst);
+  const int nt = blockDim.x;
+  for (int i0 = threadIdx.x; i0 < kTablePieces; i0 += 8 * nt) {
+    uint4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = src[i0 + k * nt];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dst[i0 + k * nt] = v[k];
+  }
+}
+// The same for a workgroup of exactly 1024 threads, in two halves, so that
+// other loads can be issued between them: table_fetch (the thread's eight
+// pieces into registers) and table_put (into LDS).
+struct TablePieces {
+  uint4 v[8];
+};
+__device__ __forceinline__ void table_fetch(TablePieces& t) {
+  const uint4* src = reinterpret_cast<const uint4*>(g_lut);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) t.v[k] = src[threadIdx.x + 1024 * k];
+}
+__device__ __forceinline__ void table_put(const TablePieces& t, uint16_t* s_dst) {
+  uint4* dst = reinterpret_cast<uint4*>(s_dst);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) dst[threadIdx.x + 1024 * k] = t.v[k];
+}
+
 }  // namespace esc

@@ -19,6 +19,7 @@
 #include "q8.hpp"
 #include "probe.hpp"
 #include "layers.hpp"
+#include "proj.hpp"
 
 namespace {
 
@@ -253,6 +254,25 @@ struct FastRowsF {
 constexpr int kLinearSmallRows = 16;
 constexpr int kLinearSmallRowsLut = 8;
 
+// k_proj_rows1: partial slots per 256-column group (at least the
+// workgroups a group of TK units can span: TK / 16 + 2 with P >= 1)
+int rows1_maxc(int TK) { return TK / 16 + 2; }
+// K=3 step pairs of every 8 that k_proj_rows1 decodes from the table
+constexpr int kTablePairs3 = 4;
+
+// One row (M = 1): the persistent table-mix kernel (k_proj_rows1) for the
+// table decode of a projection of at least kRows1MinUnits units (kt x
+// 256-column groups); the one-launch split-K kernel (k_linear_small)
+// otherwise.  Measured on MI355X with HIP-graph replay: the persistent kernel
+// is ahead from 5120 x 5120 (15.5 against 16.5 us K=2; 22.2 against 38.3 us
+// for K=3 5120 -> 17408) and behind below (4096 x 4096 K=2: 15.7 against
+// 14.6 us); by hash the split-K kernel is ahead or level at every size.
+constexpr long kRows1MinUnits = 6144;
+bool rows1_single(int M, int IC, int OC, bool lut) {
+  return M == 1 && lut && OC % 256 == 0 && (long)(IC / 16) * (OC / 256) >= kRows1MinUnits;
+}
+size_t rows1_part_bytes(int TK, int TN) { return (size_t)(TN / 16) * rows1_maxc(TK) * 256 * 4; }
+
 struct LinearPlan {
   int R, S, KS, groups, row_groups;
   size_t off_part, off_cnt, off_xh, off_mid, total;
@@ -289,6 +309,11 @@ LinearPlan linear_plan(int M, int K, int IC, int OC, bool lut) {
     p.off_cnt = 0;
     p.off_part = al((size_t)p.groups * std::max(p.row_groups, rg_max) * 4);
     p.total = p.off_part + al((size_t)p.S * M * OC * 4);
+    // one row, OC a multiple of 256: room for the persistent kernel
+    // (k_proj_rows1, also esc_linear_multi's), whose counters (one per 256
+    // columns) fit in the ones above and whose partials start at off_part
+    if (M == 1 && TN % 16 == 0)
+      p.total = std::max(p.total, p.off_part + al(rows1_part_bytes(TK, TN)));
   } else {
     p.off_xh = 0;
     p.off_mid = al((size_t)M * IC * 2);
@@ -354,6 +379,69 @@ int device_cus() {
     cus[dev] = n;
   }
   return cus[dev];
+}
+
+// k_proj_rows1 over a.np projections whose x .. TK, TN are filled: each
+// projection's plan from its own shape (one workgroup per CU, or more when a
+// wave would run more than kProjMaxP units), its workgroups after the
+// previous projection's.  K=2 with the table decodes kTablePairsLayers of 8
+// pairs from it, K=3 4 of 8.
+template <int K, int NT>
+int launch_rows1_k(const esc::ProjArgs& a, int grid, hipStream_t s) {
+  static std::once_flag once;
+  static hipError_t err = hipSuccess;
+  if constexpr (NT > 0)
+    std::call_once(once, [] {
+      err = hipFuncSetAttribute((const void*)esc::k_proj_rows1<K, NT>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 65536 * 2);
+    });
+  if (int rc = hip_check(err, "hipFuncSetAttribute")) return rc;
+  const size_t lds = NT > 0 ? 65536 * 2 : esc::kProjLdsWork;
+  hipLaunchKernelGGL((esc::k_proj_rows1<K, NT>), dim3(grid), dim3(64 * esc::kProjWaves), lds, s, a);
+  return launched("k_proj_rows1");
+}
+
+// units per wave for n units over wgs workgroups (at most kProjMaxP: more
+// workgroups than wgs when that is not enough)
+int rows1_units_per_wave(long n, int wgs) {
+  const long wg = esc::kProjWaves;
+  const long grid = std::max(std::min<long>(wgs, (n + wg - 1) / wg),
+                             (n + wg * esc::kProjMaxP - 1) / (wg * esc::kProjMaxP));
+  return (int)((n + wg * grid - 1) / (wg * grid));
+}
+
+int rows1_plan(esc::ProjOne& q, int P, int wg0) {
+  const long wg = esc::kProjWaves;
+  q.n = (q.TN / 16) * q.TK;
+  q.P = P;
+  q.maxc = rows1_maxc(q.TK);
+  q.wg0 = wg0;
+  return (int)((q.n + wg * q.P - 1) / (wg * q.P));  // workgroups with units
+}
+
+// merged: one P for all projections, from their total (one round of
+// workgroups for several small projections); otherwise each projection's P
+// from its own size, so that its outputs are those of its own launch.
+int launch_rows1(esc::ProjArgs& a, int K, bool lut, hipStream_t s, bool merged = false) {
+  // one workgroup per CU (two per CU without the table measured slower:
+  // fewer units per wave, more partials per group)
+  const int wgs = device_cus();
+  long total = 0;
+  for (int i = 0; i < a.np; ++i) {
+    ESC_REQUIRE((long)(a.pr[i].TN / 16) * a.pr[i].TK < (1L << 28), "projection too large");
+    total += (long)(a.pr[i].TN / 16) * a.pr[i].TK;
+  }
+  long grid = 0;
+  for (int i = 0; i < a.np; ++i) {
+    const int P = rows1_units_per_wave(merged ? total : (long)(a.pr[i].TN / 16) * a.pr[i].TK, wgs);
+    grid += rows1_plan(a.pr[i], P, (int)grid);
+  }
+  if (lut)
+    if (int rc = ensure_lut()) return rc;
+  if (K == 2)
+    return lut ? launch_rows1_k<2, esc::kTablePairsLayers>(a, (int)grid, s)
+               : launch_rows1_k<2, 0>(a, (int)grid, s);
+  return lut ? launch_rows1_k<3, kTablePairs3>(a, (int)grid, s) : launch_rows1_k<3, 0>(a, (int)grid, s);
 }
 
 // Row blocks of 16 per k_gemm_mma2 workgroup (NRB in {2,4,6,8}).  The kernel
@@ -506,6 +594,16 @@ int esc_linear(const uint16_t* x, const float* rin, const uint32_t* code, const 
   const int TK = IC / 16, TN = OC / 16;
   hipStream_t s = S(stream);
   char* w = static_cast<char*>(ws);
+  if (rows1_single(M, IC, OC, use_lut != 0)) {
+    // one row: the persistent kernel, its counters at off_cnt and its
+    // partials at off_part (linear_plan sizes both)
+    esc::ProjArgs a{};
+    a.np = 1;
+    a.rs = rs;
+    a.pr[0] = esc::ProjOne{x, rin, code, rout, bias, y, reinterpret_cast<float*>(w + lp.off_part),
+                           reinterpret_cast<int*>(w + lp.off_cnt), TK, TN};
+    return launch_rows1(a, K, use_lut != 0, s);
+  }
   if (M < kLinearSmallRows) {
     if (use_lut)
       if (int rc = ensure_lut()) return rc;
@@ -562,6 +660,29 @@ int esc_linear_pair(const uint16_t* x, int M, int IC, const float* rin0, const u
   const LinearPlan p0 = linear_plan(M, K0, IC, OC0, use_lut != 0);
   const LinearPlan p1 = linear_plan(M, K1, IC, OC1, use_lut != 0);
   char* w1 = w + off1;
+  const bool r0 = rows1_single(M, IC, OC0, use_lut != 0), r1 = rows1_single(M, IC, OC1, use_lut != 0);
+  if (r0 && r1 && K0 == K1) {
+    // one row: both projections in one persistent launch, each with its own
+    // plan and workspace, so each output is its own esc_linear call's
+    esc::ProjArgs a{};
+    a.np = 2;
+    a.rs = rs;
+    a.pr[0] = esc::ProjOne{x, rin0, code0, rout0, bias0, y0,
+                           reinterpret_cast<float*>(w + p0.off_part),
+                           reinterpret_cast<int*>(w + p0.off_cnt), TK, OC0 / 16};
+    a.pr[1] = esc::ProjOne{x, rin1, code1, rout1, bias1, y1,
+                           reinterpret_cast<float*>(w1 + p1.off_part),
+                           reinterpret_cast<int*>(w1 + p1.off_cnt), TK, OC1 / 16};
+    return launch_rows1(a, K0, use_lut != 0, S(stream));
+  }
+  if (r0 || r1) {
+    // one row, the projections on different kernels (or K): each as its own call
+    if (int rc = esc_linear(x, rin0, code0, rout0, bias0, M, K0, IC, OC0, use_lut, rs, y0, w, ws0,
+                            stream))
+      return rc;
+    return esc_linear(x, rin1, code1, rout1, bias1, M, K1, IC, OC1, use_lut, rs, y1, w + off1,
+                      ws_bytes - off1, stream);
+  }
   const esc::LinearSmallArgs a0 =
       small_args(x, rin0, code0, rout0, bias0, M, TK, OC0 / 16, p0, rs,
                  reinterpret_cast<float*>(w + p0.off_part), reinterpret_cast<int*>(w + p0.off_cnt), y0);
@@ -570,6 +691,46 @@ int esc_linear_pair(const uint16_t* x, int M, int IC, const float* rin0, const u
                  reinterpret_cast<float*>(w1 + p1.off_part), reinterpret_cast<int*>(w1 + p1.off_cnt), y1);
   return use_lut ? linear_pair_k<true>(K0, K1, a0, a1, S(stream))
                  : linear_pair_k<false>(K0, K1, a0, a1, S(stream));
+}
+
+size_t esc_linear_multi_workspace(int n, int K, int IC, const int* OC) {
+  if (n < 1 || n > esc::kProjMax || !OC) return 0;
+  size_t total = 0;
+  for (int i = 0; i < n; ++i) {
+    if (check_proj(K, IC, OC[i]) || OC[i] % 256) return 0;
+    // this projection's counters, then its partials
+    total += ((size_t)(OC[i] / 256) * 4 + 255) / 256 * 256 + rows1_part_bytes(IC / 16, OC[i] / 16);
+  }
+  return total;
+}
+
+int esc_linear_multi(const uint16_t* x, int IC, int K, int n, const uint32_t* const* code,
+                     const float* const* rin, const float* const* rout,
+                     const uint16_t* const* bias, const int* OC, int use_lut, float rs,
+                     uint16_t* const* y, void* ws, size_t ws_bytes, void* stream) {
+  ESC_REQUIRE(x && code && rin && rout && OC && y, "null pointer");
+  ESC_REQUIRE(n >= 1 && n <= esc::kProjMax, "%d projections (1 to %d)", n, esc::kProjMax);
+  for (int i = 0; i < n; ++i) {
+    if (int rc = check_proj(K, IC, OC[i])) return rc;
+    ESC_REQUIRE(code[i] && rin[i] && rout[i] && y[i], "null pointer (projection %d)", i);
+    ESC_REQUIRE(OC[i] % 256 == 0, "OC=%d of projection %d is not a multiple of 256", OC[i], i);
+  }
+  const size_t need = esc_linear_multi_workspace(n, K, IC, OC);
+  if (!ws || ws_bytes < need)
+    return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, need);
+  esc::ProjArgs a{};
+  a.np = n;
+  a.rs = rs;
+  char* w = static_cast<char*>(ws);
+  for (int i = 0; i < n; ++i) {
+    int* cnt = reinterpret_cast<int*>(w);
+    w += ((size_t)(OC[i] / 256) * 4 + 255) / 256 * 256;
+    float* part = reinterpret_cast<float*>(w);
+    w += rows1_part_bytes(IC / 16, OC[i] / 16);
+    a.pr[i] = esc::ProjOne{x, rin[i], code[i], rout[i], bias ? bias[i] : nullptr, y[i], part, cnt,
+                           IC / 16, OC[i] / 16};
+  }
+  return launch_rows1(a, K, use_lut != 0, S(stream), true);
 }
 
 size_t esc_gemm_rows_fast_workspace(int M, int R, int K, int IC, int OC) {

@@ -44,9 +44,7 @@ __device__ __forceinline__ float dec_f32(uint32_t s, const uint16_t* lut) {
 template <bool LUT>
 __device__ __forceinline__ void stage_lut(uint16_t* s_lut) {
   if constexpr (LUT) {
-    const uint4* src = reinterpret_cast<const uint4*>(g_lut);
-    uint4* dst = reinterpret_cast<uint4*>(s_lut);
-    for (int i = threadIdx.x; i < 65536 / 8; i += blockDim.x) dst[i] = src[i];
+    copy_table(s_lut);
     __syncthreads();
   }
 }

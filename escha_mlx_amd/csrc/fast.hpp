@@ -477,6 +477,61 @@ __device__ __forceinline__ void fast_tile_mix(const LaneWords<2>& lw, uint32_t w
   }
 }
 
+// K=3 tile decode with NT of every 8 step pairs from the table in LDS (at
+// byte address tb) and the rest by hash (as fast_tile_rows<3, false, 1>).
+// The two states of a pair (steps u + 8 and u) are 24 bits apart, so each
+// is extracted on its own (state3); a table pair then costs the two
+// extractions, two v_mad_u32_u16 for the byte addresses (the u16 operand
+// ignores the bits above the state), two ds_read_u16 and one v_lshl_or_b32,
+// against the extractions and 8 VALU by hash.  Same order of the reads, the
+// hash work and the products as fast_tile_mix: bit-identical to the hash
+// decode for every NT.
+template <int NT>
+__device__ __forceinline__ void fast_tile_mix3(const LaneWords<3>& lw, uint32_t wprev,
+                                               const uint32_t* xp, float* acc, uint32_t tb) {
+  const uint32_t clo = kClo, chi = kChi;
+  // pair k (0..15) is step u = 16 (k / 8) + k % 8 with step u + 8
+  auto step_of = [](int k) { return 16 * (k >> 3) + (k & 7); };
+  uint32_t tlo[16], thi[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    if ((k & 7) < 8 - NT) continue;
+    const int u = step_of(k);
+    const uint32_t s_lo = state3(lw, wprev, u + 8), s_hi = state3(lw, wprev, u);
+    uint32_t a_lo, a_hi;
+    __asm__("v_mad_u32_u16 %0, %1, 2, %2" : "=v"(a_lo) : "v"(s_lo), "v"(tb));
+    __asm__("v_mad_u32_u16 %0, %1, 2, %2" : "=v"(a_hi) : "v"(s_hi), "v"(tb));
+    tlo[k] = lds_u16(a_lo);
+    thi[k] = lds_u16(a_hi);
+  }
+  LaneWords<3> lh = lw;
+  uint32_t wph = wprev;
+  if constexpr (NT > 0)
+    __asm__ volatile("" : "+v"(lh.w[0]), "+v"(lh.w[1]), "+v"(lh.w[2]), "+v"(wph) : : "memory");
+  uint32_t hw[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    if ((k & 7) >= 8 - NT) continue;
+    const int u = step_of(k);
+    const uint32_t s_lo = state3(lh, wph, u + 8), s_hi = state3(lh, wph, u);
+    hw[k] = halves_sum2(mask_xor(hash_x<false>(s_lo, clo, chi)),
+                        mask_xor(hash_x<false>(s_hi, clo, chi)));
+    if constexpr (NT > 0) __asm__ volatile("" : "+v"(hw[k]));
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int u = step_of(k);
+    uint32_t w2;
+    if ((k & 7) < 8 - NT) {
+      w2 = hw[k];
+    } else {
+      __asm__ volatile("" : "+v"(tlo[k]), "+v"(thi[k]));
+      w2 = (thi[k] << 16) | tlo[k];
+    }
+    acc[Geo<3>::col_slot(u)] = dot2(xp[xpair_index(fast_row(u))], w2, acc[Geo<3>::col_slot(u)]);
+  }
+}
+
 // One wave's share of the split-K row-group GEMM on the matrix core: tiles
 // [tile0, tile0 + 16/LPT) of the stream at code_e over kt [z*KS, (z+1)*KS),
 // B column c = input row xr_c (the lane's row, xr), accumulated into acc.

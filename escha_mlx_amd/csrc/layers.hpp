@@ -67,9 +67,7 @@ struct LayersMoe {
 
 // This workgroup's copy of the decode table (LDS byte address).
 __device__ __forceinline__ uint32_t stage_table(uint16_t* s_tab) {
-  const uint4* src = reinterpret_cast<const uint4*>(g_lut);
-  uint4* dst = reinterpret_cast<uint4*>(s_tab);
-  for (int i = threadIdx.x; i < 65536 / 8; i += blockDim.x) dst[i] = src[i];
+  copy_table(s_tab);
   return (uint32_t)(size_t)s_tab;
 }
 
