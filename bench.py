@@ -11,9 +11,10 @@ every step reads its experts cold.
 
 Two measurements, both one token per layer (batch 1):
   sustained (the `value`): the 40 token-layers are independent and go to the
-      GPU as ONE esc_moe_expert_path_layers call (three kernels: every gate_up
-      item, every down item, the slot combine; the decode takes 4 of every 8
-      step pairs from a table in LDS); steady-state coded-weight throughput.
+      GPU as ONE esc_moe_expert_path_layers call (two kernels: every gate_up
+      item, then every down item with the slot combine; the decode takes 4 of
+      every 8 step pairs from a table in LDS); steady-state coded-weight
+      throughput.
   chained (`tok_s`): a decode step -- layer l's output is layer l+1's input --
       as 40 calls of the drop-in esc_moe_expert_path; tok/s = 1 / step.
 Inputs are resident in HBM before timing starts; HIP events on the launch stream.
@@ -49,9 +50,9 @@ BYTES_TOKEN_LAYER = TOP_K * (BYTES_GU + BYTES_DN)   # 6,291,456
 HBM_PEAK_GBS = 8000.0
 ROUTE_SETS = 4
 COPY_BYTES = 1 << 30                   # counter calibration copy
-KERNELS = ("k_moe_layers_gu", "k_moe_layers_dn", "k_moe_layers_combine")
-SUSTAINED_KERNELS = ("k_moe_layers_gu + k_moe_layers_dn + k_moe_layers_combine "
-                     "(table-assisted decode, 4 of 8 step pairs from LDS)")
+KERNELS = ("k_moe_layers_gu", "k_moe_layers_dn")
+SUSTAINED_KERNELS = ("k_moe_layers_gu + k_moe_layers_dn (slot combine in the down kernel; "
+                     "table-assisted decode, 4 of 8 step pairs from LDS)")
 
 
 def parse():

@@ -254,9 +254,10 @@ struct FastRowsF {
 constexpr int kLinearSmallRows = 16;
 constexpr int kLinearSmallRowsLut = 8;
 
-// k_proj_rows1: partial slots per 256-column group (at least the
-// workgroups a group of TK units can span: TK / 16 + 2 with P >= 1)
-int rows1_maxc(int TK) { return TK / 16 + 2; }
+// k_proj_rows1: partial slots per 256-column group, at least the workgroups
+// a group of TK units can span: every workgroup holds at least 8 units when
+// there are several (at most ceil(n / 16) workgroups for n units)
+int rows1_maxc(int TK) { return TK / 8 + 2; }
 // K=3 step pairs of every 8 that k_proj_rows1 decodes from the table
 constexpr int kTablePairs3 = 4;
 
@@ -401,31 +402,25 @@ int launch_rows1_k(const esc::ProjArgs& a, int grid, hipStream_t s) {
   return launched("k_proj_rows1");
 }
 
-// units per wave for n units over wgs workgroups (at most kProjMaxP: more
-// workgroups than wgs when that is not enough)
-int rows1_units_per_wave(long n, int wgs) {
-  const long wg = esc::kProjWaves;
-  const long grid = std::max(std::min<long>(wgs, (n + wg - 1) / wg),
-                             (n + wg * esc::kProjMaxP - 1) / (wg * esc::kProjMaxP));
-  return (int)((n + wg * grid - 1) / (wg * grid));
+// workgroups for n units: wgs, fewer when a wave would get fewer than two
+// units, more when it would get more than kProjMaxP.  (Measured on MI355X:
+// spreading 6,400 units over 256 workgroups, one or two per wave, is 5 %
+// slower than 200 workgroups of two per wave -- more partials per group; 5 to
+// 6 units per wave over 256 workgroups beat 6 over 227 by 2 %.)
+int rows1_workgroups(long n, long wgs) {
+  const long w = esc::kProjWaves;
+  return (int)std::max(std::min(wgs, (n + 2 * w - 1) / (2 * w)),
+                       (n + w * esc::kProjMaxP - 1) / (w * esc::kProjMaxP));
 }
 
-int rows1_plan(esc::ProjOne& q, int P, int wg0) {
-  const long wg = esc::kProjWaves;
-  q.n = (q.TN / 16) * q.TK;
-  q.P = P;
-  q.maxc = rows1_maxc(q.TK);
-  q.wg0 = wg0;
-  return (int)((q.n + wg * q.P - 1) / (wg * q.P));  // workgroups with units
-}
-
-// merged: one P for all projections, from their total (one round of
-// workgroups for several small projections); otherwise each projection's P
-// from its own size, so that its outputs are those of its own launch.
+// merged: the workgroups shared out over the projections by their units
+// (one round of workgroups for several small projections); otherwise each
+// projection's from its own size alone, so that its outputs are those of
+// its own launch.
 int launch_rows1(esc::ProjArgs& a, int K, bool lut, hipStream_t s, bool merged = false) {
   // one workgroup per CU (two per CU without the table measured slower:
   // fewer units per wave, more partials per group)
-  const int wgs = device_cus();
+  const int cus = device_cus();
   long total = 0;
   for (int i = 0; i < a.np; ++i) {
     ESC_REQUIRE((long)(a.pr[i].TN / 16) * a.pr[i].TK < (1L << 28), "projection too large");
@@ -433,8 +428,12 @@ int launch_rows1(esc::ProjArgs& a, int K, bool lut, hipStream_t s, bool merged =
   }
   long grid = 0;
   for (int i = 0; i < a.np; ++i) {
-    const int P = rows1_units_per_wave(merged ? total : (long)(a.pr[i].TN / 16) * a.pr[i].TK, wgs);
-    grid += rows1_plan(a.pr[i], P, (int)grid);
+    esc::ProjOne& q = a.pr[i];
+    q.n = (q.TN / 16) * q.TK;
+    q.G = rows1_workgroups(q.n, merged ? std::max(1L, (cus * (long)q.n + total / 2) / total) : cus);
+    q.maxc = rows1_maxc(q.TK);
+    q.wg0 = (int)grid;
+    grid += q.G;
   }
   if (lut)
     if (int rc = ensure_lut()) return rc;
@@ -1261,7 +1260,7 @@ int launch_fused(const esc::FusedMoe& p, int K_gu, int K_dn, int grid, hipStream
 // floats where their counters are.
 struct LayersWs {
   FusedPlan f;  // the item kernels' plan
-  size_t off_cnt_gu, off_cnt_dn, off_part, off_xh2, off_rows, total;
+  size_t off_cnt_gu, off_cnt_dn, off_cnt_cb, off_part, off_xh2, off_rows, total;
 };
 
 LayersWs layers_ws(int L, int T, int top_k, int H, int I) {
@@ -1270,7 +1269,8 @@ LayersWs layers_ws(int L, int T, int top_k, int H, int I) {
   const size_t M = (size_t)T * top_k, NB = I / 128, NKC = H / 128, NCP = H / 256;
   w.off_cnt_gu = al((size_t)fused_plan(L, T, top_k, H, I, true).n_int * 4);
   w.off_cnt_dn = w.off_cnt_gu + al(L * M * NB * 4);
-  const size_t ireg = w.off_cnt_dn + al(L * M * NCP * 4);
+  w.off_cnt_cb = w.off_cnt_dn + al(L * M * NCP * 4);
+  const size_t ireg = w.off_cnt_cb + al((size_t)L * T * NCP * 4);
   w.f = fused_plan(L, T, top_k, H, I, true, ireg);
   // partials: at most one slot per item of a group (one item per wave)
   w.off_part = ireg;
@@ -1306,6 +1306,7 @@ int launch_layers_table(const esc::MoeLayer* layers, const LayersWs& w, void* ws
   p.off_part = w.off_part;
   p.off_xh2 = w.off_xh2;
   p.off_rows = w.off_rows;
+  p.off_cnt_cb = w.off_cnt_cb;
   p.L = L;
   p.T = T;
   p.top_k = top_k;
@@ -1343,9 +1344,7 @@ int launch_layers_table(const esc::MoeLayer* layers, const LayersWs& w, void* ws
     hipLaunchKernelGGL(esc::k_moe_layers_dn<1>, dim3(grid), blk, lds, s, p);
   else
     hipLaunchKernelGGL(esc::k_moe_layers_dn<2>, dim3(grid), blk, lds, s, p);
-  if (int rc = launched("k_moe_layers_dn")) return rc;
-  hipLaunchKernelGGL(esc::k_moe_layers_combine, dim3((L * T * p.NHB + 3) / 4), dim3(256), 0, s, p);
-  return launched("k_moe_layers_combine");
+  return launched("k_moe_layers_dn");
 }
 }  // namespace
 

@@ -4,7 +4,7 @@
 // EschaSparseMoeBlock._expert_path, escha_mlx/models/qwen3_5_moe.py:207-253)
 // for 2-bit (K=2) gate_up and down.
 //
-// Launches: gate_up items, down items, slot combine.  The item kernels run
+// Launches: gate_up items, then down items with the slot combine.  The item kernels run
 // one workgroup of 16 waves per CU: it stages the 65,536-entry decode table
 // (128 KiB) in LDS once, and its waves decode kTablePairsLayers of every 8
 // step pairs from it and the rest by hash (fast_tile_mix).  Every wave works
@@ -28,8 +28,10 @@
 //     inputs: I/128 wave-steps of 16 tiles.  Groups (l, r, cp) of 8 items
 //     are published and finished as above: the output transform of both
 //     blocks into the f16 rows.
-//   combine (l, t, hb): the top_k rows of the token in slot order (f16(score)
-//     weights, float32 sum, one f16 rounding).
+//   combine (l, t, cp): the last of a token's top_k finishers of column pair
+//     cp (a device-scope counter per (l, t, cp), reset by it) sums the f16
+//     rows of the token in slot order (f16(score) weights, float32 sum, one
+//     f16 rounding) into y.
 //
 // Hand-offs use agent-scope atomics, with a wave's partial stores completed
 // (s_waitcnt) before its increment of the group counter; the finisher resets
@@ -54,6 +56,7 @@ struct LayersMoe {
   char* ws;                // workspace; byte offsets:
   size_t off_part;         //   [groups][maxc][2][128] f32 partials of this launch's groups
   size_t off_cnt;          //   [groups] int: partials published per group
+  size_t off_cnt_cb;       //   [L][T][H/256] int: down rows finished per (token, column pair)
   size_t off_xh2;          //   [L][M][I/2] u32 down inputs (paired f16 words)
   size_t off_rows;         //   [L][M][H/2] u32 down output rows (f16 pairs)
   int L, T, top_k, H, I;
@@ -69,6 +72,13 @@ struct LayersMoe {
 __device__ __forceinline__ uint32_t stage_table(uint16_t* s_tab) {
   copy_table(s_tab);
   return (uint32_t)(size_t)s_tab;
+}
+
+__device__ __forceinline__ void st_coherent_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_coherent_u32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void lds_wave_sync() {
@@ -306,6 +316,42 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_gu(LayersMoe p
 
 // ---------------------------------------------------------------- down
 
+// y of (l, t) at the column pair cp (blocks 2 cp and 2 cp + 1): the token's
+// top_k rows in slot order (f16(score) weights, float32 sum, one f16
+// rounding), read with device-coherent loads (other waves wrote them).
+__device__ __forceinline__ void combine_pair(const LayersMoe& p, int l, int t, int cp) {
+  const int lane = threadIdx.x & 63;
+  const MoeLayer& L = p.layers[l];
+  const uint32_t* rws = reinterpret_cast<const uint32_t*>(p.ws + p.off_rows) +
+                        ((size_t)l * p.M + t * p.top_k) * (p.H / 2) + 128 * cp + lane;
+  float s[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+  for (int k0 = 0; k0 < p.top_k; k0 += 8) {
+    uint32_t d8[2][8];
+    float w8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (k0 + j < p.top_k) {
+        d8[0][j] = ld_coherent_u32(rws + (size_t)(k0 + j) * (p.H / 2));
+        d8[1][j] = ld_coherent_u32(rws + (size_t)(k0 + j) * (p.H / 2) + 64);
+        w8[j] = (float)(half_t)L.scores[t * p.top_k + k0 + j];
+      }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (k0 + j < p.top_k) {
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+          s[blk][0] = s[blk][0] + (float)__builtin_bit_cast(half_t, (uint16_t)d8[blk][j]) * w8[j];
+          s[blk][1] = s[blk][1] + (float)__builtin_bit_cast(half_t, (uint16_t)(d8[blk][j] >> 16)) * w8[j];
+        }
+      }
+  }
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+    reinterpret_cast<uint32_t*>(L.y + (size_t)t * p.H + 256 * cp + 128 * blk)[lane] =
+        pack2((half_t)s[blk][0], (half_t)s[blk][1]);
+}
+
+
 struct DnItem {
   int l, r, cp, e8;
 };
@@ -411,45 +457,25 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_dn(LayersMoe p
         h128_wave(b0, b1);
         uint32_t* row = reinterpret_cast<uint32_t*>(p.ws + p.off_rows) +
                         (size_t)(it.l * p.M + it.r) * (p.H / 2) + 128 * it.cp + lane;
-        row[0] = pack2(to_f16((a0 * kRS) * ra.x), to_f16((a1 * kRS) * ra.y));
-        row[64] = pack2(to_f16((b0 * kRS) * rb.x), to_f16((b1 * kRS) * rb.y));
+        st_coherent_u32(row, pack2(to_f16((a0 * kRS) * ra.x), to_f16((a1 * kRS) * ra.y)));
+        st_coherent_u32(row + 64, pack2(to_f16((b0 * kRS) * rb.x), to_f16((b1 * kRS) * rb.y)));
+        wait_vm();
+        // the last of the token's top_k rows of this column pair combines them
+        const int t = it.r / p.top_k;
+        int last = 0;
+        if (lane == 0) {
+          int* c = reinterpret_cast<int*>(p.ws + p.off_cnt_cb) +
+                   ((size_t)it.l * p.T + t) * (p.NHB / 2) + it.cp;
+          last = add_relaxed(c, 1) == p.top_k - 1;
+          if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (__builtin_amdgcn_readfirstlane(last)) combine_pair(p, it.l, t, it.cp);
       }
 #pragma unroll
       for (int c = 0; c < 4; ++c) acc[c] = 0.f;
     }
     m = m1;
   }
-}
-
-// y of (l, t, column block hb): the token's top_k rows in slot order.
-// grid: ceil(L T NHB / 4) blocks of 256.
-__global__ __launch_bounds__(256) void k_moe_layers_combine(LayersMoe p) {
-  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (gw >= p.L * p.T * p.NHB) return;
-  const int lane = threadIdx.x & 63;
-  const int hb = gw % p.NHB, lt = gw / p.NHB, t = lt % p.T, l = lt / p.T;
-  const MoeLayer& L = p.layers[l];
-  const uint32_t* rws = reinterpret_cast<const uint32_t*>(p.ws + p.off_rows) +
-                        ((size_t)l * p.M + t * p.top_k) * (p.H / 2) + 64 * hb + lane;
-  float s0 = 0.f, s1 = 0.f;
-  for (int k0 = 0; k0 < p.top_k; k0 += 8) {
-    uint32_t d8[8];
-    float w8[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (k0 + j < p.top_k) {
-        d8[j] = rws[(size_t)(k0 + j) * (p.H / 2)];
-        w8[j] = (float)(half_t)L.scores[t * p.top_k + k0 + j];
-      }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (k0 + j < p.top_k) {
-        s0 = s0 + (float)__builtin_bit_cast(half_t, (uint16_t)d8[j]) * w8[j];
-        s1 = s1 + (float)__builtin_bit_cast(half_t, (uint16_t)(d8[j] >> 16)) * w8[j];
-      }
-  }
-  reinterpret_cast<uint32_t*>(L.y + (size_t)t * p.H + 128 * hb)[lane] =
-      pack2((half_t)s0, (half_t)s1);
 }
 
 }  // namespace esc

@@ -6,13 +6,16 @@
 // Work unit: one kt (16 inputs) of one column group (16 tiles = 256 output
 // columns) of one projection: 1 KiB of K=2 code (one wave-step) or 1.5 KiB of
 // K=3 code (two wave-steps of 8 tiles).  A projection's units are ordered
-// (column group, kt), and wave w of its workgroups runs units [wP, wP + P):
-// the code of consecutive kt of one column group, one unit's load in flight
-// while the previous one decodes.  With P <= 8 a wave's range touches at most
-// two 128-input blocks and at most two column groups, so it input-transforms
-// both blocks once at its start and keeps at most two partial sums in
-// registers.  Each projection has its own workgroups, P and partials, chosen
-// from its own shape: its outputs do not depend on what shares the launch.
+// (column group, kt); its G workgroups split them evenly (workgroup k:
+// [k n / G, (k + 1) n / G), rounded down) and each splits its range evenly
+// over its 16 waves, so every wave runs one run of consecutive units -- the
+// code of consecutive kt of one column group, one unit's load in flight while
+// the previous one decodes.  With at most 8 units per wave a range touches at
+// most two 128-input blocks and at most two column groups, so the wave
+// input-transforms both blocks once at its start and keeps at most two
+// partial sums in registers.  Each projection has its own workgroups and
+// partials; a single launch chooses G from the projection's own shape, so its
+// outputs do not depend on what else shares the launch.
 //
 // With the table (NT > 0; staged in LDS once per workgroup) NT of every 8
 // step pairs are decoded from it and the rest by hash (fast_tile_mix for K=2,
@@ -47,7 +50,7 @@ struct ProjOne {
   int* cnt;              // [TN/16] workgroups published per group (zero between calls)
   int TK, TN;            // IC / 16, OC / 16 (TN a multiple of 16)
   int n;                 // units: (TN / 16) TK
-  int P;                 // units per wave (<= kProjMaxP)
+  int G;                 // workgroups (at most kProjMaxP units per wave)
   int maxc;              // partial slots per group (>= the workgroups a group spans)
   int wg0;               // first workgroup of this projection in the launch
 };
@@ -69,6 +72,13 @@ struct ProjUnit {
 };
 __device__ __forceinline__ ProjUnit proj_unit(const ProjOne& q, int u) {
   return ProjUnit{u / q.TK, u % q.TK};
+}
+// first unit of workgroup k, and the workgroup that holds unit u
+__device__ __forceinline__ int proj_wg_start(const ProjOne& q, int k) {
+  return (int)((long)k * q.n / q.G);
+}
+__device__ __forceinline__ int proj_wg_of(const ProjOne& q, int u) {
+  return (int)(((long)(u + 1) * q.G - 1) / q.n);
 }
 
 // the first wave-step's words of unit (g, kt)
@@ -150,8 +160,8 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_proj_rows1(ProjArgs p) {
   for (int i = 1; i < kProjMax; ++i)
     if (i < p.np && (int)blockIdx.x >= p.pr[i].wg0) q = p.pr[i];
   const int wg = blockIdx.x - q.wg0;
-  const int a = (wg * kProjWaves + wave) * q.P;
-  const int b = min(a + q.P, q.n);
+  const int wa = proj_wg_start(q, wg), wlen = proj_wg_start(q, wg + 1) - wa;
+  const int a = wa + wave * wlen / kProjWaves, b = wa + (wave + 1) * wlen / kProjWaves;
   const bool busy = a < b;
   // per lane: K=2 16 consecutive tiles x 4 words; K=3 8 tiles x 3 words, twice
   const uint32_t off = (uint32_t)(lane * Geo<K>::WPL);
@@ -223,10 +233,8 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_proj_rows1(ProjArgs p) {
   __syncthreads();
 
   // 2. one wave per group of this workgroup: the waves' partials in wave order
-  const int span = kProjWaves * q.P;
-  const int wa = wg * span;
-  if (wa >= q.n) return;
-  const int gfirst = wa / q.TK, glast = (min(wa + span, q.n) - 1) / q.TK;
+  if (wlen == 0) return;
+  const int gfirst = wa / q.TK, glast = (wa + wlen - 1) / q.TK;
   for (int g = gfirst + wave; g <= glast; g += kProjWaves) {
     // the group's output scales and bias, requested before the hand-off so
     // that the finisher does not wait on them
@@ -250,7 +258,8 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_proj_rows1(ProjArgs p) {
     }
     // the workgroups that publish for group g (its units [g TK, (g+1) TK));
     // a group inside one workgroup needs no hand-off
-    const int wfirst = g * q.TK / span, count = ((g + 1) * q.TK - 1) / span - wfirst + 1;
+    const int wfirst = proj_wg_of(q, g * q.TK),
+              count = proj_wg_of(q, (g + 1) * q.TK - 1) - wfirst + 1;
     float4 t = s;
     if (count > 1) {
       float* part = q.part + (size_t)g * q.maxc * 256;
