@@ -58,8 +58,11 @@ SUSTAINED_KERNELS = ("k_moe_layers_gu + k_moe_layers_dn (slot combine in the dow
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # 300 untimed calls (about 45 ms of work for config 3) bring the GPU to its
+    # steady clock first: after 3 the sustained call measured 155-161 us per
+    # call, after 300 143.5-143.8 us (same box, alternating)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--cpu-sample", type=int, default=64,
                     help="token-layers timed through the CPU oracle")

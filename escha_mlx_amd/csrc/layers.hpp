@@ -68,11 +68,6 @@ struct LayersMoe {
   int maxc;  // partial slots per group (waves a group's items can span)
 };
 
-// This workgroup's copy of the decode table (LDS byte address).
-__device__ __forceinline__ uint32_t stage_table(uint16_t* s_tab) {
-  copy_table(s_tab);
-  return (uint32_t)(size_t)s_tab;
-}
 
 __device__ __forceinline__ void st_coherent_u32(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -206,8 +201,7 @@ struct GuMeta {
   const float* drin;     // the expert's down rin at input 128 b
 };
 
-__device__ __forceinline__ GuMeta gu_meta(const LayersMoe& p, const GuItem& it) {
-  const MoeLayer& L = p.layers[it.l];
+__device__ __forceinline__ GuMeta gu_meta(const LayersMoe& p, const MoeLayer& L, const GuItem& it) {
   const int e = L.ids[it.r];
   const size_t tn = 2 * p.I / 16;
   GuMeta m;
@@ -265,11 +259,20 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_gu(LayersMoe p
   extern __shared__ uint16_t s_tab[];
   __shared__ GuMeta s_meta[kLayersMaxRange * kLayersWaves];
   const int n = p.L * p.M * p.NB * p.NKC;
-  const uint32_t tb = stage_table(s_tab);
   {
+    // the item's layer record, then the table's pieces, then the item's
+    // routed pointers: the table copy overlaps the dependent loads
     const int t = threadIdx.x, i = blockIdx.x * kLayersWaves * p.P + t;
-    if (t < p.P * kLayersWaves && i < n) s_meta[t] = gu_meta(p, gu_item(p, i));
+    const bool has = t < p.P * kLayersWaves && i < n;
+    const GuItem it = gu_item(p, has ? i : 0);
+    const MoeLayer L = p.layers[it.l];
+    TablePieces tp;
+    table_fetch(tp);
+    const GuMeta m = gu_meta(p, L, it);
+    table_put(tp, s_tab);
+    if (has) s_meta[t] = m;
   }
+  const uint32_t tb = (uint32_t)(size_t)s_tab;
   __syncthreads();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -372,8 +375,7 @@ struct DnMeta {
   const float* rout;     // the expert's down rout at column 256 cp
 };
 
-__device__ __forceinline__ DnMeta dn_meta(const LayersMoe& p, const DnItem& it) {
-  const MoeLayer& L = p.layers[it.l];
+__device__ __forceinline__ DnMeta dn_meta(const LayersMoe& p, const MoeLayer& L, const DnItem& it) {
   const int e = L.ids[it.r];
   const size_t tn = p.H / 16;
   DnMeta m;
@@ -405,11 +407,19 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_dn(LayersMoe p
   __shared__ DnMeta s_meta[kLayersMaxRange * kLayersWaves];
   const int n = p.L * p.M * (p.NHB / 2) * kDownEighths;
   const int NS = p.I / 128;  // wave-steps per item
-  const uint32_t tb = stage_table(s_tab);
   {
+    // as in the gate_up kernel: the table copy overlaps the item's loads
     const int t = threadIdx.x, i = blockIdx.x * kLayersWaves * p.P + t;
-    if (t < p.P * kLayersWaves && i < n) s_meta[t] = dn_meta(p, dn_item(p, i));
+    const bool has = t < p.P * kLayersWaves && i < n;
+    const DnItem it = dn_item(p, has ? i : 0);
+    const MoeLayer L = p.layers[it.l];
+    TablePieces tp;
+    table_fetch(tp);
+    const DnMeta m = dn_meta(p, L, it);
+    table_put(tp, s_tab);
+    if (has) s_meta[t] = m;
   }
+  const uint32_t tb = (uint32_t)(size_t)s_tab;
   __syncthreads();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;

@@ -137,6 +137,7 @@ class EschaLinear(torch.nn.Module):
         envs.kt_block()  # validated like the reference's; no code tiles are staged here
         self._ws = {}  # zero-filled one-launch workspaces per (rows, device)
         self._pair_ws = {}  # the same for project_pair with this linear first
+        self._multi_ws = {}  # the same for project_many with this linear first
 
     @property
     def K(self) -> int:
@@ -222,6 +223,41 @@ def project_pair(first: EschaLinear, second: EschaLinear, x: torch.Tensor):
                              (w1.code, w1.rin, w1.rout, w1.K, w1.OC, second.bias),
                              lut=first._lut, ws=ws)
     return (y0.reshape(*shape[:-1], w0.OC).to(x.dtype), y1.reshape(*shape[:-1], w1.OC).to(x.dtype))
+
+
+def project_many(linears, x: torch.Tensor):
+    """Several coded projections of the same input (an attention block's q, k
+    and v): [lin(x) for lin in linears].  At one row, with one K, the input
+    width, the latched decode mode and the fused transforms in common and
+    every OC a multiple of 256, the 2 to 4 projections run as one launch
+    (esc_linear_multi), each within the tolerance contract of its own call;
+    otherwise two of them take project_pair and the rest their own calls.  No
+    counterpart in the reference, which fuses projections only for several
+    rows (escha_mlx/dense.py:365-437)."""
+    linears = list(linears)
+    shape = x.shape
+    rows = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
+    first = linears[0]
+    ws_ = [lin._w for lin in linears]
+    compatible = (
+        2 <= len(linears) <= 4 and rows.shape[0] == 1
+        and len({w.K for w in ws_}) == 1 and all(w.IC == rows.shape[-1] for w in ws_)
+        and all(w.OC % 256 == 0 for w in ws_)
+        and len({lin._lut for lin in linears}) == 1
+        and all(lin._fused_had and not lin._exact and lin._block_r_pin is None for lin in linears)
+    )
+    if not compatible:
+        if len(linears) == 2:
+            return list(project_pair(linears[0], linears[1], x))
+        return [lin(x) for lin in linears]
+    key = (rows.device, tuple(id(lin) for lin in linears[1:]))
+    ws = first._multi_ws.get(key)
+    if ws is None:
+        need = ops.linear_multi_workspace(ws_[0].K, ws_[0].IC, [w.OC for w in ws_])
+        ws = first._multi_ws[key] = torch.zeros(max(need, 4), dtype=torch.uint8, device=rows.device)
+    ys = ops.linear_multi(rows, [(w.code, w.rin, w.rout, w.K, w.OC, lin.bias)
+                                 for w, lin in zip(ws_, linears)], lut=first._lut, ws=ws)
+    return [y.reshape(*shape[:-1], w.OC).to(x.dtype) for y, w in zip(ys, ws_)]
 
 
 class EschaMLP(torch.nn.Module):

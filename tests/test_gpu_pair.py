@@ -98,6 +98,29 @@ def test_project_pair_and_fused_mlp_vs_oracle(m):
     assert ulps.max() <= 1
 
 
+@pytest.mark.parametrize("m", [1, 3])
+def test_project_many_vs_oracle(m):
+    """q, k and v of one input: one launch at one row (within the float16
+    tolerance of the oracle's projections), single calls otherwise
+    (bit-identical to them)."""
+    from escha_mlx_amd import dense
+    rng = np.random.default_rng(11 + m)
+    IC = 1024
+    mods = [_linear_mod(rng, IC, oc, 2, bias=(rng.standard_normal(oc) * 0.02).astype(np.float16)
+                        if oc == 512 else None) for oc in (512, 256, 768)]
+    x = rng.standard_normal((m, IC)).astype(np.float16)
+    xd = _dev(x)
+    ys = dense.project_many([mm for mm, _ in mods], xd)
+    for (mod, (code, rin, rout)), y in zip(mods, ys):
+        want = R.dense_linear(x, code, rin, rout, 2)
+        if mod.bias is not None:
+            want = (want.astype(np.float32) + mod.bias.cpu().numpy().astype(np.float32))
+        got = y.cpu().numpy().astype(np.float64)
+        assert np.abs(got - want).max() / np.abs(want).max() < 5e-3
+        if m > 1:
+            assert torch.equal(y, mod(xd))
+
+
 def test_project_pair_falls_back_when_incompatible(monkeypatch):
     from escha_mlx_amd import dense
     rng = np.random.default_rng(3)
