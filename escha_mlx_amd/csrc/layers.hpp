@@ -234,17 +234,28 @@ __device__ __forceinline__ uint32_t gu_inputs(uint32_t xw, float2 ri) {
 }
 
 // gate and up sums of the lane's two columns -> the lane's word of xh2
+// the lane's gate and up output scales and down input scales of the item's
+// h-block (requested before the group's hand-off, so the finisher does not
+// wait on them)
+struct GuScales {
+  float2 rg, ru, ri;
+};
+__device__ __forceinline__ GuScales gu_scales(const LayersMoe& p, const GuMeta& m) {
+  const int lane = threadIdx.x & 63;
+  return GuScales{*reinterpret_cast<const float2*>(m.rout + 2 * lane),
+                  *reinterpret_cast<const float2*>(m.rout + p.I + 2 * lane),
+                  *reinterpret_cast<const float2*>(m.drin + 2 * lane)};
+}
+
 __device__ __forceinline__ void gu_epilogue(const LayersMoe& p, int l, int r, int b,
-                                            const float* rout, const float* drin, float g0,
-                                            float g1, float u0, float u1) {
+                                            const GuScales& sc, float g0, float g1, float u0,
+                                            float u1) {
   const int lane = threadIdx.x & 63;
   h128_wave(g0, g1);
   h128_wave(u0, u1);
-  const float2 rg = *reinterpret_cast<const float2*>(rout + 2 * lane);
-  const float2 ru = *reinterpret_cast<const float2*>(rout + p.I + 2 * lane);
+  const float2 rg = sc.rg, ru = sc.ru, ri = sc.ri;
   const half_t h0 = swiglu1(to_f16((g0 * kRS) * rg.x), to_f16((u0 * kRS) * ru.x));
   const half_t h1 = swiglu1(to_f16((g1 * kRS) * rg.y), to_f16((u1 * kRS) * ru.y));
-  const float2 ri = *reinterpret_cast<const float2*>(drin + 2 * lane);
   float v0 = (float)h0 * ri.x;
   float v1 = (float)h1 * ri.y;
   h128_wave(v0, v1);
@@ -304,11 +315,12 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_gu(LayersMoe p
     }
     const int g = i / p.NKC;  // group (l, r, b)
     if (!more || (i + 1) / p.NKC != g) {
+      const GuScales sc = gu_scales(p, m);
       if (publish(p, g, p.NKC, acc)) {
         float g0, g1, u0, u1;
         group_sum(p, g, p.NKC, g0, g1, u0, u1);
         const GuItem it = gu_item(p, i);
-        gu_epilogue(p, it.l, it.r, it.b, m.rout, m.drin, g0, g1, u0, u1);
+        gu_epilogue(p, it.l, it.r, it.b, sc, g0, g1, u0, u1);
       }
 #pragma unroll
       for (int c = 0; c < 4; ++c) acc[c] = 0.f;
@@ -456,13 +468,14 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_dn(LayersMoe p
     }
     const int g = i / kDownEighths;  // group (l, r, cp)
     if (!more || (i + 1) / kDownEighths != g) {
+      // the output scales, requested before the hand-off
+      const float2 ra = *reinterpret_cast<const float2*>(m.rout + 2 * lane);
+      const float2 rb = *reinterpret_cast<const float2*>(m.rout + 128 + 2 * lane);
       if (publish(p, g, kDownEighths, acc)) {
         // columns 2 lane, +1 of block 2 cp (tiles 0-7, a) and 2 cp + 1 (b)
         float a0, a1, b0, b1;
         group_sum(p, g, kDownEighths, a0, a1, b0, b1);
         const DnItem it = dn_item(p, i);
-        const float2 ra = *reinterpret_cast<const float2*>(m.rout + 2 * lane);
-        const float2 rb = *reinterpret_cast<const float2*>(m.rout + 128 + 2 * lane);
         h128_wave(a0, a1);
         h128_wave(b0, b1);
         uint32_t* row = reinterpret_cast<uint32_t*>(p.ws + p.off_rows) +
