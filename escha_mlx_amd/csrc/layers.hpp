@@ -76,6 +76,22 @@ __device__ __forceinline__ uint32_t ld_coherent_u32(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Issue priority from the work a wave has left: a SIMD issues from its
+// oldest ready wave first, so with equal ranges the oldest wave runs ahead
+// and the youngest is left alone at the end with nothing to hide its
+// latencies; a wave with more items left gets the higher priority instead,
+// and the waves of a SIMD finish together.
+__device__ __forceinline__ void prio_left(int left) {
+  if (left >= 4)
+    __builtin_amdgcn_s_setprio(3);
+  else if (left == 3)
+    __builtin_amdgcn_s_setprio(2);
+  else if (left == 2)
+    __builtin_amdgcn_s_setprio(1);
+  else
+    __builtin_amdgcn_s_setprio(0);
+}
+
 __device__ __forceinline__ void lds_wave_sync() {
   __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
@@ -300,6 +316,7 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_gu(LayersMoe p
   float2 ri = *reinterpret_cast<const float2*>(m.rin + 2 * lane);
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (int i = i0; i < iend; ++i) {
+    prio_left(iend - i);
     const bool more = i + 1 < iend;
     const GuMeta m1 = more ? gu_meta_uniform(meta[i + 1]) : m;
     const uint32_t xv = gu_inputs(xw, ri);
@@ -447,6 +464,7 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_dn(LayersMoe p
   dn_load_inputs<QV>(p, i0, xq);
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (int i = i0; i < iend; ++i) {
+    prio_left(iend - i);
     const bool more = i + 1 < iend;
     const int in = more ? i + 1 : i;
     const DnMeta m1 = {uniform_ptr(meta[in].code), uniform_ptr(meta[in].rout)};
