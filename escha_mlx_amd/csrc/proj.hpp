@@ -198,6 +198,7 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_proj_rows1(ProjArgs p) {
   if (busy) {
 #pragma unroll 1
     for (int u = a; u < b; ++u) {
+      prio_left(b - u);
       // the next unit (this one again at the end: in bounds, unused)
       ProjUnit cn = c;
       if (u + 1 < b && ++cn.kt == q.TK) {
