@@ -40,6 +40,16 @@ __global__ __launch_bounds__(1024) void k_decode_probe(const uint32_t* __restric
 #pragma unroll
   for (int j = 0; j < PF; ++j) w[j] = load_lane_words<2>(lp + (size_t)j * 256);
   for (int k0 = 0; k0 < steps; k0 += 4) {
+    // issue priority from the quarter of the range left, as in the item
+    // kernels (otherwise the oldest wave of a SIMD runs ahead and the last
+    // ones finish alone)
+    {
+      const int q4 = 4 * (steps - k0) / steps;
+      if (q4 >= 3) __builtin_amdgcn_s_setprio(3);
+      else if (q4 == 2) __builtin_amdgcn_s_setprio(2);
+      else if (q4 == 1) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int k = k0 + j;
