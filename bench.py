@@ -370,8 +370,7 @@ def _linear(ops, P, x, i, lut, mat=True):
     if key not in P:   # zero-filled once, before any graph capture
         P[key] = torch.zeros(max(ops.linear_workspace(m, P["K"], P["ic"], P["oc"]), 4),
                              dtype=torch.uint8, device=x.device)
-    ws = P[key] if m < ops.LINEAR_SMALL_ROWS else None
-    return ops.linear(x, code, P["rin"], P["rout"], P["K"], P["ic"], P["oc"], lut=lut, ws=ws)
+    return ops.linear(x, code, P["rin"], P["rout"], P["K"], P["ic"], P["oc"], lut=lut, ws=P[key])
 
 
 def _linear_pair(ops, P0, P1, x, i, lut):
@@ -805,9 +804,13 @@ def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffi
         flop = 2 * M * 5120 * (17408 + 5120)
         xh_up = ops.scaled_had(x, up["rin"], None)
         xh_o = ops.scaled_had(x, o["rin"], None)
-        ms_gu = timed(torch, lambda i: ops.dense_gemm_mat(xh_up, up["code"][0], 3, 5120, 17408),
+        # the module's GEMM launches on their own: esc_gemm_mfma_out (the
+        # GEMM with the output transform in its epilogue) on the transformed rows
+        ms_gu = timed(torch, lambda i: ops.gemm_mfma_out(xh_up, up["code"][0], up["rout"], 3, 5120,
+                                                         17408),
                       args.steps, args.warmup, stream)
-        ms_go = timed(torch, lambda i: ops.dense_gemm_mat(xh_o, o["code"][0], 2, 5120, 5120),
+        ms_go = timed(torch, lambda i: ops.gemm_mfma_out(xh_o, o["code"][0], o["rout"], 2, 5120,
+                                                         5120),
                       args.steps, args.warmup, stream)
         ms_mod = timed(torch, lambda i: (_linear(ops, up, x, i, False), _linear(ops, o, x, i, False)),
                        args.steps, args.warmup, stream)
@@ -822,9 +825,10 @@ def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffi
                    gemm_up_us=round(ms_gu * 1e3, 1), gemm_o_us=round(ms_go * 1e3, 1),
                    roofline=roofline_block(
                        "mfma", tf_k, 2500.0, "TFLOP/s", tr, tr_detail,
-                       "k_gemm_mma2<3,8> + k_gemm_mma2<2,6> (row blocks per workgroup chosen "
-                       "by the host for this shape); traffic: HBM bytes per module pass (both "
-                       "projections, input transforms included)",
+                       "k_gemm_mma2<3,8,true> + k_gemm_mma2<2,6,true> (esc_gemm_mfma_out: the "
+                       "GEMM with the output transform in its epilogue; row blocks per workgroup "
+                       "chosen by the host for this shape); traffic: HBM bytes per module pass "
+                       "(both projections, input transforms included)",
                        flop_per_launch_pair=flop))
         if not args.no_cpu:
             res["cpu_baseline"] = c5_cpu()

@@ -40,6 +40,8 @@ SIGNATURES = {
     "esc_dense_gemm_rows": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _P, _P]),
     "esc_dense_gemm_rows_out": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P]),
     "esc_gemm_mfma": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _P]),
+    "esc_gemm_mfma_out_workspace": (_Z, [_I, _I, _I, _I]),
+    "esc_gemm_mfma_out": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _Z, _P]),
     "esc_linear_workspace": (_Z, [_I, _I, _I, _I]),
     "esc_linear": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _Z, _P]),
     "esc_linear_pair_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),

@@ -616,9 +616,31 @@ int esc_linear(const uint16_t* x, const float* rin, const uint32_t* code, const 
   // transform in its epilogue (or GEMM + output transform for OC % 256 != 0)
   uint16_t* xh = reinterpret_cast<uint16_t*>(w + lp.off_xh);
   if (int rc = esc_input_transform(x, rin, nullptr, M, IC, rs, xh, stream)) return rc;
+  return esc_gemm_mfma_out(xh, code, rout, bias, M, K, IC, OC, rs, y, w + lp.off_mid,
+                           lp.total - lp.off_mid, stream);
+}
+
+size_t esc_gemm_mfma_out_workspace(int M, int K, int IC, int OC) {
+  if (check_proj(K, IC, OC) || M <= 0) return 0;
+  return OC % 256 ? (size_t)M * OC * sizeof(float) : 0;
+}
+
+int esc_gemm_mfma_out(const uint16_t* xh, const uint32_t* code, const float* rout,
+                      const uint16_t* bias, int M, int K, int IC, int OC, float rs, uint16_t* y,
+                      void* ws, size_t ws_bytes, void* stream) {
+  if (int rc = check_proj(K, IC, OC)) return rc;
+  ESC_REQUIRE(xh && code && rout && y, "null pointer");
+  ESC_REQUIRE(M >= 0, "negative row count");
+  if (M == 0) return ESC_OK;
+  const int TK = IC / 16, TN = OC / 16;
+  hipStream_t s = S(stream);
+  // OC a multiple of 256: the output transform in the GEMM's epilogue
   if (TN % 16 == 0) return gemm_mma2<true>(K, xh, code, M, TK, TN, nullptr, rout, bias, rs, y, s);
-  float* mid = reinterpret_cast<float*>(w + lp.off_mid);
-  if (int rc = esc_gemm_mfma(xh, code, M, K, IC, OC, use_lut, mid, stream)) return rc;
+  const size_t need = esc_gemm_mfma_out_workspace(M, K, IC, OC);
+  if (!ws || ws_bytes < need)
+    return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, need);
+  float* mid = static_cast<float*>(ws);
+  if (int rc = esc_gemm_mfma(xh, code, M, K, IC, OC, 0, mid, stream)) return rc;
   return esc_output_transform(mid, rout, nullptr, bias, M, OC, rs, y, stream);
 }
 

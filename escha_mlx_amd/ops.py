@@ -311,6 +311,32 @@ def dense_gemm_rows_fast_out(xh: torch.Tensor, code_u32: torch.Tensor, rout: tor
     return out
 
 
+def gemm_mfma_out_workspace(m: int, K: int, IC: int, OC: int) -> int:
+    return int(_lib.load().esc_gemm_mfma_out_workspace(m, K, IC, OC))
+
+
+def gemm_mfma_out(xh: torch.Tensor, code_u32: torch.Tensor, rout: torch.Tensor, K: int, IC: int,
+                  OC: int, bias: torch.Tensor | None = None, rs: float = RS,
+                  ws: torch.Tensor | None = None) -> torch.Tensor:
+    """The many-row GEMM with its output transform -> y f16 [m, OC]
+    (EschaLinear's dense_gemm_mat + dense_scaled_had_out, dense.py:356): for
+    OC a multiple of 256 one launch with the transform in its epilogue, else
+    the GEMM into ws (f32 mid) and the output transform."""
+    _dev(xh, code_u32, rout, bias)
+    m = xh.shape[0]
+    if xh.dtype != torch.float16 or tuple(xh.shape) != (m, IC):
+        raise ValueError(f"xh must be f16 [m, {IC}]")
+    y = torch.empty((m, OC), dtype=torch.float16, device=xh.device)
+    if m == 0:
+        return y
+    if ws is None:
+        ws = torch.empty(max(gemm_mfma_out_workspace(m, K, IC, OC), 4), dtype=torch.uint8,
+                         device=xh.device)
+    _lib.call("esc_gemm_mfma_out", _ptr(xh), _ptr(_as_u32(code_u32)), _ptr(rout), _ptr(bias), m, K,
+              IC, OC, rs, _ptr(y), _ptr(ws), ws.numel(), _stream())
+    return y
+
+
 def dense_gemm_mat(xh: torch.Tensor, code_u32: torch.Tensor, K: int, IC: int, OC: int,
                    lut: bool | None = None) -> torch.Tensor:
     """Matrix-core dense GEMM -> mid f32 [m, OC] (msl.py:1762-1782).  Deterministic,

@@ -111,6 +111,21 @@ int esc_dense_gemm_rows_out(const uint16_t* xh, const uint32_t* code, const floa
 int esc_gemm_mfma(const uint16_t* xh, const uint32_t* code, int M, int K, int IC, int OC,
                   int use_lut, float* mid, void* stream);
 
+/* The many-row GEMM and its output transform in one step: y f16 [M][OC] =
+ * (bias +) f16((H128(xh @ decode(code)) * rs) * rout), xh f16 [M][IC] already
+ * input-transformed.  For OC a multiple of 256 the transform runs in the
+ * epilogue of esc_gemm_mfma's kernel (no f32 mid; ws unused, the workspace
+ * size is 0); otherwise esc_gemm_mfma into ws (esc_gemm_mfma_out_workspace
+ * bytes, M * OC f32), then esc_output_transform.  Bit-identical to those two
+ * calls; deterministic, reassociated float32 sum (tolerance contract).
+ * Replaces EschaLinear's many-row path, self._output_rows(self._gemv(xh))
+ * (escha_mlx/dense.py:356): msl.dense_gemm_mat then msl.dense_scaled_had_out
+ * (escha_mlx/msl.py:1762-1782, 1486-1489). */
+size_t esc_gemm_mfma_out_workspace(int M, int K, int IC, int OC);
+int esc_gemm_mfma_out(const uint16_t* xh, const uint32_t* code, const float* rout,
+                      const uint16_t* bias, int M, int K, int IC, int OC, float rs, uint16_t* y,
+                      void* ws, size_t ws_bytes, void* stream);
+
 /* The whole coded linear, y f16 [M][OC] = (bias +) f16((H128(xh @ W) * rs) *
  * rout) with xh = f16(H128(f32(x) * rin) * rs), x f16 [M][IC], rin f32 [IC],
  * rout f32 [OC], bias f16 [OC] or NULL (added in f32 after the f16 round).
@@ -118,7 +133,7 @@ int esc_gemm_mfma(const uint16_t* xh, const uint32_t* code, int M, int K, int IC
  * the VALU for one row, for 2..15 rows the rows of a group share each decoded
  * weight on the matrix core; the last split of each column group sums the
  * partials in fixed order and output-transforms); M >= 16: input transform,
- * matrix-core GEMM, output transform.  ws: esc_linear_workspace bytes, zero-filled before its
+ * then esc_gemm_mfma_out.  ws: esc_linear_workspace bytes, zero-filled before its
  * first use (its counters are left zero after every call); calls sharing one
  * ws must not overlap.  Tolerance contract (reassociated float32 sum);
  * decoded weights bit-exact.

@@ -108,3 +108,74 @@ def test_dense_module_prefill_uses_matrix_path(monkeypatch):
     y_rows = EschaLinear(w)(x)
     d = (y_mat.float() - y_rows.float()).abs().max() / y_rows.float().abs().mean()
     assert float(d) < 5e-3
+
+
+# ---- esc_gemm_mfma_out: the many-row GEMM with its output transform (one
+# launch for OC a multiple of 256, else GEMM into the workspace + transform)
+OUT_SHAPES = [(2, 512, 5120, 2048), (3, 1024, 3072, 2100), (3, 512, 640, 70), (2, 256, 384, 33),
+              (2, 1024, 1024, 300)]
+
+
+def _rout(rng, oc):
+    return (rng.choice([-1.0, 1.0], oc) * rng.uniform(0.5, 1.5, oc) * 1e-2).astype(
+        np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("K,ic,oc,m", OUT_SHAPES)
+def test_gemm_out_one_hot_rows_exact(K, ic, oc, m):
+    """One non-zero input per row: each output row is the oracle's output
+    transform of v * W[k] bit-for-bit, with and without bias."""
+    rng = np.random.default_rng(41 * K + m)
+    u32, code = _code(rng, ic, oc, K)
+    rout = _rout(rng, oc)
+    bias = (rng.standard_normal(oc) * 0.05).astype(np.float16)
+    k_of_row = rng.integers(0, ic, size=m)
+    v = rng.choice([-1.5, 0.75, 1.0, 2.0], size=m).astype(np.float16)
+    xh = np.zeros((m, ic), np.float16)
+    xh[np.arange(m), k_of_row] = v
+    w = R.reconstruct(u32, ic, oc, K)
+    mid = v.astype(np.float32)[:, None] * w[k_of_row].astype(np.float32)
+    want = R.output_transform(mid, rout)
+    xh_d, rout_d = torch.from_numpy(xh).to(DEV), torch.from_numpy(rout).to(DEV)
+    y = ops().gemm_mfma_out(xh_d, code, rout_d, K, ic, oc).cpu().numpy()
+    assert np.array_equal(y.view(np.uint16), want.view(np.uint16))
+    yb = ops().gemm_mfma_out(xh_d, code, rout_d, K, ic, oc,
+                             bias=torch.from_numpy(bias).to(DEV)).cpu().numpy()
+    wantb = (want.astype(np.float32) + bias.astype(np.float32)).astype(np.float16)
+    assert np.array_equal(yb.view(np.uint16), wantb.view(np.uint16))
+
+
+@pytest.mark.parametrize("K,ic,oc,m", OUT_SHAPES[:4])
+def test_gemm_out_vs_f64_and_two_launches(K, ic, oc, m):
+    """Random rows: within the float16 tolerance of the float64 product after
+    the output transform, and bit-identical to esc_gemm_mfma followed by
+    esc_output_transform (the same float32 order)."""
+    rng = np.random.default_rng(17 * K + m)
+    u32, code = _code(rng, ic, oc, K)
+    rout = _rout(rng, oc)
+    xh = (rng.standard_normal((m, ic)) * 0.3).astype(np.float16)
+    xh_d, rout_d = torch.from_numpy(xh).to(DEV), torch.from_numpy(rout).to(DEV)
+    y = ops().gemm_mfma_out(xh_d, code, rout_d, K, ic, oc)
+    exact = R.h128(xh.astype(np.float64) @ R.reconstruct(u32, ic, oc, K).astype(np.float64)) \
+        * R.RS * rout
+    got = y.cpu().numpy().astype(np.float64)
+    err = (np.abs(got - exact).max(axis=1) / np.abs(exact).max(axis=1)).max()
+    assert err < 2e-3, err
+    two = ops().scaled_had_out(ops().dense_gemm_mat(xh_d, code, K, ic, oc), rout_d, None)
+    assert torch.equal(y, two)
+
+
+def test_linear_many_rows_is_transform_then_gemm_out():
+    """esc_linear from 16 rows = esc_input_transform then esc_gemm_mfma_out,
+    bit-identical."""
+    rng = np.random.default_rng(23)
+    K, ic, oc, m = 2, 512, 5120, 2048
+    u32, code = _code(rng, ic, oc, K)
+    rin = rng.choice([-1.0, 1.0], ic).astype(np.float16).astype(np.float32)
+    rout = _rout(rng, oc)
+    bias = torch.from_numpy((rng.standard_normal(oc) * 0.05).astype(np.float16)).to(DEV)
+    x = torch.from_numpy(rng.standard_normal((m, ic)).astype(np.float16)).to(DEV)
+    rin_d, rout_d = torch.from_numpy(rin).to(DEV), torch.from_numpy(rout).to(DEV)
+    y = ops().linear(x, code, rin_d, rout_d, K, ic, oc, bias=bias)
+    want = ops().gemm_mfma_out(ops().scaled_had(x, rin_d, None), code, rout_d, K, ic, oc, bias=bias)
+    assert torch.equal(y, want)
