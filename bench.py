@@ -446,7 +446,7 @@ C2_PROJS = [("q", 5120, 5120, 2, True), ("k", 5120, 5120, 2, True), ("v", 5120, 
             ("o", 5120, 5120, 2, True), ("up", 5120, 17408, 3, False),
             ("down", 17408, 5120, 3, False)]
 C2_BYTES = sum(ic * oc * K_ // 8 for _, ic, oc, K_, _ in C2_PROJS)
-TRAFFIC_KERNELS = {1: ("k_linear_small",), 2: ("k_proj_rows1",),
+TRAFFIC_KERNELS = {1: ("k_linear_small",), 2: ("k_proj_rows1", "k_linear_small"),
                    4: ("k_gemv_fast_rows", "k_moe_prep", "k_moe_mid", "k_moe_combine"),
                    5: ("k_gemm_mma2", "k_input_transform")}
 
@@ -489,8 +489,9 @@ def c2_layer(ops, P, xs, i):
     one esc_linear_multi launch, then o, up and down; at several rows k and v
     as one pair launch."""
     if xs["q"].shape[0] == 1:
-        # one row: every projection with the table mix (k_proj_rows1; for up
-        # and down measured 23-25 us against 25-26 us by hash)
+        # one row, the table decode asked for: q+k+v, up and down in
+        # k_proj_rows1 (table mix), o below its size bound in k_linear_small
+        # by hash
         return (*_linear_multi(ops, [P["q"][0], P["k"][0], P["v"][0]], xs["q"], i, True),
                 *(_linear(ops, P[n][0], xs[n], i, True) for n in ("o", "up", "down")))
     pk, pv = P["k"][0], P["v"][0]
@@ -793,8 +794,9 @@ def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffi
                    bytes_per_layer=C2_BYTES, **per,
                    roofline=roofline_block(
                        "hbm", gbs, HBM_PEAK_GBS, "GB/s", tr, tr_detail,
-                       "the layer's four k_proj_rows1 launches at batch 1 (q+k+v, o, up, down; "
-                       "table + hash mix), one HIP graph", bytes_per_layer=C2_BYTES,
+                       "the layer's four launches at batch 1, one HIP graph: k_proj_rows1 for "
+                       "q+k+v, up and down (table + hash mix), k_linear_small for o (hash)",
+                       bytes_per_layer=C2_BYTES,
                        avg_layer_us=us_layer))
         if not args.no_cpu:
             res["cpu_baseline"] = c2_cpu()

@@ -263,14 +263,21 @@ constexpr int kTablePairs3 = 4;
 
 // One row (M = 1): the persistent table-mix kernel (k_proj_rows1) for the
 // table decode of a projection of at least kRows1MinUnits units (kt x
-// 256-column groups); the one-launch split-K kernel (k_linear_small)
-// otherwise.  Measured on MI355X with HIP-graph replay: the persistent kernel
-// is ahead from 5120 x 5120 (15.5 against 16.5 us K=2; 22.2 against 38.3 us
-// for K=3 5120 -> 17408) and behind below (4096 x 4096 K=2: 15.7 against
-// 14.6 us); by hash the split-K kernel is ahead or level at every size.
-constexpr long kRows1MinUnits = 6144;
+// 256-column groups); the one-launch split-K kernel (k_linear_small) by hash
+// otherwise, also when the table decode was asked for (the two decodes give
+// the same weights; by hash the split-K kernel is ahead of its table form at
+// every size).  Measured on MI355X with HIP-graph replay: K=2 5120 x 5120
+// (6,400 units) 12.35 us by hash split-K against 14.8 us in the persistent
+// kernel; K=3 5120 -> 17408 (21,760 units) 20.0 against 22.6 us, and
+// 17408 -> 5120 level (23.2 against 23.1 us).
+constexpr long kRows1MinUnits = 16384;
 bool rows1_single(int M, int IC, int OC, bool lut) {
   return M == 1 && lut && OC % 256 == 0 && (long)(IC / 16) * (OC / 256) >= kRows1MinUnits;
+}
+// The decode a one-launch linear runs: the table only where the persistent
+// kernel takes it (one row) or for 2..15 rows.
+bool linear_uses_lut(int M, int IC, int OC, bool lut) {
+  return lut && (M != 1 || rows1_single(M, IC, OC, lut));
 }
 size_t rows1_part_bytes(int TK, int TN) { return (size_t)(TN / 16) * rows1_maxc(TK) * 256 * 4; }
 
@@ -587,6 +594,7 @@ int esc_linear(const uint16_t* x, const float* rin, const uint32_t* code, const 
   ESC_REQUIRE(x && rin && code && rout && y, "null pointer");
   ESC_REQUIRE(M >= 0, "negative row count");
   if (M == 0) return ESC_OK;
+  use_lut = linear_uses_lut(M, IC, OC, use_lut != 0);
   const LinearPlan lp = linear_plan(M, K, IC, OC, use_lut != 0);
   if (!ws || ws_bytes < lp.total)
     return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, lp.total);
@@ -675,13 +683,15 @@ int esc_linear_pair(const uint16_t* x, int M, int IC, const float* rin0, const u
     return esc_linear(x, rin1, code1, rout1, bias1, M, K1, IC, OC1, use_lut, rs, y1, w + off1,
                       ws_bytes - off1, stream);
   }
+  const bool r0 = rows1_single(M, IC, OC0, use_lut != 0), r1 = rows1_single(M, IC, OC1, use_lut != 0);
+  // the pair kernel runs the decode each projection's own call would
+  if (!r0 && !r1) use_lut = linear_uses_lut(M, IC, OC0, use_lut != 0);
   if (use_lut)
     if (int rc = ensure_lut()) return rc;
   const int TK = IC / 16;
   const LinearPlan p0 = linear_plan(M, K0, IC, OC0, use_lut != 0);
   const LinearPlan p1 = linear_plan(M, K1, IC, OC1, use_lut != 0);
   char* w1 = w + off1;
-  const bool r0 = rows1_single(M, IC, OC0, use_lut != 0), r1 = rows1_single(M, IC, OC1, use_lut != 0);
   if (r0 && r1 && K0 == K1) {
     // one row: both projections in one persistent launch, each with its own
     // plan and workspace, so each output is its own esc_linear call's

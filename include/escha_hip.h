@@ -129,11 +129,14 @@ int esc_gemm_mfma_out(const uint16_t* xh, const uint32_t* code, const float* rou
 /* The whole coded linear, y f16 [M][OC] = (bias +) f16((H128(xh @ W) * rs) *
  * rout) with xh = f16(H128(f32(x) * rin) * rs), x f16 [M][IC], rin f32 [IC],
  * rout f32 [OC], bias f16 [OC] or NULL (added in f32 after the f16 round).
- * M < 16: one launch (in-block input transform; split-K GEMV, packed dot2 on
- * the VALU for one row, for 2..15 rows the rows of a group share each decoded
- * weight on the matrix core; the last split of each column group sums the
- * partials in fixed order and output-transforms); M >= 16: input transform,
- * then esc_gemm_mfma_out.  ws: esc_linear_workspace bytes, zero-filled before its
+ * M < 16: one launch (in-block input transform).  One row: with the table
+ * decode and at least 16,384 units (kt x 256-column groups) the persistent
+ * kernel (one workgroup per CU stages the table once, units split evenly
+ * over its waves), otherwise the split-K GEMV by hash (packed dot2 on the
+ * VALU; the decodes give the same weights); 2..15 rows: split-K, the rows of
+ * a group sharing each decoded weight on the matrix core.  The last split of
+ * each column group sums the partials in fixed order and output-transforms.
+ * M >= 16: input transform, then esc_gemm_mfma_out.  ws: esc_linear_workspace bytes, zero-filled before its
  * first use (its counters are left zero after every call); calls sharing one
  * ws must not overlap.  Tolerance contract (reassociated float32 sum);
  * decoded weights bit-exact.

@@ -1,8 +1,9 @@
 """GPU parity of the one-row persistent projection kernel (k_proj_rows1):
 esc_linear_multi (one to four projections of one row; one projection is
 exactly esc_linear's computation), and esc_linear / esc_linear_pair at M = 1
-where they take it (table decode, at least 6,144 kt x 256-column units)
-(EschaLinear.__call__, escha_mlx/dense.py:337-362).
+where they take it (table decode, at least 16,384 kt x 256-column units;
+smaller projections run the split-K kernel by hash whichever decode is asked
+for) (EschaLinear.__call__, escha_mlx/dense.py:337-362).
 
 Shapes are chosen to exercise the kernel's bookkeeping: one unit per wave
 (small projections), ranges that cross a 128-input block and a column group,
@@ -44,7 +45,7 @@ def ops():
 
 
 SHAPES = [(2, 128, 256), (2, 1024, 4096), (2, 5120, 1280), (2, 4352, 512), (3, 128, 512),
-          (3, 2048, 1024), (3, 4352, 768), (3, 1024, 2816), (2, 8192, 3072)]
+          (3, 2048, 1024), (3, 4352, 768), (3, 1024, 2816), (2, 8192, 3072), (2, 8192, 8192)]
 
 
 @pytest.mark.parametrize("lut", [False, True], ids=["hash", "lut"])
@@ -93,7 +94,7 @@ def test_rows1_vs_f64_and_repeatable(K, ic, oc, lut):
     # esc_linear on the same row: the same computation where it takes this
     # kernel, within the tolerance contract where it takes the split-K one
     single = ops().linear(_dev(x), _code(u32), _dev(rin), _dev(rout), K, ic, oc, lut=lut)
-    if lut and (ic // 16) * (oc // 256) >= 6144:
+    if lut and (ic // 16) * (oc // 256) >= 16384:
         assert torch.equal(single, y)
     s32 = single.cpu().numpy().astype(np.float32)
     assert np.abs(s32 - exact).max() / np.abs(exact).max() < 2e-3
@@ -102,7 +103,8 @@ def test_rows1_vs_f64_and_repeatable(K, ic, oc, lut):
 @pytest.mark.parametrize("lut", [False, True], ids=["hash", "lut"])
 @pytest.mark.parametrize("K,ic,oc0,oc1", [(2, 1024, 256, 1280), (3, 2048, 768, 512),
                                           (2, 8192, 3072, 3072), (3, 6144, 4096, 4096),
-                                          (2, 8192, 3072, 512)])
+                                          (2, 8192, 3072, 512), (2, 8192, 8192, 8192),
+                                          (2, 8192, 8192, 3072)])
 def test_rows1_pair_bit_identical_to_single(K, ic, oc0, oc1, lut):
     rng = np.random.default_rng(ic + oc0 + 7 * oc1)
     o = ops()
