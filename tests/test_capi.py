@@ -94,6 +94,31 @@ def test_workspace_sizes_are_positive():
     assert lib.esc_gemv_fast_workspace(8, 4, 2048, 1024) == 0
 
 
+def test_gemm_mfma_out_workspace_and_rejections():
+    """The fused many-row GEMM needs no workspace when the transform runs in its
+    epilogue (OC a multiple of 256), M * OC float32 otherwise; bad shapes size
+    to 0 and are rejected before any launch, as is a short workspace."""
+    lib = _lib.load()
+    assert lib.esc_gemm_mfma_out_workspace(64, 2, 1024, 2048) == 0
+    assert lib.esc_gemm_mfma_out_workspace(64, 3, 1024, 640) == 64 * 640 * 4
+    assert lib.esc_gemm_mfma_out_workspace(64, 4, 1024, 640) == 0
+    assert lib.esc_gemm_mfma_out_workspace(64, 2, 1000, 640) == 0
+    args = [DUMMY, DUMMY, DUMMY, None, 64, 2, 1024, 640, ctypes.c_float(0.088), DUMMY, DUMMY,
+            64 * 640 * 4, None]
+    bad = list(args)
+    bad[5] = 4
+    rc, msg = _rc_msg("esc_gemm_mfma_out", *bad)
+    assert rc == _lib.ESC_EINVAL and "K=4" in msg
+    bad = list(args)
+    bad[9] = None
+    rc, msg = _rc_msg("esc_gemm_mfma_out", *bad)
+    assert rc == _lib.ESC_EINVAL and "null" in msg
+    bad = list(args)
+    bad[11] = 16
+    rc, msg = _rc_msg("esc_gemm_mfma_out", *bad)
+    assert rc == _lib.ESC_ENOSPACE and "workspace" in msg
+
+
 def test_check_maps_status_to_exceptions():
     with pytest.raises(ValueError):
         _lib.check(_lib.ESC_EINVAL, "x")
