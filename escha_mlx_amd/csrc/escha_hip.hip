@@ -275,10 +275,11 @@ bool rows1_single(int M, int IC, int OC, bool lut) {
   return M == 1 && lut && OC % 256 == 0 && (long)(IC / 16) * (OC / 256) >= kRows1MinUnits;
 }
 // The decode a one-launch linear runs: the table only where the persistent
-// kernel takes it (one row) or for 2..15 rows.
-bool linear_uses_lut(int M, int IC, int OC, bool lut) {
-  return lut && (M != 1 || rows1_single(M, IC, OC, lut));
-}
+// kernel takes it (one row); 2..15 rows run the row-blocked split-K kernel by
+// hash (the table form stages 128 KiB of LDS per workgroup and holds 8 rows:
+// measured on MI355X at 4 rows, K=2 5120 x 5120 21.3 us by hash against
+// 23.7 us, K=3 5120 -> 17408 30.9 against 48.9 us).
+bool linear_uses_lut(int M, int IC, int OC, bool lut) { return rows1_single(M, IC, OC, lut); }
 size_t rows1_part_bytes(int TK, int TN) { return (size_t)(TN / 16) * rows1_maxc(TK) * 256 * 4; }
 
 struct LinearPlan {
@@ -298,16 +299,30 @@ LinearPlan linear_plan(int M, int K, int IC, int OC, bool lut) {
     // the matrix-core multiply each); the table path's LDS holds 8 rows
     p.R = std::min(M, lut ? kLinearSmallRowsLut : kLinearSmallRows - 1);
     p.groups = (TN + tpw - 1) / tpw;
-    p.row_groups = (M + p.R - 1) / p.R;
     const int nb = TK / 8;  // 128-input blocks
-    // fewest splits (largest KS <= 64) that still fill the GPU
-    const int target = lut ? 128 : 256;  // measured best on MI355X for 2048..17408 shapes
-    p.S = nb;
-    for (int S = 1; S <= std::min(nb, 64); ++S) {
-      if (nb % S || 8 * (nb / S) > 64) continue;
-      p.S = S;
-      if (p.groups * p.row_groups * S >= target) break;
-    }
+    // fewest splits (largest KS <= 64) that reach `target` workgroups
+    auto splits = [&](int row_groups, int target) {
+      int best = nb;
+      for (int S = 1; S <= std::min(nb, 64); ++S) {
+        if (nb % S || 8 * (nb / S) > 64) continue;
+        best = S;
+        if (p.groups * row_groups * S >= target) break;
+      }
+      return best;
+    };
+    // Several rows by hash: each split's float32 partials (written and summed
+    // back through the device-coherent level) grow with the rows, so fewer
+    // splits than one row wants; and two row groups when one group at its
+    // fewest splits leaves the GPU short of workgroups (each group decodes
+    // the weights once, the partials halve again).  Measured on MI355X, K=2
+    // 5120 x 5120: 4 rows 21.3 us at 200 workgroups against 23.9 us at 400;
+    // 15 rows 30.9 us as 8 + 7 rows against 36.0 us as one group.
+    if (!lut && M > 1 && p.R > kLinearSmallRowsLut && p.groups * splits(1, 0) < 256)
+      p.R = (M + 1) / 2;
+    p.row_groups = (M + p.R - 1) / p.R;
+    // measured best on MI355X for 2048..17408 shapes
+    const int target = lut ? 128 : M > 1 ? 200 : 256;
+    p.S = splits(p.row_groups, target);
     p.KS = 8 * (nb / p.S);
     // counters first, sized for the most row groups either plan of this M
     // has (the table plan's 8-row groups), so that neither plan's partials
@@ -612,13 +627,11 @@ int esc_linear(const uint16_t* x, const float* rin, const uint32_t* code, const 
     return launch_rows1(a, K, use_lut != 0, s);
   }
   if (M < kLinearSmallRows) {
-    if (use_lut)
-      if (int rc = ensure_lut()) return rc;
+    // the split-K kernel, by hash (linear_uses_lut)
     float* part = reinterpret_cast<float*>(w + lp.off_part);
     int* cnt = reinterpret_cast<int*>(w + lp.off_cnt);
     const esc::LinearSmallArgs a = small_args(x, rin, code, rout, bias, M, TK, TN, lp, rs, part, cnt, y);
-    if (K == 2) return use_lut ? LinearSmallF<2, true>::run(a, s) : LinearSmallF<2, false>::run(a, s);
-    return use_lut ? LinearSmallF<3, true>::run(a, s) : LinearSmallF<3, false>::run(a, s);
+    return K == 2 ? LinearSmallF<2, false>::run(a, s) : LinearSmallF<3, false>::run(a, s);
   }
   // many rows: input transform, then the matrix-core GEMM with the output
   // transform in its epilogue (or GEMM + output transform for OC % 256 != 0)
@@ -685,7 +698,7 @@ int esc_linear_pair(const uint16_t* x, int M, int IC, const float* rin0, const u
   }
   const bool r0 = rows1_single(M, IC, OC0, use_lut != 0), r1 = rows1_single(M, IC, OC1, use_lut != 0);
   // the pair kernel runs the decode each projection's own call would
-  if (!r0 && !r1) use_lut = linear_uses_lut(M, IC, OC0, use_lut != 0);
+  if (!r0 && !r1) use_lut = 0;
   if (use_lut)
     if (int rc = ensure_lut()) return rc;
   const int TK = IC / 16;
@@ -706,8 +719,9 @@ int esc_linear_pair(const uint16_t* x, int M, int IC, const float* rin0, const u
                            reinterpret_cast<int*>(w1 + p1.off_cnt), TK, OC1 / 16};
     return launch_rows1(a, K0, use_lut != 0, S(stream));
   }
-  if (r0 || r1) {
-    // one row, the projections on different kernels (or K): each as its own call
+  if (r0 || r1 || p0.R != p1.R) {
+    // one row with the projections on different kernels (or K), or row
+    // groups of different sizes: each as its own call
     if (int rc = esc_linear(x, rin0, code0, rout0, bias0, M, K0, IC, OC0, use_lut, rs, y0, w, ws0,
                             stream))
       return rc;
@@ -720,8 +734,8 @@ int esc_linear_pair(const uint16_t* x, int M, int IC, const float* rin0, const u
   const esc::LinearSmallArgs a1 =
       small_args(x, rin1, code1, rout1, bias1, M, TK, OC1 / 16, p1, rs,
                  reinterpret_cast<float*>(w1 + p1.off_part), reinterpret_cast<int*>(w1 + p1.off_cnt), y1);
-  return use_lut ? linear_pair_k<true>(K0, K1, a0, a1, S(stream))
-                 : linear_pair_k<false>(K0, K1, a0, a1, S(stream));
+  // the split-K pair kernel, by hash (linear_uses_lut)
+  return linear_pair_k<false>(K0, K1, a0, a1, S(stream));
 }
 
 size_t esc_linear_multi_workspace(int n, int K, int IC, const int* OC) {

@@ -15,8 +15,9 @@
 //      block publishes float32 partials [S][M][OC] with device-coherent stores;
 //   3. the last of the S blocks of a (row group, column group) -- found with
 //      a device-scope counter that it resets to zero -- sums the S partials
-//      in z order (one thread per column, 32 loads in flight at a time),
-//      output-transforms each 128-column block and writes y.
+//      of each (row, column pair) in z order (each thread walks its pairs'
+//      partials 32 loads at a time, so all rows' loads overlap),
+//      output-transforms each (row, 128-column block) and writes y.
 // Deterministic (fixed summation order, no float atomics); tolerance
 // contract like k_gemv_fast (reassociated float32 sum).
 #pragma once
@@ -41,14 +42,15 @@ struct LinearSmallArgs {
 };
 
 // The workgroup's LDS: decode table (table decode only), the transformed
-// inputs of its rows, the VALU path's wave partials, the finishing sums.
+// inputs of its rows (after the decode loop: the finishing sums, [R][TPW*16]
+// floats), the VALU path's wave partials.
 template <int K, bool LUT, int RMAX>
 struct LinearSmallSmem {
   uint16_t lut[LUT ? 65536 : 1];
   alignas(16) uint32_t x[RMAX][8 * 64];  // up to 64 kt per row
   float red[RMAX > 1 ? 1 : 4][64][Geo<K>::NCOL];
-  float sum[2][Geo<K>::TPW * 16];
   int last;
+  static_assert(Geo<K>::TPW * 16 <= 8 * 64, "finishing sums fit in the input stage");
 };
 
 template <int K, bool LUT, int RMAX>
@@ -72,7 +74,6 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
   uint16_t* s_lut = sm.lut;
   auto& s_x = sm.x;
   auto& s_red = sm.red;
-  auto& s_sum = sm.sum;
   int& s_last = sm.last;
   stage_lut<LUT>(s_lut);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -96,16 +97,37 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
   // overlaps the input transform
   LaneWords<K> cur{};
   if (valid) cur = load_lane_words<K>(lp + (size_t)kt0 * kstride);
-  // 1. input transform: xh = f16(H128(f32(x) * rin) * RS) per (row, block)
-  for (int it = wave; it < R * nb; it += 4) {
-    const int r = it / nb, b = it % nb;
-    const int row = min(row0 + r, M - 1);
-    const int cc = 16 * KS * z + 128 * b + 2 * lane;
-    float v0 = (float)__builtin_bit_cast(half_t, x[(size_t)row * IC + cc]) * rin[cc];
-    float v1 = (float)__builtin_bit_cast(half_t, x[(size_t)row * IC + cc + 1]) * rin[cc + 1];
-    h128_wave(v0, v1);
-    const uint32_t pr = pack2(to_f16(v0 * rs), to_f16(v1 * rs));
-    s_x[r][64 * b + lane] = pr;
+  // 1. input transform: xh = f16(H128(f32(x) * rin) * RS) per (row, block);
+  // wave w takes items w, w + 4, ... and requests up to 8 items' inputs
+  // before transforming them, so one memory round trip serves 8 items
+  constexpr int kXB = 8;
+  for (int base = wave; base < R * nb; base += 4 * kXB) {
+    uint16_t xa[kXB], xb[kXB];
+    float ra[kXB], rb[kXB];
+    int r = base / nb, b = base - (base / nb) * nb;
+#pragma unroll
+    for (int j = 0; j < kXB; ++j) {
+      if (base + 4 * j < R * nb) {
+        const int row = min(row0 + r, M - 1);
+        const int cc = 16 * KS * z + 128 * b + 2 * lane;
+        xa[j] = x[(size_t)row * IC + cc];
+        xb[j] = x[(size_t)row * IC + cc + 1];
+        ra[j] = rin[cc];
+        rb[j] = rin[cc + 1];
+      }
+      for (b += 4; b >= nb; b -= nb) ++r;
+    }
+    r = base / nb, b = base - (base / nb) * nb;
+#pragma unroll
+    for (int j = 0; j < kXB; ++j) {
+      if (base + 4 * j < R * nb) {
+        float v0 = (float)__builtin_bit_cast(half_t, xa[j]) * ra[j];
+        float v1 = (float)__builtin_bit_cast(half_t, xb[j]) * rb[j];
+        h128_wave(v0, v1);
+        s_x[r][64 * b + lane] = pack2(to_f16(v0 * rs), to_f16(v1 * rs));
+      }
+      for (b += 4; b >= nb; b -= nb) ++r;
+    }
   }
   __syncthreads();
   // 2. decode + multiply over the block's kt range
@@ -181,51 +203,80 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
   }
   __syncthreads();
   if (!s_last) return;
-  // one thread per column: the splits' partials are requested 32 at a time,
-  // summed in z order, and staged in LDS for the output transform
+  // The group's (row, column pair) items: thread t sums items t, t + 256, ...
+  // walking each item's S partials in z order, 32 loads in flight across its
+  // items, into LDS (over the inputs' stage, unused since the decode loop)
   const int col0 = ntg * kCols;
-  for (int r0 = 0; r0 < R; r0 += 2) {  // two rows per pass
-    for (int rr = 0; rr < 2 && r0 + rr < R; ++rr) {
-      const int row = min(row0 + r0 + rr, M - 1);
-      const int j = threadIdx.x;
-      if (j < kCols && col0 + j < OC) {
-        const float* pb = part + (size_t)row * OC + col0 + j;
-        float v = 0.f;
-        for (int z0 = 0; z0 < S; z0 += 32) {
-          float pv[32];
+  constexpr int kPairs = kCols / 2;
+  const int n_rows = min(R, M - row0);
+  float* s_fin = reinterpret_cast<float*>(&s_x[0][0]);  // [n_rows][kCols]
+  {
+    const int t = threadIdx.x, n_items = n_rows * kPairs;
+    const int T = t < n_items ? ((n_items - 1 - t) / 256 + 1) * S : 0;
+    const size_t zstride = (size_t)M * OC;
+    auto item_ptr = [&](int jj) {
+      const int item = t + 256 * jj, r = item / kPairs, cp = item % kPairs;
+      return part + (size_t)(row0 + r) * OC + col0 + 2 * cp;
+    };
+    auto item_ok = [&](int jj) { return col0 + 2 * ((t + 256 * jj) % kPairs) < OC; };
+    int jl = 0, zl = 0;  // the next load's item and split
+    const float* pl = item_ptr(0);
+    bool okl = item_ok(0);
+    int js = 0, zs = 0;  // the next sum's item and split
+    float sx = 0.f, sy = 0.f;
+    for (int p0 = 0; p0 < T; p0 += 32) {
+      float2 pv[32];
 #pragma unroll
-          for (int zz = 0; zz < 32; ++zz)
-            if (z0 + zz < S)
-              pv[zz] = __builtin_bit_cast(
-                  float, __hip_atomic_load(
-                             reinterpret_cast<const uint32_t*>(pb + (size_t)(z0 + zz) * M * OC),
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-#pragma unroll
-          for (int zz = 0; zz < 32; ++zz)
-            if (z0 + zz < S) v = v + pv[zz];
+      for (int q = 0; q < 32; ++q) {
+        pv[q] = make_float2(0.f, 0.f);
+        if (p0 + q < T) {
+          if (okl) pv[q] = ld_coherent2(pl);
+          pl += zstride;
+          if (++zl == S) {
+            zl = 0;
+            ++jl;
+            pl = item_ptr(jl);
+            okl = item_ok(jl);
+          }
         }
-        s_sum[rr][j] = v;
+      }
+#pragma unroll
+      for (int q = 0; q < 32; ++q) {
+        if (p0 + q < T) {
+          sx = sx + pv[q].x;
+          sy = sy + pv[q].y;
+          if (++zs == S) {
+            const int item = t + 256 * js, r = item / kPairs, cp = item % kPairs;
+            s_fin[r * kCols + 2 * cp] = sx;
+            s_fin[r * kCols + 2 * cp + 1] = sy;
+            sx = 0.f;
+            sy = 0.f;
+            zs = 0;
+            ++js;
+          }
+        }
       }
     }
-    __syncthreads();
-    for (int it = wave; it < 2 * kBlocks; it += 4) {
-      const int rr = it / kBlocks, b = it % kBlocks, r = r0 + rr;
-      const int col = col0 + 128 * b + 2 * lane;
-      if (r >= R || row0 + r >= M || col >= OC) continue;
-      float v0 = s_sum[rr][128 * b + 2 * lane];
-      float v1 = s_sum[rr][128 * b + 2 * lane + 1];
-      h128_wave(v0, v1);
-      half_t y0 = to_f16((v0 * rs) * ro0);  // col == colw
-      half_t y1 = to_f16((v1 * rs) * ro1);
-      if (bias) {
-        y0 = to_f16((float)y0 + bs0);
-        y1 = to_f16((float)y1 + bs1);
-      }
-      uint16_t* yr = y + (size_t)(row0 + r) * OC + col;
-      yr[0] = __builtin_bit_cast(uint16_t, y0);
-      yr[1] = __builtin_bit_cast(uint16_t, y1);
+  }
+  __syncthreads();
+  // one wave per (row, 128-column block); a wave's blocks are all block
+  // wave % kBlocks, whose output scales it requested above
+  for (int it = wave; it < n_rows * kBlocks; it += 4) {
+    const int r = it / kBlocks, b = it % kBlocks;
+    const int col = col0 + 128 * b + 2 * lane;
+    if (col >= OC) continue;
+    float v0 = s_fin[r * kCols + 128 * b + 2 * lane];
+    float v1 = s_fin[r * kCols + 128 * b + 2 * lane + 1];
+    h128_wave(v0, v1);
+    half_t y0 = to_f16((v0 * rs) * ro0);  // col == colw
+    half_t y1 = to_f16((v1 * rs) * ro1);
+    if (bias) {
+      y0 = to_f16((float)y0 + bs0);
+      y1 = to_f16((float)y1 + bs1);
     }
-    __syncthreads();
+    uint16_t* yr = y + (size_t)(row0 + r) * OC + col;
+    yr[0] = __builtin_bit_cast(uint16_t, y0);
+    yr[1] = __builtin_bit_cast(uint16_t, y1);
   }
 }
 

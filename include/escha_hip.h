@@ -133,9 +133,11 @@ int esc_gemm_mfma_out(const uint16_t* xh, const uint32_t* code, const float* rou
  * decode and at least 16,384 units (kt x 256-column groups) the persistent
  * kernel (one workgroup per CU stages the table once, units split evenly
  * over its waves), otherwise the split-K GEMV by hash (packed dot2 on the
- * VALU; the decodes give the same weights); 2..15 rows: split-K, the rows of
- * a group sharing each decoded weight on the matrix core.  The last split of
- * each column group sums the partials in fixed order and output-transforms.
+ * VALU; the decodes give the same weights); 2..15 rows: split-K by hash
+ * whichever decode is asked for, the rows of a group (all rows, or two
+ * groups when one would leave the GPU short of workgroups) sharing each
+ * decoded weight on the matrix core.  The last split of each column group
+ * sums the partials in fixed order and output-transforms.
  * M >= 16: input transform, then esc_gemm_mfma_out.  ws: esc_linear_workspace bytes, zero-filled before its
  * first use (its counters are left zero after every call); calls sharing one
  * ws must not overlap.  Tolerance contract (reassociated float32 sum);

@@ -59,9 +59,13 @@ def _sylvester128():
     return h
 
 
+# 9..15 rows: (2, 1024, 1024, 9), (3, 2048, 384, 13) and (2, 5120, 5120, 15)
+# run as two row groups (one group at its fewest splits would leave the GPU
+# short of workgroups), (3, 4096, 8192, 12) as one group of 12 rows
 @pytest.mark.parametrize("lut", [False, True], ids=["hash", "lut"])
 @pytest.mark.parametrize("K,ic,oc,m", [(2, 2048, 2048, 1), (2, 5120, 640, 3), (3, 1024, 1152, 7),
-                                       (3, 2048, 384, 13), (2, 1024, 1024, 9)])
+                                       (3, 2048, 384, 13), (2, 1024, 1024, 9), (2, 5120, 5120, 4),
+                                       (2, 5120, 5120, 15), (3, 4096, 8192, 12)])
 def test_linear_single_term_bit_exact(K, ic, oc, m, lut):
     rng = np.random.default_rng(100 * K + m)
     u32, rin, rout = _proj(rng, ic, oc, K)
@@ -122,11 +126,11 @@ def test_linear_workspace_shared_by_table_and_hash_calls():
 
 
 def test_linear_workspace_shared_two_row_groups():
-    """9-15 rows: the table plan has two 8-row groups per column group, the hash
-    plan one group of all rows.  With more than 32 column groups (K=2, OC >
-    8192) the hash plan's partials would start inside the table plan's second
-    counter block unless the counter region is sized for both; alternating
-    table and hash calls on one workspace must stay bit-identical."""
+    """9-15 rows: the workspace's counters are sized for two row groups per
+    column group (the hash plan here splits 12 rows into two groups of 6:
+    48 column groups x 5 splits < 256 workgroups).  A request for the table
+    decode runs the same hash plan (the two decodes give the same weights), so
+    alternating requests on one workspace give the same bits."""
     rng = np.random.default_rng(12)
     K, ic, oc, m = 2, 5120, 12288, 12
     u32, rin, rout = _proj(rng, ic, oc, K)
@@ -134,6 +138,7 @@ def test_linear_workspace_shared_two_row_groups():
     ws = torch.zeros(max(ops().linear_workspace(m, K, ic, oc), 4), dtype=torch.uint8, device=DEV)
     args = (_dev(x), _code(u32), _dev(rin), _dev(rout), K, ic, oc)
     fresh = {lut: ops().linear(*args, lut=lut, ws=torch.zeros_like(ws)) for lut in (True, False)}
+    assert torch.equal(fresh[True], fresh[False])
     for _ in range(3):
         for lut in (False, True, False, True):
             assert torch.equal(ops().linear(*args, lut=lut, ws=ws), fresh[lut]), lut

@@ -62,6 +62,25 @@ def test_pair_bit_identical_to_single_linears(K0, K1, m, lut):
         assert torch.equal(z0, s0) and torch.equal(z1, s1)
 
 
+def test_pair_with_different_row_groups_is_two_linears():
+    """12 rows: projection 0 (24 tiles) runs as two row groups of 6, projection
+    1 (K=3, 4096 -> 8192: 64 column groups x 4 splits fill 256 workgroups) as
+    one group of 12; the pair then runs each projection's own call, bit for
+    bit."""
+    rng = np.random.default_rng(4242)
+    ic, m = 4096, 12
+    p0 = _p(rng, ic, 384, 2, True)
+    p1 = _p(rng, ic, 8192, 3, False)
+    x = _dev(rng.standard_normal((m, ic)).astype(np.float16))
+    o = ops()
+    s0 = o.linear(x, p0[0], p0[1], p0[2], 2, ic, 384, bias=p0[5])
+    s1 = o.linear(x, p1[0], p1[1], p1[2], 3, ic, 8192, bias=p1[5])
+    ws = torch.zeros(o.linear_pair_workspace(m, 2, 3, ic, 384, 8192), dtype=torch.uint8, device=DEV)
+    for _ in range(2):
+        y0, y1 = o.linear_pair(x, p0, p1, ws=ws)
+        assert torch.equal(y0, s0) and torch.equal(y1, s1)
+
+
 def _linear_mod(rng, ic, oc, K, bias=None):
     from escha_mlx_amd import dense
     u32, rin, rout = _proj(rng, ic, oc, K)
