@@ -98,9 +98,10 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
   LaneWords<K> cur{};
   if (valid) cur = load_lane_words<K>(lp + (size_t)kt0 * kstride);
   // 1. input transform: xh = f16(H128(f32(x) * rin) * RS) per (row, block);
-  // wave w takes items w, w + 4, ... and requests up to 8 items' inputs
-  // before transforming them, so one memory round trip serves 8 items
-  constexpr int kXB = 8;
+  // wave w takes items w, w + 4, ...; with several rows it requests up to 8
+  // items' inputs before transforming them, so one memory round trip serves
+  // 8 items
+  constexpr int kXB = RMAX > 1 ? 8 : 1;
   for (int base = wave; base < R * nb; base += 4 * kXB) {
     uint16_t xa[kXB], xb[kXB];
     float ra[kXB], rb[kXB];
@@ -203,14 +204,36 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
   }
   __syncthreads();
   if (!s_last) return;
-  // The group's (row, column pair) items: thread t sums items t, t + 256, ...
-  // walking each item's S partials in z order, 32 loads in flight across its
-  // items, into LDS (over the inputs' stage, unused since the decode loop)
+  // The sums go to LDS over the inputs' stage (unused since the decode loop).
+  // Several rows: the group's (row, column pair) items, thread t summing
+  // items t, t + 256, ..., each item's S partials in z order, 32 loads in
+  // flight across its items.
   const int col0 = ntg * kCols;
   constexpr int kPairs = kCols / 2;
   const int n_rows = min(R, M - row0);
   float* s_fin = reinterpret_cast<float*>(&s_x[0][0]);  // [n_rows][kCols]
-  {
+  if constexpr (RMAX == 1) {
+    // one row: one thread per column, its partials 32 at a time
+    const int j = threadIdx.x;
+    if (j < kCols && col0 + j < OC) {
+      const float* pb = part + (size_t)row0 * OC + col0 + j;
+      float v = 0.f;
+      for (int z0 = 0; z0 < S; z0 += 32) {
+        float pv[32];
+#pragma unroll
+        for (int zz = 0; zz < 32; ++zz)
+          if (z0 + zz < S)
+            pv[zz] = __builtin_bit_cast(
+                float, __hip_atomic_load(
+                           reinterpret_cast<const uint32_t*>(pb + (size_t)(z0 + zz) * M * OC),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+#pragma unroll
+        for (int zz = 0; zz < 32; ++zz)
+          if (z0 + zz < S) v = v + pv[zz];
+      }
+      s_fin[j] = v;
+    }
+  } else {
     const int t = threadIdx.x, n_items = n_rows * kPairs;
     const int T = t < n_items ? ((n_items - 1 - t) / 256 + 1) * S : 0;
     const size_t zstride = (size_t)M * OC;
