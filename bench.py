@@ -472,31 +472,27 @@ def c2_setup(torch, copies):
 
 
 def _linear_multi(ops, Ps, x, i, lut):
-    """q, k and v of one input row on copy i: one esc_linear_multi launch."""
+    """q, k and v of the same input rows on copy i: one esc_linear_multi launch."""
     import torch
-    key = ("multi_ws", tuple(id(P) for P in Ps))
+    m = x.shape[0]
+    key = ("multi_ws", m, tuple(id(P) for P in Ps))
     P0 = Ps[0]
     if key not in P0:   # zero-filled once, before any graph capture
         P0[key] = torch.zeros(max(ops.linear_multi_workspace(P0["K"], P0["ic"],
-                                                             [P["oc"] for P in Ps]), 4),
+                                                             [P["oc"] for P in Ps], m), 4),
                               dtype=torch.uint8, device=x.device)
     sel = lambda P: (P["code"][i % len(P["code"])], P["rin"], P["rout"], P["K"], P["oc"], None)
     return tuple(ops.linear_multi(x, [sel(P) for P in Ps], lut=lut, ws=P0[key]))
 
 
 def c2_layer(ops, P, xs, i):
-    """One decoder layer's projections: at one row q, k and v (one input) as
-    one esc_linear_multi launch, then o, up and down; at several rows k and v
-    as one pair launch."""
-    if xs["q"].shape[0] == 1:
-        # one row, the table decode asked for: q+k+v, up and down in
-        # k_proj_rows1 (table mix), o below its size bound in k_linear_small
-        # by hash
-        return (*_linear_multi(ops, [P["q"][0], P["k"][0], P["v"][0]], xs["q"], i, True),
-                *(_linear(ops, P[n][0], xs[n], i, True) for n in ("o", "up", "down")))
-    pk, pv = P["k"][0], P["v"][0]
-    return (*_linear_pair(ops, pk, pv, xs["k"], i, True),
-            *(_linear(ops, P[n][0], xs[n], i, P[n][1]) for n in P if n not in ("k", "v")))
+    """One decoder layer's projections: q, k and v (one input) as one
+    esc_linear_multi launch, then o, up and down.  One row, the table decode
+    asked for: q+k+v, up and down in k_proj_rows1 (table mix), o below its
+    size bound in k_linear_small by hash; several rows: the split-K kernel by
+    hash for each (q+k+v in one k_linear_multi launch)."""
+    return (*_linear_multi(ops, [P["q"][0], P["k"][0], P["v"][0]], xs["q"], i, True),
+            *(_linear(ops, P[n][0], xs[n], i, True) for n in ("o", "up", "down")))
 
 
 def c2_unit(torch, ops):
@@ -766,11 +762,10 @@ def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffi
             fkv = [lambda i=i: _linear_pair(ops, pk, pv, xs["k"], i, True) for i in range(L)]
             per[f"M{M}_kv_pair_us"] = round(graph_time(torch, fkv, args.steps * 5, args.warmup,
                                                        stream, f"M{M} kv pair") * 1e3, 2)
-            if M == 1:
-                pq = [P["q"][0], P["k"][0], P["v"][0]]
-                fm = [lambda i=i: _linear_multi(ops, pq, xs["q"], i, True) for i in range(L)]
-                per["M1_qkv_multi_us"] = round(graph_time(torch, fm, args.steps * 5, args.warmup,
-                                                          stream, "M1 qkv multi") * 1e3, 2)
+            pq = [P["q"][0], P["k"][0], P["v"][0]]
+            fm = [lambda i=i: _linear_multi(ops, pq, xs["q"], i, True) for i in range(L)]
+            per[f"M{M}_qkv_multi_us"] = round(graph_time(torch, fm, args.steps * 5, args.warmup,
+                                                         stream, f"M{M} qkv multi") * 1e3, 2)
             flp = [lambda i=i: c2_layer(ops, P, xs, i) for i in range(L)]
             per[f"M{M}_layer_graph_fused_us"] = round(
                 graph_time(torch, flp, args.steps, args.warmup, stream, f"M{M} layer fused") * 1e3, 2)
@@ -789,8 +784,8 @@ def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffi
                    dtype="u32 codes -> f16 weights (table + hash mix), f32 accumulate",
                    config={"workload": "config 2: 27B-class dense layer, 5120 hidden, M=1 and "
                                        "M=4, the layer's projections replayed as one HIP graph "
-                                       "(M=1: q, k, v as one launch; M=4: k and v as one pair "
-                                       "launch), 8 layer copies rotated (745 MB, cold)"},
+                                       "(q, k, v as one launch), 8 layer copies rotated "
+                                       "(745 MB, cold)"},
                    bytes_per_layer=C2_BYTES, **per,
                    roofline=roofline_block(
                        "hbm", gbs, HBM_PEAK_GBS, "GB/s", tr, tr_detail,

@@ -47,8 +47,8 @@ SIGNATURES = {
     "esc_linear_pair_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),
     "esc_linear_pair": (_I, [_P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I, _F,
                              _P, _P, _P, _Z, _P]),
-    "esc_linear_multi_workspace": (_Z, [_I, _I, _I, _P]),
-    "esc_linear_multi": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _F, _P, _P, _Z, _P]),
+    "esc_linear_multi_workspace": (_Z, [_I, _I, _I, _I, _P]),
+    "esc_linear_multi": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _F, _P, _P, _Z, _P]),
     "esc_gemm_rows_fast_workspace": (_Z, [_I, _I, _I, _I, _I]),
     "esc_gemm_rows_fast_out": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _Z, _P]),
     "esc_build_groups": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),

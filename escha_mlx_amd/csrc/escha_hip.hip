@@ -738,44 +738,94 @@ int esc_linear_pair(const uint16_t* x, int M, int IC, const float* rin0, const u
   return linear_pair_k<false>(K0, K1, a0, a1, S(stream));
 }
 
-size_t esc_linear_multi_workspace(int n, int K, int IC, const int* OC) {
-  if (n < 1 || n > esc::kProjMax || !OC) return 0;
+size_t esc_linear_multi_workspace(int M, int n, int K, int IC, const int* OC) {
+  if (M <= 0 || n < 1 || n > esc::kProjMax || !OC) return 0;
   size_t total = 0;
   for (int i = 0; i < n; ++i) {
-    if (check_proj(K, IC, OC[i]) || OC[i] % 256) return 0;
-    // this projection's counters, then its partials
-    total += ((size_t)(OC[i] / 256) * 4 + 255) / 256 * 256 + rows1_part_bytes(IC / 16, OC[i] / 16);
+    if (check_proj(K, IC, OC[i])) return 0;
+    if (M == 1) {
+      if (OC[i] % 256) return 0;
+      // this projection's counters, then its partials
+      total += ((size_t)(OC[i] / 256) * 4 + 255) / 256 * 256 + rows1_part_bytes(IC / 16, OC[i] / 16);
+    } else {
+      // this projection's esc_linear workspace
+      total += (esc_linear_workspace(M, K, IC, OC[i]) + 255) & ~size_t(255);
+    }
   }
   return total;
 }
 
-int esc_linear_multi(const uint16_t* x, int IC, int K, int n, const uint32_t* const* code,
+int esc_linear_multi(const uint16_t* x, int M, int IC, int K, int n, const uint32_t* const* code,
                      const float* const* rin, const float* const* rout,
                      const uint16_t* const* bias, const int* OC, int use_lut, float rs,
                      uint16_t* const* y, void* ws, size_t ws_bytes, void* stream) {
   ESC_REQUIRE(x && code && rin && rout && OC && y, "null pointer");
+  ESC_REQUIRE(M >= 0, "negative row count");
   ESC_REQUIRE(n >= 1 && n <= esc::kProjMax, "%d projections (1 to %d)", n, esc::kProjMax);
+  static_assert(esc::kLinearMultiMax == esc::kProjMax, "projections per launch");
   for (int i = 0; i < n; ++i) {
     if (int rc = check_proj(K, IC, OC[i])) return rc;
     ESC_REQUIRE(code[i] && rin[i] && rout[i] && y[i], "null pointer (projection %d)", i);
-    ESC_REQUIRE(OC[i] % 256 == 0, "OC=%d of projection %d is not a multiple of 256", OC[i], i);
+    ESC_REQUIRE(M != 1 || OC[i] % 256 == 0, "OC=%d of projection %d is not a multiple of 256",
+                OC[i], i);
   }
-  const size_t need = esc_linear_multi_workspace(n, K, IC, OC);
+  if (M == 0) return ESC_OK;
+  const size_t need = esc_linear_multi_workspace(M, n, K, IC, OC);
   if (!ws || ws_bytes < need)
     return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, need);
-  esc::ProjArgs a{};
-  a.np = n;
-  a.rs = rs;
   char* w = static_cast<char*>(ws);
-  for (int i = 0; i < n; ++i) {
-    int* cnt = reinterpret_cast<int*>(w);
-    w += ((size_t)(OC[i] / 256) * 4 + 255) / 256 * 256;
-    float* part = reinterpret_cast<float*>(w);
-    w += rows1_part_bytes(IC / 16, OC[i] / 16);
-    a.pr[i] = esc::ProjOne{x, rin[i], code[i], rout[i], bias ? bias[i] : nullptr, y[i], part, cnt,
-                           IC / 16, OC[i] / 16};
+  if (M == 1) {
+    // one row: one persistent k_proj_rows1 launch, the units of all
+    // projections split over its waves
+    esc::ProjArgs a{};
+    a.np = n;
+    a.rs = rs;
+    for (int i = 0; i < n; ++i) {
+      int* cnt = reinterpret_cast<int*>(w);
+      w += ((size_t)(OC[i] / 256) * 4 + 255) / 256 * 256;
+      float* part = reinterpret_cast<float*>(w);
+      w += rows1_part_bytes(IC / 16, OC[i] / 16);
+      a.pr[i] = esc::ProjOne{x, rin[i], code[i], rout[i], bias ? bias[i] : nullptr, y[i], part,
+                             cnt, IC / 16, OC[i] / 16};
+    }
+    return launch_rows1(a, K, use_lut != 0, S(stream), true);
   }
-  return launch_rows1(a, K, use_lut != 0, S(stream), true);
+  // several rows: each projection's esc_linear plan and workspace, as one
+  // k_linear_multi launch when all run the split-K kernel with one row group
+  // size, else one call each
+  size_t off[esc::kProjMax];
+  LinearPlan pl[esc::kProjMax];
+  bool one = M < kLinearSmallRows;
+  size_t o = 0;
+  for (int i = 0; i < n; ++i) {
+    off[i] = o;
+    o += (esc_linear_workspace(M, K, IC, OC[i]) + 255) & ~size_t(255);
+    pl[i] = linear_plan(M, K, IC, OC[i], false);
+    one = one && pl[i].R == pl[0].R;
+  }
+  if (!one) {
+    for (int i = 0; i < n; ++i)
+      if (int rc = esc_linear(x, rin[i], code[i], rout[i], bias ? bias[i] : nullptr, M, K, IC,
+                              OC[i], use_lut, rs, y[i], w + off[i], ws_bytes - off[i], stream))
+        return rc;
+    return ESC_OK;
+  }
+  esc::LinearMultiArgs m{};
+  m.n = n;
+  long nw = 0;
+  for (int i = 0; i < n; ++i) {
+    char* wi = w + off[i];
+    m.p[i] = small_args(x, rin[i], code[i], rout[i], bias ? bias[i] : nullptr, M, IC / 16, OC[i] / 16,
+                        pl[i], rs, reinterpret_cast<float*>(wi + pl[i].off_part),
+                        reinterpret_cast<int*>(wi + pl[i].off_cnt), y[i]);
+    nw += (long)pl[i].groups * pl[i].row_groups * pl[i].S;
+  }
+  ESC_REQUIRE(pl[0].R >= 2 && pl[0].R <= kLinearSmallRows, "rows per group %d", pl[0].R);
+  if (K == 2)
+    hipLaunchKernelGGL((esc::k_linear_multi<2, kLinearSmallRows>), dim3(nw), dim3(256), 0, S(stream), m);
+  else
+    hipLaunchKernelGGL((esc::k_linear_multi<3, kLinearSmallRows>), dim3(nw), dim3(256), 0, S(stream), m);
+  return launched("k_linear_multi");
 }
 
 size_t esc_gemm_rows_fast_workspace(int M, int R, int K, int IC, int OC) {

@@ -310,6 +310,32 @@ __global__ __launch_bounds__(256) void k_linear_small(LinearSmallArgs a) {
   linear_small_body<K, LUT, RMAX>(a, blockIdx.x, blockIdx.y, blockIdx.z, sm);
 }
 
+// 1 to 4 projections of the same input rows and K in one launch (an attention
+// block's q, k and v): the flat grid holds projection 0's workgroups, then
+// projection 1's, ..., each running exactly its own single-projection plan
+// (column groups, splits, partials and counters), so each output is
+// bit-identical to its own k_linear_small launch.
+constexpr int kLinearMultiMax = 4;
+struct LinearMultiArgs {
+  LinearSmallArgs p[kLinearMultiMax];
+  int n;
+};
+
+template <int K, int RMAX>
+__global__ __launch_bounds__(256) void k_linear_multi(LinearMultiArgs m) {
+  __shared__ LinearSmallSmem<K, false, RMAX> sm;
+  int b = blockIdx.x, i = 0;
+  for (; i + 1 < m.n; ++i) {
+    const int nw = m.p[i].groups * m.p[i].row_groups * m.p[i].S;
+    if (b < nw) break;
+    b -= nw;
+  }
+  // one body, its arguments chosen per workgroup (as k_linear_pair)
+  const LinearSmallArgs& a = m.p[i];
+  const int gr = a.groups * a.row_groups;
+  linear_small_body<K, false, RMAX>(a, b % a.groups, (b % gr) / a.groups, b / gr, sm);
+}
+
 // Two projections of the same input rows in one launch (the projection-pair
 // dispatch of escha_mlx/dense.py:365-437): the flat grid holds projection
 // 0's workgroups, then projection 1's, each running exactly the single

@@ -227,22 +227,25 @@ def project_pair(first: EschaLinear, second: EschaLinear, x: torch.Tensor):
 
 def project_many(linears, x: torch.Tensor):
     """Several coded projections of the same input (an attention block's q, k
-    and v): [lin(x) for lin in linears].  At one row, with one K, the input
-    width, the latched decode mode and the fused transforms in common and
-    every OC a multiple of 256, the 2 to 4 projections run as one launch
-    (esc_linear_multi), each within the tolerance contract of its own call;
-    otherwise two of them take project_pair and the rest their own calls.  No
-    counterpart in the reference, which fuses projections only for several
-    rows (escha_mlx/dense.py:365-437)."""
+    and v): [lin(x) for lin in linears].  Below 16 rows, with one K, the input
+    width, the latched decode mode and the fused transforms in common (and at
+    one row every OC a multiple of 256), the 2 to 4 projections run as one
+    esc_linear_multi call: at one row one launch, each output within the
+    tolerance contract of its own call; at 2..15 rows one launch where the
+    plans allow, each output bit-identical to its own call.  Otherwise two
+    of them take project_pair and the rest their own calls.  No counterpart
+    in the reference, which pairs two projections for several rows
+    (escha_mlx/dense.py:365-437)."""
     linears = list(linears)
     shape = x.shape
     rows = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
     first = linears[0]
     ws_ = [lin._w for lin in linears]
+    m = rows.shape[0]
     compatible = (
-        2 <= len(linears) <= 4 and rows.shape[0] == 1
+        2 <= len(linears) <= 4 and 1 <= m < 16
         and len({w.K for w in ws_}) == 1 and all(w.IC == rows.shape[-1] for w in ws_)
-        and all(w.OC % 256 == 0 for w in ws_)
+        and (m > 1 or all(w.OC % 256 == 0 for w in ws_))
         and len({lin._lut for lin in linears}) == 1
         and all(lin._fused_had and not lin._exact and lin._block_r_pin is None for lin in linears)
     )
@@ -250,10 +253,10 @@ def project_many(linears, x: torch.Tensor):
         if len(linears) == 2:
             return list(project_pair(linears[0], linears[1], x))
         return [lin(x) for lin in linears]
-    key = (rows.device, tuple(id(lin) for lin in linears[1:]))
+    key = (rows.device, m, tuple(id(lin) for lin in linears[1:]))
     ws = first._multi_ws.get(key)
     if ws is None:
-        need = ops.linear_multi_workspace(ws_[0].K, ws_[0].IC, [w.OC for w in ws_])
+        need = ops.linear_multi_workspace(ws_[0].K, ws_[0].IC, [w.OC for w in ws_], m)
         ws = first._multi_ws[key] = torch.zeros(max(need, 4), dtype=torch.uint8, device=rows.device)
     ys = ops.linear_multi(rows, [(w.code, w.rin, w.rout, w.K, w.OC, lin.bias)
                                  for w, lin in zip(ws_, linears)], lut=first._lut, ws=ws)

@@ -264,32 +264,36 @@ def _ptr_array(ts) -> ctypes.Array:
     return (ctypes.c_void_p * len(ts))(*[_ptr(t) for t in ts])
 
 
-def linear_multi_workspace(K: int, IC: int, OCs) -> int:
+def linear_multi_workspace(K: int, IC: int, OCs, m: int = 1) -> int:
     oc = (ctypes.c_int * len(OCs))(*OCs)
-    return int(_lib.load().esc_linear_multi_workspace(len(OCs), K, IC, oc))
+    return int(_lib.load().esc_linear_multi_workspace(m, len(OCs), K, IC, oc))
 
 
 def linear_multi(x: torch.Tensor, projs, lut: bool | None = None, rs: float = RS,
                  ws: torch.Tensor | None = None):
-    """1 to 4 coded linears of one input row in one launch (M = 1): projs =
-    [(code_u32, rin, rout, K, OC, bias or None), ...] with one K and every OC
-    a multiple of 256; returns the outputs, each within the tolerance contract
-    of ``linear`` on its own.  ws must be zero-filled before its first use."""
+    """1 to 4 coded linears of the same input rows x f16 [m, IC]: projs =
+    [(code_u32, rin, rout, K, OC, bias or None), ...] with one K (every OC a
+    multiple of 256 at one row).  One row: one launch, each output within the
+    tolerance contract of ``linear`` on its own; 2..15 rows: one launch when
+    the projections' plans allow, each output bit-identical to ``linear`` on
+    its own.  ws must be zero-filled before its first use."""
     _dev(x, *[t for p in projs for t in (p[0], p[1], p[2], p[5])])
-    if x.dtype != torch.float16 or x.dim() != 2 or x.shape[0] != 1:
-        raise ValueError("x must be f16 [1, IC]")
-    IC = x.shape[1]
+    if x.dtype != torch.float16 or x.dim() != 2:
+        raise ValueError("x must be f16 [m, IC]")
+    m, IC = x.shape
     Ks = {p[3] for p in projs}
     if len(Ks) != 1:
         raise ValueError(f"projections with different K {sorted(Ks)}")
     K = Ks.pop()
     OCs = [int(p[4]) for p in projs]
-    ys = [torch.empty((1, oc), dtype=torch.float16, device=x.device) for oc in OCs]
-    need = linear_multi_workspace(K, IC, OCs)
+    ys = [torch.empty((m, oc), dtype=torch.float16, device=x.device) for oc in OCs]
+    if m == 0:
+        return ys
+    need = linear_multi_workspace(K, IC, OCs, m)
     if ws is None:
         ws = torch.zeros(max(need, 4), dtype=torch.uint8, device=x.device)
     codes = [_as_u32(p[0]) for p in projs]
-    _lib.call("esc_linear_multi", _ptr(x), IC, K, len(projs), _ptr_array(codes),
+    _lib.call("esc_linear_multi", _ptr(x), m, IC, K, len(projs), _ptr_array(codes),
               _ptr_array([p[1] for p in projs]), _ptr_array([p[2] for p in projs]),
               _ptr_array([p[5] for p in projs]), (ctypes.c_int * len(OCs))(*OCs), _lut_flag(lut),
               rs, _ptr_array(ys), _ptr(ws), ws.numel(), _stream())

@@ -164,20 +164,24 @@ int esc_linear_pair(const uint16_t* x, int M, int IC, const float* rin0, const u
                     int OC1, int use_lut, float rs, uint16_t* y0, uint16_t* y1, void* ws,
                     size_t ws_bytes, void* stream);
 
-/* n (1 to 4) coded linears of one input row in one launch (M = 1):
+/* n (1 to 4) coded linears of the same input rows x f16 [M][IC]:
  * y[i] = esc_linear(x; rin[i], code[i], rout[i], bias[i], K, OC[i]) for the
  * projections of one input (an attention block's q, k and v), all with the
- * same K and every OC[i] a multiple of 256.  code, rin, rout, bias (may be
- * null, or hold nulls), OC and y are host arrays of n entries (device
- * pointers).  The projections share one plan (units per wave from their
- * total), so each output is within the tolerance contract of its own
- * esc_linear call, not bit-identical to it.  ws: esc_linear_multi_workspace
- * bytes, zero-filled before its first use (its counters are left zero).
- * No counterpart in the reference, which computes the three projections as
- * separate EschaLinear calls (escha_mlx/dense.py:337-362) and pairs
- * projections only for several rows (dense.py:365-437). */
-size_t esc_linear_multi_workspace(int n, int K, int IC, const int* OC);
-int esc_linear_multi(const uint16_t* x, int IC, int K, int n, const uint32_t* const* code,
+ * same K.  code, rin, rout, bias (may be null, or hold nulls), OC and y are
+ * host arrays of n entries (device pointers).  One row: every OC[i] a
+ * multiple of 256, one persistent launch whose projections share one plan
+ * (units per wave from their total), so each output is within the tolerance
+ * contract of its own esc_linear call, not bit-identical to it.  2..15 rows:
+ * one split-K launch whose workgroups run each projection's own esc_linear
+ * plan (bit-identical to its own call) when the plans have one row-group
+ * size, else one esc_linear call each; 16 rows and more: one esc_linear call
+ * each.  ws: esc_linear_multi_workspace bytes, zero-filled before its first
+ * use (its counters are left zero).  No counterpart in the reference, which
+ * computes the three projections as separate EschaLinear calls
+ * (escha_mlx/dense.py:337-362) and pairs two projections for several rows
+ * (dense.py:365-437). */
+size_t esc_linear_multi_workspace(int M, int n, int K, int IC, const int* OC);
+int esc_linear_multi(const uint16_t* x, int M, int IC, int K, int n, const uint32_t* const* code,
                      const float* const* rin, const float* const* rout,
                      const uint16_t* const* bias, const int* OC, int use_lut, float rs,
                      uint16_t* const* y, void* ws, size_t ws_bytes, void* stream);

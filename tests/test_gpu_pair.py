@@ -81,6 +81,42 @@ def test_pair_with_different_row_groups_is_two_linears():
         assert torch.equal(y0, s0) and torch.equal(y1, s1)
 
 
+@pytest.mark.parametrize("K", [2, 3])
+@pytest.mark.parametrize("m", [2, 4, 15, 16, 24])
+def test_multi_rows_bit_identical_to_single_linears(K, m):
+    """esc_linear_multi at several rows: q, k and v style projections of one
+    input in one k_linear_multi launch (below 16 rows) or one call each, every
+    output bit-identical to its own esc_linear call; a reused workspace keeps
+    giving the same bits."""
+    rng = np.random.default_rng(500 + 10 * K + m)
+    ic = 1024
+    projs = [_p(rng, ic, 384, K, True), _p(rng, ic, 1280, K, False), _p(rng, ic, 512, K, True)]
+    x = _dev(rng.standard_normal((m, ic)).astype(np.float16))
+    o = ops()
+    want = [o.linear(x, p[0], p[1], p[2], K, ic, p[4], bias=p[5]) for p in projs]
+    ys = o.linear_multi(x, projs)
+    assert all(torch.equal(y, w) for y, w in zip(ys, want))
+    ws = torch.zeros(o.linear_multi_workspace(K, ic, [p[4] for p in projs], m), dtype=torch.uint8,
+                     device=DEV)
+    for _ in range(2):
+        ys = o.linear_multi(x, projs, lut=True, ws=ws)
+        assert all(torch.equal(y, w) for y, w in zip(ys, want))
+
+
+def test_multi_rows_with_different_row_groups_is_separate_linears():
+    """12 rows, K=3: projection 0 (3 column groups) runs as two row groups of
+    6, projection 1 (4096 -> 8192: 64 column groups x 4 splits) as one group
+    of 12, so the call runs each projection's own esc_linear, bit for bit."""
+    rng = np.random.default_rng(4343)
+    ic, m = 4096, 12
+    projs = [_p(rng, ic, 384, 3, True), _p(rng, ic, 8192, 3, False)]
+    x = _dev(rng.standard_normal((m, ic)).astype(np.float16))
+    o = ops()
+    want = [o.linear(x, p[0], p[1], p[2], 3, ic, p[4], bias=p[5]) for p in projs]
+    ys = o.linear_multi(x, projs)
+    assert all(torch.equal(y, w) for y, w in zip(ys, want))
+
+
 def _linear_mod(rng, ic, oc, K, bias=None):
     from escha_mlx_amd import dense
     u32, rin, rout = _proj(rng, ic, oc, K)
@@ -119,9 +155,9 @@ def test_project_pair_and_fused_mlp_vs_oracle(m):
 
 @pytest.mark.parametrize("m", [1, 3])
 def test_project_many_vs_oracle(m):
-    """q, k and v of one input: one launch at one row (within the float16
-    tolerance of the oracle's projections), single calls otherwise
-    (bit-identical to them)."""
+    """q, k and v of one input in one launch: at one row within the float16
+    tolerance of the oracle's projections, at 3 rows also bit-identical to
+    each module's own call."""
     from escha_mlx_amd import dense
     rng = np.random.default_rng(11 + m)
     IC = 1024
