@@ -119,6 +119,40 @@ def test_gemm_mfma_out_workspace_and_rejections():
     assert rc == _lib.ESC_ENOSPACE and "workspace" in msg
 
 
+def test_linear_multi_workspace_and_rejections():
+    """esc_linear_multi's workspace: at one row the persistent kernel's
+    counters and partials (every OC a multiple of 256), at several rows each
+    projection's esc_linear workspace, 256-byte aligned; bad shapes size to 0
+    and are rejected before any launch, as is a short workspace."""
+    lib = _lib.load()
+    oc = lambda *v: (ctypes.c_int * len(v))(*v)
+    al = lambda v: (v + 255) // 256 * 256
+    for m in (2, 4, 15, 24):
+        want = sum(al(lib.esc_linear_workspace(m, 2, 1024, o)) for o in (384, 1280, 512))
+        assert lib.esc_linear_multi_workspace(m, 3, 2, 1024, oc(384, 1280, 512)) == want > 0
+    assert lib.esc_linear_multi_workspace(1, 2, 2, 1024, oc(512, 1280)) > 0
+    assert lib.esc_linear_multi_workspace(1, 2, 2, 1024, oc(512, 384)) == 0   # one row: OC % 256
+    assert lib.esc_linear_multi_workspace(0, 1, 2, 1024, oc(512)) == 0
+    assert lib.esc_linear_multi_workspace(4, 5, 2, 1024, oc(512, 512, 512, 512, 512)) == 0
+    assert lib.esc_linear_multi_workspace(4, 1, 4, 1024, oc(512)) == 0
+    ptrs = lambda n: (ctypes.c_void_p * n)(*([DUMMY] * n))
+    need = lib.esc_linear_multi_workspace(4, 2, 2, 1024, oc(384, 1280))
+    args = [DUMMY, 4, 1024, 2, 2, ptrs(2), ptrs(2), ptrs(2), None, oc(384, 1280), 0,
+            ctypes.c_float(0.088), ptrs(2), DUMMY, need, None]
+    bad = list(args)
+    bad[1] = 1   # one row: OC = 384 is not a multiple of 256
+    rc, msg = _rc_msg("esc_linear_multi", *bad)
+    assert rc == _lib.ESC_EINVAL and "multiple of 256" in msg
+    bad = list(args)
+    bad[4] = 5
+    rc, msg = _rc_msg("esc_linear_multi", *bad)
+    assert rc == _lib.ESC_EINVAL and "projections" in msg
+    bad = list(args)
+    bad[14] = need - 1
+    rc, msg = _rc_msg("esc_linear_multi", *bad)
+    assert rc == _lib.ESC_ENOSPACE and "workspace" in msg
+
+
 def test_check_maps_status_to_exceptions():
     with pytest.raises(ValueError):
         _lib.check(_lib.ESC_EINVAL, "x")
