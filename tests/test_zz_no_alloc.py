@@ -118,3 +118,88 @@ def test_static_expert_path_rejects_oversize():
     y_s, y_r = _both(small)
     assert torch.equal(y_s.view(torch.int16), y_r.view(torch.int16))
     assert ops.moe_expert_path_static_max() == 4 << 20
+
+
+def _args(d, K=2):
+    return (d["x"], d["ids"], d["scores"], d["gu_code"], d["gu_rin"], d["gu_rout"], K,
+            d["dn_code"], d["dn_rin"], d["dn_rout"], K)
+
+
+def test_static_grouped_shape_between_fused_shapes():
+    """More than 64 routed rows at small H and I (E=8, H=512, I=256, 16
+    tokens, top-8: the grouped split-K chain, whose data starts after the
+    counter region) between two calls of the two-launch path and one of the
+    persistent launch, each bit-identical to the workspace entry point."""
+    k = 8
+    fused = _device(_case(256, 2048, 512, 1, k, 910), k)
+    grouped = _device(_case(8, 512, 256, 16, k, 911), k)
+    pers = _device(_case(64, 512, 256, 2, k, 912), k)
+    for name, d in (("two-launch T=1", fused), ("grouped T=16", grouped), ("persistent T=2", pers),
+                    ("grouped again", grouped), ("two-launch again", fused)):
+        y_s, y_r = _both(d)
+        torch.cuda.synchronize()
+        assert not torch.isnan(y_s.float()).any(), name
+        assert torch.equal(y_s.view(torch.int16), y_r.view(torch.int16)), name
+
+
+def test_static_give_up_leaves_later_shapes_exact():
+    """A static call of the persistent launch whose waits give up (spin limit
+    0, forced from the host: no wait runs, every kernel reaches its end)
+    writes NaN and raises the device flag; the next persistent call reports
+    it without running.  Later static calls of the two-launch path and of
+    another persistent shape then match the workspace entry point
+    bit-for-bit: the give-up's status flag is kept outside every shape's
+    counters."""
+    from escha_mlx_amd import _lib, ops
+    k = 8
+    ops.init()
+    pers = _device(_case(64, 512, 256, 2, k, 913), k)
+    two = _device(_case(256, 2048, 512, 1, k, 914), k)
+    pers2 = _device(_case(32, 1024, 256, 3, 4, 915), 4)
+    y = torch.empty((2, 512), dtype=torch.float16, device=DEV)
+    ops.set_moe_spin_limit(0)
+    try:
+        ops.moe_expert_path_static(*_args(pers), out=y)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_moe_spin_limit(-1)
+    assert torch.isnan(y.float()).all()
+    with pytest.raises(_lib.EschaWaitTimeout, match="bounded wait"):
+        ops.moe_expert_path_static(*_args(pers), out=y)
+    for name, d in (("two-launch T=1", two), ("persistent E=32 H=1024 T=3 top-4", pers2),
+                    ("persistent T=2", pers), ("two-launch again", two)):
+        y_s, y_r = _both(d)
+        torch.cuda.synchronize()
+        assert not torch.isnan(y_s.float()).any(), name
+        assert torch.equal(y_s.view(torch.int16), y_r.view(torch.int16)), name
+
+
+@pytest.mark.parametrize("shape", ["two-launch", "persistent"])
+def test_static_expert_path_in_a_captured_graph(shape):
+    """After esc_init, the static call is captured into a HIP graph and
+    replayed three times with eager calls of the workspace entry point in
+    between: every replay is bit-identical to the eager result."""
+    from escha_mlx_amd import ops
+    k = 8
+    ops.init()
+    E, H, I, T = (256, 2048, 512, 1) if shape == "two-launch" else (64, 512, 256, 2)
+    d = _device(_case(E, H, I, T, k, 916), k)
+    other = _device(_case(E, H, I, T, k, 917), k)
+    want = ops.moe_expert_path(*_args(d))
+    y_g = torch.empty((T, H), dtype=torch.float16, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ops.moe_expert_path_static(*_args(d), out=y_g)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.moe_expert_path_static(*_args(d), out=y_g)
+    for i in range(3):
+        y_g.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_g.view(torch.int16), want.view(torch.int16)), f"replay {i}"
+        ops.moe_expert_path(*_args(other))
+        torch.cuda.synchronize()
