@@ -32,6 +32,7 @@ SIGNATURES = {
     "esc_init": (_I, []),
     "esc_decode_tiles": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "esc_input_transform": (_I, [_P, _P, _P, _I, _I, _F, _P, _P]),
+    "esc_input_transform_typed": (_I, [_P, _I, _P, _P, _I, _I, _F, _P, _P]),
     "esc_output_transform": (_I, [_P, _P, _P, _P, _I, _I, _F, _P, _P]),
     "esc_gemv": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "esc_gemv_fast_workspace": (_Z, [_I, _I, _I, _I]),

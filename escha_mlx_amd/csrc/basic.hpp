@@ -97,9 +97,33 @@ __device__ __forceinline__ void h128_wave(float& v0, float& v1) {
 // their loads issued together).  grid (dim/128, ceil(m / kTransformRows)).
 constexpr int kTransformRows = 16;
 
+// Element types of the rows an input transform reads (esc_input_transform_typed).
+enum { kRowsF16 = 0, kRowsBF16 = 1, kRowsF32 = 2 };
+
+// Elements c, c + 1 of a row as float32 (exact for every type).
+template <int DT>
+__device__ __forceinline__ float2 row_pair(const void* rows, size_t i) {
+  if constexpr (DT == kRowsF32) {
+    return *reinterpret_cast<const float2*>(static_cast<const float*>(rows) + i);
+  } else {
+    const uint32_t xv = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(rows) + i);
+    if constexpr (DT == kRowsBF16)
+      return make_float2(__builtin_bit_cast(float, xv << 16),
+                         __builtin_bit_cast(float, xv & 0xFFFF0000u));
+    else
+      return make_float2((float)__builtin_bit_cast(half_t, (uint16_t)xv),
+                         (float)__builtin_bit_cast(half_t, (uint16_t)(xv >> 16)));
+  }
+}
+
 // xh = f16(H128(f32(rows) * rin) * RS); rin is [E][IC] gathered by row_expert,
 // or [IC] when row_expert is null (escha_mlx/msl.py:875-916, 1029-1047).
-__global__ __launch_bounds__(256) void k_input_transform(const uint16_t* __restrict__ rows,
+// DT: the rows' element type; f16 rows are the fused kernel's input, bf16 and
+// f32 rows the reference's unfused branch (escha_mlx/dense.py:290-292,
+// models/qwen3_5_moe.py:108-110), converted exactly to float32 here with no
+// f16 rounding before the transform.
+template <int DT>
+__global__ __launch_bounds__(256) void k_input_transform(const void* __restrict__ rows,
                                                          const float* __restrict__ rin,
                                                          const int* __restrict__ row_expert,
                                                          int m, int IC, float rs,
@@ -112,10 +136,10 @@ __global__ __launch_bounds__(256) void k_input_transform(const uint16_t* __restr
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {
     const int row = min(row0 + j, m - 1);
-    const uint32_t xv = *reinterpret_cast<const uint32_t*>(rows + (size_t)row * IC + c);
+    const float2 xv = row_pair<DT>(rows, (size_t)row * IC + c);
     const float* r = rin + (row_expert ? (size_t)row_expert[row] * IC : 0) + c;
-    v[j][0] = (float)__builtin_bit_cast(half_t, (uint16_t)xv) * r[0];
-    v[j][1] = (float)__builtin_bit_cast(half_t, (uint16_t)(xv >> 16)) * r[1];
+    v[j][0] = xv.x * r[0];
+    v[j][1] = xv.y * r[1];
   }
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {

@@ -533,16 +533,33 @@ int esc_decode_tiles(const uint32_t* code, int K, int IC, int OC, int use_lut, u
   return by_k_lut<DecodeF>(K, use_lut, code, IC, OC, w, S(stream));
 }
 
-int esc_input_transform(const uint16_t* rows, const float* rin, const int32_t* row_expert, int m,
-                        int IC, float rs, uint16_t* out, void* stream) {
+int esc_input_transform_typed(const void* rows, int dtype, const float* rin,
+                              const int32_t* row_expert, int m, int IC, float rs, uint16_t* out,
+                              void* stream) {
   ESC_REQUIRE(rows && rin && out, "null pointer");
   ESC_REQUIRE(IC > 0 && IC % 128 == 0, "Hadamard dimension must be divisible by 128, got %d", IC);
   ESC_REQUIRE(m >= 0, "negative row count");
+  ESC_REQUIRE(dtype == ESC_ROWS_F16 || dtype == ESC_ROWS_BF16 || dtype == ESC_ROWS_F32,
+              "row element type must be ESC_ROWS_F16, ESC_ROWS_BF16 or ESC_ROWS_F32, got %d",
+              dtype);
   if (m == 0) return ESC_OK;
   const int ry = (m + esc::kTransformRows - 1) / esc::kTransformRows;
-  hipLaunchKernelGGL(esc::k_input_transform, dim3(IC / 128, ry), dim3(256), 0, S(stream), rows,
-                     rin, row_expert, m, IC, rs, out);
+  const dim3 grid(IC / 128, ry), blk(256);
+  if (dtype == ESC_ROWS_F16)
+    hipLaunchKernelGGL(esc::k_input_transform<esc::kRowsF16>, grid, blk, 0, S(stream), rows, rin,
+                       row_expert, m, IC, rs, out);
+  else if (dtype == ESC_ROWS_BF16)
+    hipLaunchKernelGGL(esc::k_input_transform<esc::kRowsBF16>, grid, blk, 0, S(stream), rows,
+                       rin, row_expert, m, IC, rs, out);
+  else
+    hipLaunchKernelGGL(esc::k_input_transform<esc::kRowsF32>, grid, blk, 0, S(stream), rows, rin,
+                       row_expert, m, IC, rs, out);
   return launched("k_input_transform");
+}
+
+int esc_input_transform(const uint16_t* rows, const float* rin, const int32_t* row_expert, int m,
+                        int IC, float rs, uint16_t* out, void* stream) {
+  return esc_input_transform_typed(rows, ESC_ROWS_F16, rin, row_expert, m, IC, rs, out, stream);
 }
 
 int esc_output_transform(const float* mid, const float* rout, const int32_t* row_expert,
@@ -1513,12 +1530,18 @@ int moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, 
     // on gfx950; otherwise the single persistent launch
     const bool two = throughput_ok(H, I);
     const FusedPlan f = fused_plan(1, T, top_k, H, I, two, int_region);
-    if (int_region && (size_t)f.n_int * 4 > int_region)
+    // a fixed counter region keeps its last word for the status flag
+    if (int_region && (size_t)f.n_int * 4 > int_region - 4)
       return fail(ESC_ENOSPACE, "%d counters exceed the %zu-byte counter region", f.n_int,
-                  int_region);
+                  int_region - 4);
     if (!ws || ws_bytes < f.total)
       return fail(ESC_ENOSPACE, "workspace %zu bytes < required %zu", ws_bytes, f.total);
     esc::FusedMoe p = fused_args(f, ws, T, top_k, H, I);
+    // Nothing clears the status flag of a fixed counter region (no caller
+    // workspace is read by esc_moe_status): it lives in the region's last
+    // word, outside every shape's counters, so a give-up of one call never
+    // lands in the counters of a later call of another shape.
+    if (int_region) p.status = reinterpret_cast<int*>(static_cast<char*>(ws) + int_region) - 1;
     p.l0 = esc::MoeLayer{x, ids, scores, gu_code, gu_rin, gu_rout, dn_code, dn_rin, dn_rout, y};
     p.layers = nullptr;
     if (two) return launch_fused<true>(p, K_gu, K_dn, f.grid, S(stream));
@@ -1611,6 +1634,13 @@ int ensure_scratch(void** out) {
   *out = g_scratch_ptr[dev];
   return ESC_OK;
 }
+
+bool scratch_ready() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  return g_scratch_ptr[dev] != nullptr;
+}
 }  // namespace
 
 extern "C" {
@@ -1638,6 +1668,16 @@ int esc_moe_expert_path_static(const uint16_t* x, const int32_t* ids, const floa
   if (T == 0) return ESC_OK;
   // the table, when asked for, is built by esc_init (a kernel, no allocation)
   ESC_REQUIRE(!use_lut || lut_ready(), "use_lut needs esc_init() on this device first");
+  // the scratch set-up launches a fill kernel and synchronises, which a
+  // stream under graph capture cannot do: such callers run esc_init first
+  if (!scratch_ready()) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (int rc = hip_check(hipStreamIsCapturing(S(stream), &cs), "hipStreamIsCapturing"))
+      return rc;
+    ESC_REQUIRE(cs == hipStreamCaptureStatusNone,
+                "the static scratch is not set up on this device: call esc_init() before "
+                "capturing esc_moe_expert_path_static");
+  }
   void* ptr = nullptr;
   if (int rc = ensure_scratch(&ptr)) return rc;
   return moe_expert_path(x, ids, scores, T, top_k, E, H, I, gu_code, gu_rin, gu_rout, K_gu,

@@ -155,17 +155,23 @@ class EschaLinear(torch.nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         w = self._w
         shape = x.shape
-        rows = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
+        # f16 rows take the fused transforms; bf16 / f32 rows are transformed
+        # from their float32 values first (dense.py:287-292), then the same
+        # kernels run from xh
+        rows = ops.as_rows(x.reshape(-1, shape[-1]))
         m = rows.shape[0]
-        if (not self._exact and self._block_r_pin is None and self._fused_had
-                and (m < ops.LINEAR_SMALL_ROWS or self._mat)):
+        if (rows.dtype == torch.float16 and not self._exact and self._block_r_pin is None
+                and self._fused_had and (m < ops.LINEAR_SMALL_ROWS or self._mat)):
             # the whole linear in esc_linear (one launch below 16 rows)
             y = ops.linear(rows, w.code, w.rin, w.rout, w.K, w.IC, w.OC, bias=self.bias,
                            lut=self._lut, ws=self._linear_ws(m, rows.device))
             return y.reshape(*shape[:-1], w.OC).to(x.dtype)
         xh = ops.scaled_had(rows, w.rin, None)
         r = dense_block_r(m, self._block_r_pin)
-        if self._mat and r == DENSE_MAT_R:
+        if self._mat and r == DENSE_MAT_R and self._fused_had and not self._exact:
+            # the many-row GEMM with the output transform in its epilogue
+            y = ops.gemm_mfma_out(xh, w.code, w.rout, w.K, w.IC, w.OC)
+        elif self._mat and r == DENSE_MAT_R:
             y = ops.scaled_had_out(ops.dense_gemm_mat(xh, w.code, w.K, w.IC, w.OC), w.rout, None)
         elif not self._fused_had:
             # ESCHA_MLX_FUSED_HAD off: the output transform is its own launch
@@ -202,10 +208,11 @@ def project_pair(first: EschaLinear, second: EschaLinear, x: torch.Tensor):
     is traded for the saved launch."""
     w0, w1 = first._w, second._w
     shape = x.shape
-    rows = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
+    rows = x.reshape(-1, shape[-1]).contiguous()
     m = rows.shape[0]
     compatible = (
-        w0.IC == w1.IC == rows.shape[-1]
+        rows.dtype == torch.float16
+        and w0.IC == w1.IC == rows.shape[-1]
         and first._lut == second._lut
         and first._fused_had and second._fused_had
         and not (first._exact or second._exact)
@@ -238,12 +245,12 @@ def project_many(linears, x: torch.Tensor):
     (escha_mlx/dense.py:365-437)."""
     linears = list(linears)
     shape = x.shape
-    rows = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
+    rows = x.reshape(-1, shape[-1]).contiguous()
     first = linears[0]
     ws_ = [lin._w for lin in linears]
     m = rows.shape[0]
     compatible = (
-        2 <= len(linears) <= 4 and 1 <= m < 16
+        rows.dtype == torch.float16 and 2 <= len(linears) <= 4 and 1 <= m < 16
         and len({w.K for w in ws_}) == 1 and all(w.IC == rows.shape[-1] for w in ws_)
         and (m > 1 or all(w.OC % 256 == 0 for w in ws_))
         and len({lin._lut for lin in linears}) == 1

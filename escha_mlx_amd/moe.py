@@ -128,25 +128,45 @@ class EschaMoEExperts(torch.nn.Module):
                                 m, lut=self._lut)
         return mid[:m].contiguous()
 
-    def _forward_exact(self, x, ids, scores):
+    def _forward_staged(self, x, ids, scores, exact: bool = True):
+        """The chain as separate launches: input transform, GEMV, output
+        transform, SwiGLU, down input transform, GEMV, output transform,
+        combine (models/qwen3_5_moe.py:207-253).  exact: the order-exact
+        GEMVs (bit-reproducible); otherwise split-K GEMVs with the output
+        transform fused (tolerance contract).  x may be f16, bf16 or f32: the
+        first transform reads the rows' exact float32 values."""
         t = x.shape[0]
         row_expert, row_token = self._rows(t, ids)
         gu, dn = self._gu, self._dn
         xh = ops.scaled_had(x[row_token].contiguous(), gu.rin, row_expert)
-        gu16 = ops.scaled_had_out(self._gemv(xh, row_expert, gu), gu.rout, row_expert)
+        if exact:
+            gu16 = ops.scaled_had_out(self._gemv(xh, row_expert, gu), gu.rout, row_expert)
+        else:
+            gu16 = ops.gemv_fast_out(xh, gu.code, row_expert, gu.rout, gu.K, gu.IC, gu.OC,
+                                     lut=self._lut)
         h = ops.swiglu(gu16)
         xh2 = ops.scaled_had(h, dn.rin, row_expert)
-        d16 = ops.scaled_had_out(self._gemv(xh2, row_expert, dn), dn.rout, row_expert)
+        if exact:
+            d16 = ops.scaled_had_out(self._gemv(xh2, row_expert, dn), dn.rout, row_expert)
+        else:
+            d16 = ops.gemv_fast_out(xh2, dn.code, row_expert, dn.rout, dn.K, dn.IC, dn.OC,
+                                    lut=self._lut)
         return ops.moe_combine(d16, scores.reshape(-1).contiguous(), self.top_k)
 
     def forward(self, x: torch.Tensor, ids: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
-        x = x.to(torch.float16).contiguous()
+        """y f16 [T, H], the routed sum rounded to f16 (models/qwen3_5_moe.py:253).
+        x f16 takes the fused expert path; bf16 / f32 rows are transformed from
+        their float32 values (models/qwen3_5_moe.py:103-110), then the staged
+        chain runs."""
+        x = ops.as_rows(x)
         ids = ids.to(torch.int32).contiguous()
         scores = scores.to(torch.float32).contiguous()
+        if x.dtype != torch.float16:
+            return self._forward_staged(x, ids, scores, exact=self._exact)
         if self._exact or not self._fused_had:
             # ESCHA_MLX_FUSED_HAD off: every transform is its own launch around
             # the GEMVs (models/qwen3_5_moe.py:103-122), the staged chain
-            return self._forward_exact(x, ids, scores)
+            return self._forward_staged(x, ids, scores)
         t, h = x.shape
         # one zero-initialised workspace per token count: the one-launch path
         # keeps its counters there and leaves them zero after every call
@@ -198,11 +218,15 @@ class EschaSparseMoeBlock(torch.nn.Module):
         self.sh_down = quant.make_linear(shared["down_w8"], shared["down_scale"], group_size, device)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """out [.., H] in x's dtype.  The routed experts read bf16 / f32 rows
+        unrounded; the router gate and the shared expert (f16 weights, int8
+        w8a16: f16 activations) read the rows rounded to f16."""
         shape = x.shape
-        xf = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
+        rows = ops.as_rows(x.reshape(-1, shape[-1]))
+        xf = rows.to(torch.float16).contiguous()
         logits = ops.gemv_f16w(xf, self.gate_w).to(torch.float32)
         ids, scores = route(logits, self.top_k)
-        y = self.experts(xf, ids, scores)
+        y = self.experts(rows, ids, scores)
         hh = ops.moe_shared_act(self.sh_gate(xf), self.sh_up(xf))
         sh = self.sh_down(hh)
         shg = ops.gemv_f16w(xf, self.shg_w)

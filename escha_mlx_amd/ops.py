@@ -81,17 +81,43 @@ def decode_tiles(code_u32: torch.Tensor, K: int, IC: int, OC: int,
     return w
 
 
+# element type codes of esc_input_transform_typed (ESC_ROWS_* in escha_hip.h)
+ROWS_DTYPES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
 def scaled_had(rows: torch.Tensor, rin: torch.Tensor, row_expert: torch.Tensor | None,
                rs: float = RS) -> torch.Tensor:
     """rows [m, IC] f16, rin [E, IC] f32 (or [IC] with row_expert None) -> [m, IC] f16
-    (msl.py:1029-1047, dense variant msl.py:1481-1483)."""
+    (msl.py:1029-1047, dense variant msl.py:1481-1483).  bf16 and f32 rows are
+    transformed from their exact float32 values, with no f16 rounding first, as
+    the reference's unfused branch does (dense.py:287-292,
+    models/qwen3_5_moe.py:103-110)."""
     _dev(rows, rin, row_expert)
     m, ic = rows.shape
-    _check_rows(rows, torch.float16, rin, row_expert, m, ic)
-    out = torch.empty_like(rows)
-    _lib.call("esc_input_transform", _ptr(rows), _ptr(rin), _ptr(row_expert), m, ic, rs,
-              _ptr(out), _stream())
+    if rows.dtype not in ROWS_DTYPES:
+        raise ValueError(f"rows must be float16, bfloat16 or float32, got {rows.dtype}")
+    _check_rows(rows, rows.dtype, rin, row_expert, m, ic)
+    if not rows.is_contiguous():
+        raise ValueError("rows must be contiguous")
+    out = torch.empty((m, ic), dtype=torch.float16, device=rows.device)
+    if rows.dtype == torch.float16:
+        _lib.call("esc_input_transform", _ptr(rows), _ptr(rin), _ptr(row_expert), m, ic, rs,
+                  _ptr(out), _stream())
+    else:
+        _lib.call("esc_input_transform_typed", _ptr(rows), ROWS_DTYPES[rows.dtype], _ptr(rin),
+                  _ptr(row_expert), m, ic, rs, _ptr(out), _stream())
     return out
+
+
+def as_rows(x2d: torch.Tensor) -> torch.Tensor:
+    """Rows for the input transform: f16, bf16 and f32 as they are; any other
+    floating type converted to float32 (the reference's rows.astype(float32),
+    escha_mlx/dense.py:290); contiguous."""
+    if x2d.dtype not in ROWS_DTYPES:
+        if not x2d.is_floating_point():
+            raise ValueError(f"rows must be floating point, got {x2d.dtype}")
+        x2d = x2d.to(torch.float32)
+    return x2d.contiguous()
 
 
 def scaled_had_out(mid: torch.Tensor, rout: torch.Tensor, row_expert: torch.Tensor | None,

@@ -54,6 +54,21 @@ int esc_decode_tiles(const uint32_t* code, int K, int IC, int OC, int use_lut, u
 int esc_input_transform(const uint16_t* rows, const float* rin, const int32_t* row_expert, int m,
                         int IC, float rs, uint16_t* out, void* stream);
 
+/* Element types of the rows esc_input_transform_typed reads. */
+#define ESC_ROWS_F16 0
+#define ESC_ROWS_BF16 1
+#define ESC_ROWS_F32 2
+
+/* esc_input_transform for rows of another element type: rows [m][IC] of
+ * f16, bf16 or f32 (dtype ESC_ROWS_*), converted exactly to f32 before the
+ * transform (no f16 rounding of the rows), xh f16 [m][IC] out.  f16 rows give
+ * esc_input_transform's result.  Mirrors the reference's transform of
+ * non-f16 rows, xr = rows.astype(f32) * rin; f16(H128(xr) * RS)
+ * (escha_mlx/dense.py:287-292, escha_mlx/models/qwen3_5_moe.py:103-110). */
+int esc_input_transform_typed(const void* rows, int dtype, const float* rin,
+                              const int32_t* row_expert, int m, int IC, float rs, uint16_t* out,
+                              void* stream);
+
 /* y = f16((H128(mid) * RS) * rout[e]) [+ bias f16 [OC], added in f32].
  * Mirrors msl.scaled_had_out / dense_scaled_had_out (escha_mlx/msl.py:1050-1067, 1486-1488)
  * and the bias step of EschaLinear.__call__ (escha_mlx/dense.py:356-361). */
@@ -290,11 +305,15 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  The call itself allocates nothing: the array's device address
  * is looked up and its counter region zeroed by esc_init() (or by the first
- * call on a device).  Shapes whose plan needs more scratch are rejected with
- * ESC_ENOSPACE (T * top_k <= 64 rows at H = 2048, I = 512 fit).  Every call
- * on a GPU shares that GPU's array: calls that overlap on one GPU (concurrent
- * streams, threads) race and must be serialised by the caller.  use_lut needs
- * esc_init() on the device first. */
+ * call on a device, which launches a fill kernel and synchronises: a call on
+ * a stream under graph capture before esc_init() on the device returns
+ * ESC_EINVAL, so capturing callers run esc_init() first).  Shapes whose plan
+ * needs more scratch are rejected with ESC_ENOSPACE (T * top_k <= 64 rows at
+ * H = 2048, I = 512 fit).  Every call on a GPU shares that GPU's array: calls
+ * that overlap on one GPU (concurrent streams, threads) race and must be
+ * serialised by the caller.  The status flag of a bounded wait that gave up
+ * sits in the counter region's last word, outside every shape's counters.
+ * use_lut needs esc_init() on the device first. */
 size_t esc_moe_expert_path_static_max(void);
 int esc_moe_expert_path_static(const uint16_t* x, const int32_t* ids, const float* scores, int T,
                                int top_k, int E, int H, int I, const uint32_t* gu_code,
