@@ -29,11 +29,10 @@
 // else, so that code is in registers by the time the item's inputs are ready.
 //
 // Hand-off across the GPU's XCDs (each has its own L2): partials are written
-// and read with agent-scope monotonic atomics, which the gfx9 memory model
-// keeps coherent device-wide without L2 write-back / invalidate; a producer
-// waits for its stores to complete (s_waitcnt vmcnt(0)) before the counter
-// increment that publishes them, and a consumer reads them only after
-// observing the counter.
+// and read with agent-scope monotonic atomics, which gfx950 performs at the
+// device's coherence point; a producer waits for its stores to complete
+// (s_waitcnt vmcnt(0)) before the counter increment that publishes them, and
+// a consumer reads them only after observing the counter (see add_publish).
 //
 // Forward progress: blocks never wait on a block that has not started.  Every
 // gate_up item is claimed (integer CAS) by the block that runs it; a down item
@@ -56,9 +55,24 @@ namespace esc {
 __device__ __forceinline__ int ld_relaxed(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ int add_relaxed(int* p, int v) {
+// Hand-off counters.  What a producer hands over (partials, f16 rows) it
+// writes with agent-scope atomic stores, which gfx950 performs as
+// write-through stores to the device's coherence point (sc1); the producer
+// waits for them to complete (s_waitcnt vmcnt(0), wait_vm) before the
+// relaxed agent-scope increment that publishes them, which is performed at
+// the same point.  A consumer that sees the count it waits for reads the
+// data with agent-scope atomic loads (sc1, from the coherence point, never a
+// stale L2 line), issued after the count returned; the workgroup-scope
+// acquire fence keeps the compiler from moving them above it (it emits no
+// instruction).  The memory model's release / acquire at agent scope would
+// add an L2 write-back of the XCD (buffer_wbl2 sc1) before every increment
+// and an invalidate (buffer_inv sc1) after every count, for plain stores
+// that these hand-offs do not use: measured on MI355X, 491 against 129 us
+// per many-layer expert call at config 3, so the hand-offs do not take it.
+__device__ __forceinline__ int add_publish(int* p, int v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void after_count() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }
 __device__ __forceinline__ bool claim(int* p) {
   int expected = 0;
   return __hip_atomic_compare_exchange_strong(p, &expected, 1, __ATOMIC_RELAXED,
@@ -262,7 +276,7 @@ __device__ __forceinline__ ItemCode<K, KTB> load_down(const FusedMoe& p, int l, 
 // count gate_up item a of layer l as published (its partials are complete)
 __device__ __forceinline__ void publish_gate_up(const FusedMoe& p, int l, int a) {
   const int rb = a / p.NKC, b = rb % p.NB, r = rb / p.NB;
-  add_relaxed(&p.cntA[(size_t)l * p.T * p.top_k * p.NB + r * p.NB + b], 1);
+  add_publish(&p.cntA[(size_t)l * p.T * p.top_k * p.NB + r * p.NB + b], 1);
 }
 
 // gate_up item a of layer l with its code already in flight: transform the
@@ -430,6 +444,7 @@ __device__ int wait_gate_up(const FusedMoe& p, int l, int r, int kb, int* s_flag
       else if (lane == 63)
         v = 0;
       if (__shfl(v, 0) >= p.NKC) {
+        after_count();
         st = kReady;
         break;
       }
@@ -501,8 +516,11 @@ __global__ __launch_bounds__(64 * NW) void k_moe_gate_up_items(FusedMoe p) {
     const int M = p.T * p.top_k;
     if (tid == 0) {
       int* c = &p.cntA[((size_t)l * M + r) * p.NB + b];
-      const bool last = add_relaxed(c, 1) == p.NKC - 1;
-      if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = add_publish(c, 1) == p.NKC - 1;
+      if (last) {
+        after_count();
+        __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       s_last = last;
     }
     __syncthreads();
@@ -539,8 +557,11 @@ __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_down_items(FusedMoe p)
                         p.partB + ((size_t)l * p.nB + bi) * 256);
   if (tid == 0) {
     int* c = &p.cntB[(size_t)l * p.T * p.NCP + t * p.NCP + cp];
-    const bool last = add_relaxed(c, 1) == p.top_k * p.NKB - 1;
-    if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = add_publish(c, 1) == p.top_k * p.NKB - 1;
+    if (last) {
+      after_count();
+      __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     s_flag = last;
   }
   __syncthreads();
@@ -676,8 +697,11 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down_blocks(FusedMoe p) {
     int last = 0;
     if (lane == 0) {
       int* c = &p.cntB[(size_t)l * p.T * p.NCP + t * p.NCP + hb];
-      last = add_relaxed(c, 1) == p.top_k - 1;
-      if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = add_publish(c, 1) == p.top_k - 1;
+      if (last) {
+        after_count();
+        __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     if (__shfl(last, 0)) {
       float a0 = 0.f, a1 = 0.f;
@@ -773,9 +797,11 @@ __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_fused(FusedMoe p) {
     // a 4-kt item reads the first or second half of its 128-block
     compute_item<KD, KTB>(code, s_x + ((KTB * kb) % 8) * 8, s_red,
                           p.partB + ((size_t)l * p.nB + bi) * 256);
-    if (tid == 0)
-      s_flag = (add_relaxed(&p.cntB[(size_t)l * p.T * p.NCP + t * p.NCP + cp], 1) ==
+    if (tid == 0) {
+      s_flag = (add_publish(&p.cntB[(size_t)l * p.T * p.NCP + t * p.NCP + cp], 1) ==
                 p.top_k * p.NKB - 1);
+      if (s_flag) after_count();
+    }
     __syncthreads();
     const int last = s_flag;
     __syncthreads();
@@ -786,7 +812,10 @@ __global__ __launch_bounds__(kFusedThreads, 4) void k_moe_fused(FusedMoe p) {
   // teardown: the last block resets the integer workspace for the next call
   wait_vm();
   __syncthreads();
-  if (tid == 0) s_flag = (add_relaxed(p.done, 1) == (int)gridDim.x - 1);
+  if (tid == 0) {
+    s_flag = (add_publish(p.done, 1) == (int)gridDim.x - 1);
+    if (s_flag) after_count();
+  }
   __syncthreads();
   if (s_flag) {
     for (int i = tid; i < p.L * M * p.NB; i += kFusedThreads) p.cntA[i] = 0;

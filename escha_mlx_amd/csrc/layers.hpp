@@ -33,10 +33,11 @@
 //     rows of the token in slot order (f16(score) weights, float32 sum, one
 //     f16 rounding) into y.
 //
-// Hand-offs use agent-scope atomics, with a wave's partial stores completed
-// (s_waitcnt) before its increment of the group counter; the finisher resets
-// the counter, so the integer workspace is zero again after every call (it
-// must be zero before the first).  No float atomics: every sum has a fixed
+// Hand-offs use agent-scope atomics (add_publish, fused.hpp), with a wave's
+// partial stores completed (s_waitcnt) before its increment of the group
+// counter; the finisher reads the partials with agent-scope atomic loads
+// after the count and resets the counter, so the integer workspace is zero
+// again after every call (it must be zero before the first).  No float atomics: every sum has a fixed
 // order (items in kc order within a wave, partials in wave order) and the
 // result is deterministic.
 #pragma once
@@ -154,8 +155,11 @@ __device__ __forceinline__ bool publish(const LayersMoe& p, int g, int size, con
   int last = 0;
   if (lane == 0) {
     int* c = reinterpret_cast<int*>(p.ws + p.off_cnt) + g;
-    last = add_relaxed(c, 1) == count - 1;
-    if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = add_publish(c, 1) == count - 1;
+    if (last) {
+      after_count();
+      __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   return __builtin_amdgcn_readfirstlane(last);
 }
@@ -507,8 +511,11 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_dn(LayersMoe p
         if (lane == 0) {
           int* c = reinterpret_cast<int*>(p.ws + p.off_cnt_cb) +
                    ((size_t)it.l * p.T + t) * (p.NHB / 2) + it.cp;
-          last = add_relaxed(c, 1) == p.top_k - 1;
-          if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          last = add_publish(c, 1) == p.top_k - 1;
+          if (last) {
+            after_count();
+            __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
         }
         if (__builtin_amdgcn_readfirstlane(last)) combine_pair(p, it.l, t, it.cp);
       }

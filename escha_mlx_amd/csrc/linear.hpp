@@ -198,8 +198,11 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
   // 3. the last split of (row group, column group) finishes the columns
   if (threadIdx.x == 0) {
     int* cn = &cnt[(size_t)rg * a.groups + ntg];
-    const bool last = add_relaxed(cn, 1) == S - 1;
-    if (last) __hip_atomic_store(cn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = add_publish(cn, 1) == S - 1;
+    if (last) {
+      after_count();
+      __hip_atomic_store(cn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     s_last = last;
   }
   __syncthreads();

@@ -271,8 +271,11 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_proj_rows1(ProjArgs p) {
       int last = 0;
       if (lane == 0) {
         int* cn = q.cnt + g;
-        last = add_relaxed(cn, 1) == count - 1;
-        if (last) __hip_atomic_store(cn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = add_publish(cn, 1) == count - 1;
+        if (last) {
+          after_count();
+          __hip_atomic_store(cn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
       if (!__builtin_amdgcn_readfirstlane(last)) continue;
       // 3. the group's last publisher: partials in workgroup order, 16 in flight

@@ -323,7 +323,7 @@ def test_no_float_atomics_in_kernels():
     allowed = {
         ("basic.hpp", "atomicAdd(&s_cnt[row_expert[r]], 1)"),   # int LDS expert counts
         ("basic.hpp", "atomicAdd(&s_cnt[e], 1)"),
-        ("fused.hpp", "__hip_atomic_fetch_add(p, v,"),          # add_relaxed(int* p, int v)
+        ("fused.hpp", "__hip_atomic_fetch_add(p, v,"),          # add_publish(int* p, int v)
         ("fused.hpp", "__hip_atomic_compare_exchange_strong(p, &expected, 1,"),  # claim(int* p)
         ("fused.hpp", "atomicOr(p.err, 1)"),                      # int flags
         ("fused.hpp", "atomicOr(p.status, 1)"),
@@ -342,7 +342,7 @@ def test_no_float_atomics_in_kernels():
     assert found == allowed, f"listed atomics no longer present: {allowed - found}"
     # the signatures that make the wrapped atomics integer-only
     fused = (csrc / "fused.hpp").read_text()
-    assert "int add_relaxed(int* p, int v)" in fused and "bool claim(int* p)" in fused
+    assert "int add_publish(int* p, int v)" in fused and "bool claim(int* p)" in fused
 
 
 def test_experts_container_validation():
