@@ -406,11 +406,12 @@ def _linear_parts(ops, P, x, i, lut, mat=True):
     return ops.gemv_fast_out(xh, code, None, P["rout"], P["K"], P["ic"], P["oc"], lut=lut)
 
 
-def graph_time(torch, fns, steps: int, warmup: int, stream, name: str = ""):
+def graph_time(torch, fns, steps: int, warmup: int, stream, name: str = "", sink=None):
     """Capture each fn of `fns` in its own HIP graph (one per cold copy), check
     one replay against the eager result, then time `steps` replays in rotation
     (ms per replay).  Graphs hold the launch sequence the host would otherwise
-    re-issue call by call."""
+    re-issue call by call.  `sink` (a dict) receives the graphs and the output
+    tensors each replay writes, for a value check of the timed replays."""
     graphs, outs = [], []
     eager = fns[0]()
     torch.cuda.synchronize()
@@ -435,7 +436,10 @@ def graph_time(torch, fns, steps: int, warmup: int, stream, name: str = ""):
                 d = (a.float() - b.float()).abs()
                 raise SystemExit(f"{name}: graph replay {rep} differs from the eager result: "
                                  f"{int((d > 0).sum())} of {d.numel()} values, max {float(d.max())}")
-    return timed(torch, lambda i: graphs[i % len(graphs)].replay(), steps, warmup, stream)
+    ms = timed(torch, lambda i: graphs[i % len(graphs)].replay(), steps, warmup, stream)
+    if sink is not None:
+        sink.update(graphs=graphs, outs=outs)
+    return ms
 
 
 # ------------------------------------------------------- workload units
@@ -621,6 +625,85 @@ def c1_cpu_and_parity(torch, ops, seconds: float = 8.0):
     return cpu, parity
 
 
+def _host_proj(P, copy: int = 0):
+    """Copy `copy` of a bench projection on the host: (u32 code, rin, rout)."""
+    return (P["code"][copy].cpu().numpy().view(np.uint32), P["rin"].cpu().numpy(),
+            P["rout"].cpu().numpy())
+
+
+def _rel_err(got, want):
+    """max |got - want| and, per row, max |diff| / max |want| (the worst row)."""
+    g, w = got.astype(np.float64), want.astype(np.float64)
+    d = np.abs(g - w)
+    return float(d.max()), float((d.max(axis=1) / np.abs(w).max(axis=1)).max())
+
+
+def c2_parity(torch, P, xs_by_m, outs_by_m):
+    """The outputs of the timed layer graph (copy 0, replayed once more after
+    the timing) against the oracle's expert_linear on the same weights and
+    rows, per projection and batch size."""
+    from oracle import ref_np
+    names = ("q", "k", "v", "o", "up", "down")
+    worst_abs = worst_rel = 0.0
+    per = {}
+    for n in names:
+        pp = P[n][0]
+        u32, rin, rout = _host_proj(pp)
+        w = ref_np.reconstruct(u32, pp["ic"], pp["oc"], pp["K"])
+        for M, outs in outs_by_m.items():
+            x = xs_by_m[M][n].cpu().numpy()
+            want = ref_np.expert_linear(x, u32, rin, rout, pp["K"], w_bare=w)
+            got = outs[names.index(n)].cpu().numpy()
+            a, r = _rel_err(got, want)
+            per[f"M{M}_{n}"] = round(r, 6)
+            worst_abs, worst_rel = max(worst_abs, a), max(worst_rel, r)
+    return {"checked": "the y of the timed layer graph (copy 0 of the 8, replayed once more "
+                       "after timing: q+k+v in one esc_linear_multi launch, o, up, down) at "
+                       "M=1 and M=4 against oracle/ref_np.py expert_linear on the same code, "
+                       "rin, rout and rows",
+            "max_abs_err": worst_abs, "max_row_rel_err": round(worst_rel, 6),
+            "per_projection_row_rel_err": per,
+            "tolerance": "max |diff| / max |oracle| per row < 2e-3 (split-K float32 sums)",
+            "ok": bool(worst_rel < 2e-3)}
+
+
+def c4_parity(recs, want, n_tokens: int = 4):
+    """Rows of the timed call's y (layer-step 0, its first n_tokens tokens)
+    against the oracle's routed block for those tokens (c4_cpu's output)."""
+    got = recs[0]["y"][:n_tokens].cpu().numpy()
+    a = float(np.abs(got.astype(np.float64) - want.astype(np.float64)).max())
+    r = a / float(np.abs(want.astype(np.float64)).max())
+    return {"checked": f"y rows 0-{n_tokens - 1} written by the timed esc_moe_expert_path call "
+                       "of layer-step 0 (k_moe_prep, k_gemv_fast_rows, k_moe_mid, "
+                       "k_moe_combine; every token of the step routed together) against "
+                       "oracle/ref_np.py moe_routed for those tokens",
+            "max_abs_err": a, "max_rel_err": round(r, 6),
+            "tolerance": "max |diff| / max |oracle| < 5e-3 (reassociated float32 sums)",
+            "ok": bool(r < 5e-3)}
+
+
+def c5_parity(torch, up, o, x, y_up, y_o, rows=(0, 1, 1023, 2047)):
+    """Sampled rows of the module's outputs (the timed EschaLinear calls: input
+    transform + esc_gemm_mfma_out) against the oracle's expert_linear on the
+    same weights and rows."""
+    from oracle import ref_np
+    rows = list(rows)
+    xr = x[rows].cpu().numpy()
+    res, worst = {}, 0.0
+    for n, P, y in (("up", up, y_up), ("o", o, y_o)):
+        u32, rin, rout = _host_proj(P)
+        want = ref_np.expert_linear(xr, u32, rin, rout, P["K"])
+        a, r = _rel_err(y[rows].cpu().numpy(), want)
+        res[n] = {"max_abs_err": a, "max_row_rel_err": round(r, 6)}
+        worst = max(worst, r)
+    return {"checked": f"rows {rows} of the timed module pass's outputs (up K3 and o K2: "
+                       "k_input_transform + k_gemm_mma2 with the output transform in its "
+                       "epilogue) against oracle/ref_np.py expert_linear on the same code, "
+                       "rin, rout and rows",
+            **res, "tolerance": "max |diff| / max |oracle| per row < 2e-3 (matrix-core float32 "
+                                "sums)", "ok": bool(worst < 2e-3)}
+
+
 def c2_cpu(seconds: float = 0.0):
     """Config 2's q (K2) and up (K3) projections at batch 1 through the oracle
     (one BLAS thread), each once; GB/s over their coded bytes."""
@@ -669,10 +752,10 @@ def c4_cpu(recs, n_tokens: int = 4):
                "rout": {e: host(R_["gu_rout"], e) for e in used}}
         dnp = {"w": w_dn, "rin": {e: host(R_["dn_rin"], e) for e in used},
                "rout": {e: host(R_["dn_rout"], e) for e in used}}
-        ref_np.moe_routed(x, ids, scores, gup, dnp, K, K, ordered=False)
+        want = ref_np.moe_routed(x, ids, scores, gup, dnp, K, K, ordered=False)
         t = time.perf_counter() - t0
     b = len(used) * (BYTES_GU + BYTES_DN)
-    return {"value": round(b / t / 1e9, 4), "unit": "GB/s", "cores": 1, **host_cpus(),
+    return want, {"value": round(b / t / 1e9, 4), "unit": "GB/s", "cores": 1, **host_cpus(),
             "kind": "port",
             "sample": f"layer-step 0's first {n_tokens} tokens ({len(used)} distinct experts) "
                       f"through oracle/ref_np.py moe_routed (decode every expert, f32 matmul): "
@@ -737,9 +820,10 @@ def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffi
     if cfg == 2:
         L = 8   # 8 layer copies x 93 MB = 745 MB rotated
         P, g = c2_setup(torch, L)
-        per = {}
+        per, xs_by_m, outs_by_m = {}, {}, {}
         for M in (1, 4):
             xs = {n: torch.randn(M, P[n][0]["ic"], generator=g, device=dev).half() for n in P}
+            xs_by_m[M] = xs
             t_layer = 0.0
             for n, (pp, lut) in P.items():
                 fns = [lambda i=i, pp=pp, lut=lut, n=n: (_linear(ops, pp, xs[n], i, lut),)
@@ -767,8 +851,13 @@ def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffi
             per[f"M{M}_qkv_multi_us"] = round(graph_time(torch, fm, args.steps * 5, args.warmup,
                                                          stream, f"M{M} qkv multi") * 1e3, 2)
             flp = [lambda i=i: c2_layer(ops, P, xs, i) for i in range(L)]
+            sink = {}
             per[f"M{M}_layer_graph_fused_us"] = round(
-                graph_time(torch, flp, args.steps, args.warmup, stream, f"M{M} layer fused") * 1e3, 2)
+                graph_time(torch, flp, args.steps, args.warmup, stream, f"M{M} layer fused",
+                           sink) * 1e3, 2)
+            sink["graphs"][0].replay()
+            torch.cuda.synchronize()
+            outs_by_m[M] = tuple(t.clone() for t in sink["outs"][0])
             per[f"M{M}_layer_us"] = round(t_layer * 1e3, 2)
             per[f"M{M}_layer_gbs"] = round(C2_BYTES / (t_layer * 1e-3) / 1e9, 1)
             per[f"M{M}_tok_s_per_layer"] = round(M / (t_layer * 1e-3), 1)
@@ -795,6 +884,7 @@ def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffi
                        avg_layer_us=us_layer))
         if not args.no_cpu:
             res["cpu_baseline"] = c2_cpu()
+            res["parity"] = c2_parity(torch, P, xs_by_m, outs_by_m)
         return res
     if cfg == 5:
         up, o, x = c5_setup(torch)
@@ -810,8 +900,12 @@ def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffi
         ms_go = timed(torch, lambda i: ops.gemm_mfma_out(xh_o, o["code"][0], o["rout"], 2, 5120,
                                                          5120),
                       args.steps, args.warmup, stream)
-        ms_mod = timed(torch, lambda i: (_linear(ops, up, x, i, False), _linear(ops, o, x, i, False)),
-                       args.steps, args.warmup, stream)
+        last = {}
+
+        def module(i):
+            last["y"] = (_linear(ops, up, x, i, False), _linear(ops, o, x, i, False))
+
+        ms_mod = timed(torch, module, args.steps, args.warmup, stream)
         tf_k = flop / ((ms_gu + ms_go) * 1e-3) / 1e12
         res.update(metric="prefill TFLOP/s, 2048 tokens through coded up (K3) + o (K2)",
                    value=round(flop / (ms_mod * 1e-3) / 1e12, 2), unit="TFLOP/s",
@@ -830,6 +924,7 @@ def bench_dense(args, torch, ops, cfg, traffic=(None, "not measured (--no-traffi
                        flop_per_launch_pair=flop))
         if not args.no_cpu:
             res["cpu_baseline"] = c5_cpu()
+            res["parity"] = c5_parity(torch, up, o, x, *last["y"])
         return res
     raise SystemExit(f"config {cfg}: not measured by this bench")
 
@@ -856,7 +951,8 @@ def bench_c4(args, torch, ops, traffic=(None, "not measured (--no-traffic)")):
                "k_moe_combine, one esc_moe_expert_path call per layer-step",
                bytes_per_step=int(b), avg_step_us=round(ms * 1e3, 2))}
     if not args.no_cpu:
-        res["cpu_baseline"] = c4_cpu(recs)
+        want, res["cpu_baseline"] = c4_cpu(recs)
+        res["parity"] = c4_parity(recs, want)
     return res
 
 

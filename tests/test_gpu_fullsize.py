@@ -27,6 +27,7 @@ import torch
 from oracle import ref_np as R
 
 from .conftest import has_gpu
+from .test_gpu_linear import _sylvester128
 from .test_gpu_parity import _block, _moe_case, _oracle_moe
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not has_gpu(), reason="needs a ROCm GPU")]
@@ -50,7 +51,7 @@ def _dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
 
 
-@lru_cache(maxsize=2)
+@lru_cache(maxsize=4)
 def _projection(ic, oc, K, seed):
     """Seeded code stream, signs and scales of one projection, plus the
     oracle's decoded weight (float16, ic x oc)."""
@@ -61,23 +62,94 @@ def _projection(ic, oc, K, seed):
     return u32, rin, rout, R.reconstruct(u32, ic, oc, K)
 
 
+def _single_term_row(ic, rin, k):
+    """x [1, ic] f16 whose input transform leaves only input k non-zero: the
+    Sylvester column of k scaled by rin over k's 128-input block."""
+    hs = _sylvester128()
+    blk = 128 * (k // 128)
+    x = np.zeros((1, ic), np.float32)
+    x[0, blk:blk + 128] = hs[:, k % 128] * rin[blk:blk + 128]
+    return x.astype(np.float16)
+
+
+def _single_term_want(x16, rin, rout, w, k):
+    xh = R.input_transform(x16, rin)
+    assert np.count_nonzero(xh[0]) == 1 and xh[0, k] != 0
+    mid = (xh[0, k].astype(np.float32) * w[k].astype(np.float32))[None]
+    return R.output_transform(mid, rout)[0]
+
+
+@pytest.mark.parametrize("lut", [False, True], ids=["hash", "lut"])
 @pytest.mark.parametrize("ic,oc", [(5120, 17408), (17408, 5120)], ids=["up", "down"])
 @pytest.mark.parametrize("m", [1, 4])
-def test_config2_mlp_projection_full_size_vs_oracle(ic, oc, m):
+def test_config2_mlp_projection_full_size_vs_oracle(ic, oc, m, lut):
+    """Config 2's up and down projections (K=3) through esc_linear at batch 1
+    and 4.  At one row with the table decode this is the persistent one-row
+    kernel's 21,760-unit plan (5-6 units per wave), the kernel the config 2
+    bench line times; by hash, and at 4 rows, the split-K kernel.  Single-term
+    rows are bit-exact at one row; random rows within 2e-3 of each row's max
+    against the float64 product, bit-identical on repeat calls."""
     K = 3
     u32, rin, rout, w = _projection(ic, oc, K, 2)
     rng = np.random.default_rng(ic + m)
     x = rng.standard_normal((m, ic)).astype(np.float16)
     ws = torch.zeros(max(ops().linear_workspace(m, K, ic, oc), 4), dtype=torch.uint8, device=DEV)
-    args = (_dev(x), _dev(u32.view(np.int32)), _dev(rin), _dev(rout), K, ic, oc)
-    y = ops().linear(*args, lut=False, ws=ws)
+    code, d_rin, d_rout = _dev(u32.view(np.int32)), _dev(rin), _dev(rout)
+    y = ops().linear(_dev(x), code, d_rin, d_rout, K, ic, oc, lut=lut, ws=ws)
     xh = R.input_transform(x, rin)
     exact = R.h128((xh.astype(np.float64) @ w.astype(np.float64)).astype(np.float32)) * R.RS * rout
     got = y.cpu().numpy().astype(np.float32)
     err = (np.abs(got - exact).max(axis=1) / np.abs(exact).max(axis=1)).max()
-    print(f"{ic}->{oc} m={m}: max row |diff| / max |f64| = {err:.2e}")
+    print(f"{ic}->{oc} m={m} lut={lut}: max row |diff| / max |f64| = {err:.2e}")
     assert err < 2e-3, err
-    assert torch.equal(ops().linear(*args, lut=False, ws=ws), y)
+    assert torch.equal(ops().linear(_dev(x), code, d_rin, d_rout, K, ic, oc, lut=lut, ws=ws), y)
+    if m == 1:
+        for k in (0, ic - 1, int(rng.integers(0, ic))):
+            x16 = _single_term_row(ic, rin, k)
+            y1 = ops().linear(_dev(x16), code, d_rin, d_rout, K, ic, oc, lut=lut, ws=ws)
+            want = _single_term_want(x16, rin, rout, w, k)
+            assert np.array_equal(y1.cpu().numpy()[0].view(np.uint16), want.view(np.uint16)), k
+
+
+@pytest.mark.parametrize("lut", [False, True], ids=["hash", "lut"])
+@pytest.mark.parametrize("m", [1, 4])
+def test_config2_qkv_multi_full_size_vs_oracle(m, lut):
+    """Config 2's q, k and v (3 x 5120 x 5120, K=2) as the one esc_linear_multi
+    launch the bench line times: at one row the persistent kernel with one
+    plan shared by the three projections (19,200 units), at 4 rows the
+    split-K multi launch.  Single-term rows: every projection bit-exact at
+    one row, and each output of the 4-row launch bit-identical to its own
+    esc_linear call.  Random rows: within 2e-3 of each row's max against the
+    float64 product, bit-identical on repeat calls over one workspace."""
+    ic, K = 5120, 2
+    projs = [_projection(ic, ic, K, 20 + j) for j in range(3)]
+    dproj = [(_dev(u.view(np.int32)), _dev(ri), _dev(ro), K, ic, None) for u, ri, ro, _ in projs]
+    o = ops()
+    ws = torch.zeros(o.linear_multi_workspace(K, ic, [ic] * 3, m=m), dtype=torch.uint8, device=DEV)
+    rng = np.random.default_rng(77 + m)
+    if m == 1:
+        k = int(rng.integers(0, ic))
+        for j, (u32, rin, rout, w) in enumerate(projs):
+            x16 = _single_term_row(ic, rin, k)
+            ys = o.linear_multi(_dev(x16), dproj, lut=lut, ws=ws)
+            want = _single_term_want(x16, rin, rout, w, k)
+            assert np.array_equal(ys[j].cpu().numpy()[0].view(np.uint16), want.view(np.uint16)), j
+    x = rng.standard_normal((m, ic)).astype(np.float16)
+    ys = o.linear_multi(_dev(x), dproj, lut=lut, ws=ws)
+    worst = 0.0
+    for (u32, rin, rout, w), y in zip(projs, ys):
+        xh = R.input_transform(x, rin)
+        exact = R.h128((xh.astype(np.float64) @ w.astype(np.float64)).astype(np.float32)) * R.RS * rout
+        got = y.cpu().numpy().astype(np.float32)
+        err = (np.abs(got - exact).max(axis=1) / np.abs(exact).max(axis=1)).max()
+        worst = max(worst, err)
+        assert err < 2e-3, err
+    print(f"q,k,v multi m={m} lut={lut}: max row |diff| / max |f64| = {worst:.2e}")
+    again = o.linear_multi(_dev(x), dproj, lut=lut, ws=ws)
+    assert all(torch.equal(a, b) for a, b in zip(again, ys))
+    if m > 1:
+        for (c, ri, ro, _, _, _), y in zip(dproj, ys):
+            assert torch.equal(o.linear(_dev(x), c, ri, ro, K, ic, ic, lut=lut), y)
 
 
 @pytest.mark.parametrize("ic,oc,K", [(5120, 17408, 3), (5120, 5120, 2)], ids=["up", "o"])
