@@ -333,6 +333,21 @@ def probe(torch, args):
         return
     layers = make_layers(torch, args.layers, dev)
     routes = route_sets(torch, layers)
+    if args.only == "chained":
+        # two chained decode steps: 2 x 40 esc_moe_expert_path calls
+        ws = torch.zeros(ops.moe_expert_path_workspace(1, TOP_K, E, H, I), dtype=torch.uint8,
+                         device=dev)
+        for s in range(2):
+            x = layers[0]["x"]
+            for L in routes[s]:
+                ops.moe_expert_path(x, L["ids"], L["scores"], L["gu_code"], L["gu_rin"],
+                                    L["gu_rout"], K, L["dn_code"], L["dn_rin"], L["dn_rout"], K,
+                                    ws=ws, out=L["y"])
+                x = L["y"]
+        torch.cuda.synchronize()
+        print(f"probe: copy {COPY_BYTES} B, 2 chained steps x {args.layers} token-layers",
+              flush=True)
+        return
     ws = torch.zeros(ops.moe_layers_workspace(args.layers, 1, TOP_K, H, I), dtype=torch.uint8,
                      device=dev)
     for s in range(2):
@@ -651,7 +666,8 @@ def c2_parity(torch, P, xs_by_m, outs_by_m):
         u32, rin, rout = _host_proj(pp)
         w = ref_np.reconstruct(u32, pp["ic"], pp["oc"], pp["K"])
         for M, outs in outs_by_m.items():
-            x = xs_by_m[M][n].cpu().numpy()
+            # q, k and v read the same rows (one esc_linear_multi launch)
+            x = xs_by_m[M]["q" if n in ("k", "v") else n].cpu().numpy()
             want = ref_np.expert_linear(x, u32, rin, rout, pp["K"], w_bare=w)
             got = outs[names.index(n)].cpu().numpy()
             a, r = _rel_err(got, want)
