@@ -49,6 +49,7 @@ BYTES_DN = I * H * K // 8              # 262,144 per expert
 BYTES_TOKEN_LAYER = TOP_K * (BYTES_GU + BYTES_DN)   # 6,291,456
 HBM_PEAK_GBS = 8000.0
 ROUTE_SETS = 4
+STEADY_WARMUP, STEADY_STEPS = 300, 100  # the steady-clock figure beside a short run's value
 COPY_BYTES = 1 << 30                   # counter calibration copy
 KERNELS = ("k_moe_layers_gu", "k_moe_layers_dn")
 SUSTAINED_KERNELS = ("k_moe_layers_gu + k_moe_layers_dn (slot combine in the down kernel; "
@@ -1190,6 +1191,19 @@ def main():
                          "bytes_per_launch": bytes_call,
                          "avg_launch_us": round(ms * 1e3, 2)},
         })
+
+    if args.only in ("both", "sustained") and args.warmup < STEADY_WARMUP:
+        # The same call at the GPU's steady clock, beside the line: the clock
+        # dips below its starting level for the first few ms of full load and
+        # settles after tens of ms (per-call times of one box after an idle
+        # second: calls 1-5 147.5 us, calls 10-30 160-177 us, calls 200-299
+        # 130-134 us).  Not the line's value, which keeps the flags' warm-up.
+        ms_s = timed(torch, sustained, STEADY_STEPS, STEADY_WARMUP, stream)
+        result["steady_clock"] = {
+            "gbs": round(BYTES_TOKEN_LAYER * nl / (ms_s * 1e-3) / 1e9, 2),
+            "us_per_call": round(ms_s * 1e3, 2),
+            "how": f"after the timed calls, {STEADY_WARMUP} more untimed calls, then "
+                   f"{STEADY_STEPS} timed (HIP events); reported beside value, not as it"}
 
     if args.only in ("both", "chained"):
         ws = torch.zeros(ops.moe_expert_path_workspace(1, TOP_K, E, H, I), dtype=torch.uint8,

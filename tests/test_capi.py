@@ -407,3 +407,22 @@ def test_linear_pair_rejections_and_workspace():
     bad[20] = 16
     rc, msg = _rc_msg("esc_linear_pair", *bad)
     assert rc == _lib.ESC_ENOSPACE and "workspace" in msg
+
+
+def test_input_transform_typed_rejections():
+    """esc_input_transform_typed: an unknown row type, a width that is not a
+    multiple of 128 and null pointers are refused before any HIP call; the
+    Python wrapper refuses non-float rows."""
+    rc, msg = _rc_msg("esc_input_transform_typed", DUMMY, 3, DUMMY, None, 4, 128, ctypes.c_float(1.0),
+                      DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "row element type" in msg
+    rc, msg = _rc_msg("esc_input_transform_typed", DUMMY, 2, DUMMY, None, 4, 100, ctypes.c_float(1.0),
+                      DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "divisible by 128" in msg
+    rc, msg = _rc_msg("esc_input_transform_typed", None, 1, DUMMY, None, 4, 128, ctypes.c_float(1.0),
+                      DUMMY, None)
+    assert rc == _lib.ESC_EINVAL and "null" in msg
+    assert ops.ROWS_DTYPES == {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+    with pytest.raises(ValueError, match="floating point"):
+        ops.as_rows(torch.zeros((2, 128), dtype=torch.int32))
+    assert ops.as_rows(torch.zeros((2, 128), dtype=torch.float64)).dtype == torch.float32
