@@ -72,6 +72,20 @@ __device__ __forceinline__ LaneWords<K> load_lane_words(const uint32_t* p) {
   return r;
 }
 
+// The same words through the streaming (non-temporal) path: for code that a
+// call reads once, so it does not push the inputs, scales and partials that
+// the call reads again out of the L2.
+typedef uint32_t nt_u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ LaneWords<2> load_lane_words_nt(const uint32_t* p) {
+  const nt_u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4_t*>(p));
+  LaneWords<2> r;
+  r.w[0] = v.x;
+  r.w[1] = v.y;
+  r.w[2] = v.z;
+  r.w[3] = v.w;
+  return r;
+}
+
 // Decode the lane's SPL steps of one tile and accumulate x * w into acc[NCOL].
 // xw: the 16 f16 inputs of this kt packed two per word (row r in half r&1 of
 // word r>>1).  wprev: the previous lane's last word.
