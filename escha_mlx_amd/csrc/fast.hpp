@@ -76,13 +76,20 @@ __device__ __forceinline__ LaneWords<K> load_lane_words(const uint32_t* p) {
 // call reads once, so it does not push the inputs, scales and partials that
 // the call reads again out of the L2.
 typedef uint32_t nt_u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ LaneWords<2> load_lane_words_nt(const uint32_t* p) {
-  const nt_u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4_t*>(p));
-  LaneWords<2> r;
-  r.w[0] = v.x;
-  r.w[1] = v.y;
-  r.w[2] = v.z;
-  r.w[3] = v.w;
+template <int K = 2>
+__device__ __forceinline__ LaneWords<K> load_lane_words_nt(const uint32_t* p) {
+  LaneWords<K> r;
+  if constexpr (K == 2) {
+    const nt_u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4_t*>(p));
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+    r.w[2] = v.z;
+    r.w[3] = v.w;
+  } else {
+    r.w[0] = __builtin_nontemporal_load(p);
+    r.w[1] = __builtin_nontemporal_load(p + 1);
+    r.w[2] = __builtin_nontemporal_load(p + 2);
+  }
   return r;
 }
 
@@ -564,14 +571,14 @@ __device__ __forceinline__ void rows_mma_accum(const uint16_t* __restrict__ xh,
   const int kt0 = z * KS + gk, nsteps = KS / 4;
 #pragma unroll
   for (int i = 0; i < G::NCOL; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  LaneWords<K> cur = load_lane_words<K>(lp + (size_t)kt0 * kstride);
+  LaneWords<K> cur = load_lane_words_nt<K>(lp + (size_t)kt0 * kstride);
   uint4 xa = xq[2 * kt0], xb = xq[2 * kt0 + 1];
   for (int k = 0; k < nsteps; ++k) {
     LaneWords<K> nxt = cur;
     uint4 na = xa, nb = xb;
     if (k + 1 < nsteps) {
       const int kt = kt0 + 4 * (k + 1);
-      nxt = load_lane_words<K>(lp + (size_t)kt * kstride);
+      nxt = load_lane_words_nt<K>(lp + (size_t)kt * kstride);
       na = xq[2 * kt];
       nb = xq[2 * kt + 1];
     }
@@ -655,12 +662,12 @@ __global__ __launch_bounds__(256) void k_gemv_fast(const uint16_t* __restrict__ 
   for (int i = 0; i < G::NCOL; ++i) acc[i] = 0.f;
   const size_t lane_off = (size_t)ntg * G::TPW * (8 * K) + (size_t)lane * G::WPL;
   LaneWords<K> zero{};
-  LaneWords<K> cur = valid ? load_lane_words<K>(base + (size_t)kt0 * TN * (8 * K) + lane_off) : zero;
+  LaneWords<K> cur = valid ? load_lane_words_nt<K>(base + (size_t)kt0 * TN * (8 * K) + lane_off) : zero;
   for (int k = 0; k < KW; ++k) {
     const int kt = kt0 + k;
     LaneWords<K> nxt = cur;
     if (valid && k + 1 < KW)
-      nxt = load_lane_words<K>(base + (size_t)(kt + 1) * TN * (8 * K) + lane_off);
+      nxt = load_lane_words_nt<K>(base + (size_t)(kt + 1) * TN * (8 * K) + lane_off);
     uint32_t xw[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) xw[i] = xrow[8 * kt + i];

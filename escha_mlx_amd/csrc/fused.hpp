@@ -170,7 +170,7 @@ __device__ __forceinline__ ItemCode<K, NKT, NW> load_item(const uint32_t* __rest
                        (size_t)(kt_base + wi * IG::NSTEP) * kstride;
   ItemCode<K, NKT, NW> c;
 #pragma unroll
-  for (int k = 0; k < IG::NSTEP; ++k) c.w[k] = load_lane_words<K>(lp + (size_t)k * kstride);
+  for (int k = 0; k < IG::NSTEP; ++k) c.w[k] = load_lane_words_nt<K>(lp + (size_t)k * kstride);
   return c;
 }
 
@@ -599,7 +599,7 @@ __device__ __forceinline__ BlockCode<K, NW> load_block_item(const uint32_t* __re
   BlockCode<K, NW> c;
 #pragma unroll
   for (int k = 0; k < BI::NSTEP; ++k)
-    c.w[k] = load_lane_words<K>(lp + (size_t)(k * BI::KPS) * kstride);
+    c.w[k] = load_lane_words_nt<K>(lp + (size_t)(k * BI::KPS) * kstride);
   return c;
 }
 

@@ -96,7 +96,7 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
   // the first step's code is requested before anything else, so its latency
   // overlaps the input transform
   LaneWords<K> cur{};
-  if (valid) cur = load_lane_words<K>(lp + (size_t)kt0 * kstride);
+  if (valid) cur = load_lane_words_nt<K>(lp + (size_t)kt0 * kstride);
   // 1. input transform: xh = f16(H128(f32(x) * rin) * RS) per (row, block);
   // wave w takes items w, w + 4, ...; with several rows it requests up to 8
   // items' inputs before transforming them, so one memory round trip serves
@@ -140,7 +140,7 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
       const uint32_t* xs = s_x[c < R ? c : R - 1];
       for (int k = 0; k < nsteps; ++k) {
         LaneWords<K> nxt = cur;
-        if (k + 1 < nsteps) nxt = load_lane_words<K>(lp + (size_t)(kt0 + kstep * (k + 1)) * kstride);
+        if (k + 1 < nsteps) nxt = load_lane_words_nt<K>(lp + (size_t)(kt0 + kstep * (k + 1)) * kstride);
         const u32x4_t* xb = reinterpret_cast<const u32x4_t*>(xs + 8 * (4 * k + gk));
         const uint32_t wprev = __shfl(cur.w[G::WPL - 1], src);
         mma_tile<K, LUT>(cur, wprev, xb[0], xb[1], acc, s_lut);
@@ -155,7 +155,7 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
     for (int i = 0; i < G::NCOL; ++i) acc[0][i] = 0.f;
     for (int k = 0; k < nsteps; ++k) {
       LaneWords<K> nxt = cur;
-      if (valid && k + 1 < nsteps) nxt = load_lane_words<K>(lp + (size_t)(kt0 + k + 1) * kstride);
+      if (valid && k + 1 < nsteps) nxt = load_lane_words_nt<K>(lp + (size_t)(kt0 + k + 1) * kstride);
       uint32_t xw[8], xp[1][8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) xw[i] = s_x[0][8 * (kl0 + k) + i];

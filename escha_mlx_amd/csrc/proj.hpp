@@ -135,8 +135,8 @@ __device__ __forceinline__ void proj_step(const LaneWords<K>* w, uint32_t xv, in
 template <int K>
 __device__ __forceinline__ void proj_load(const uint32_t* base, size_t half_off, uint32_t off,
                                           LaneWords<K>* w) {
-  w[0] = load_lane_words<K>(base + off);
-  if constexpr (K == 3) w[1] = load_lane_words<K>(base + half_off + off);
+  w[0] = load_lane_words_nt<K>(base + off);
+  if constexpr (K == 3) w[1] = load_lane_words_nt<K>(base + half_off + off);
 }
 
 // output column (0..255 of the group) of the lane's accumulator slot ci
