@@ -1333,7 +1333,9 @@ int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
     const dim3 ga(p.L * p.nA), gb(p.L * p.nB), blk(esc::kFusedThreads);
     // the plan's down item size: whole-input blocks (I == 512) or split-K
     const int ktb = p.I / (16 * p.NKB);
-    if (p.L > 1) {
+    // records in a device table (esc_moe_expert_path_layers, any L): the
+    // many-layer items; one record in the arguments: the single-layer ones
+    if (p.layers) {
       hipLaunchKernelGGL((esc::k_moe_gate_up_items<KG, kKtaLayers, true>), ga, blk, 0, s, p);
       if (int rc = launched("k_moe_gate_up_items")) return rc;
       if (ktb == kKtbBlocks) {

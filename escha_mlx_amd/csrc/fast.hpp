@@ -55,19 +55,44 @@ struct LaneWords {
   uint32_t w[Geo<K>::WPL];
 };
 
+// Global-memory view of a device pointer.  A pointer that arrives through
+// memory (a layer record, an item pointer staged in LDS) is generic to the
+// compiler, and its loads become FLAT instructions, which count against the
+// LDS counter as well: every wait for LDS results (the table reads, the
+// reductions) would then also wait for them, so a prefetch of the next
+// step's code could not stay in flight across the decode.  Every device
+// allocation this library reads is global memory.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* as_global(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* as_global_w(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+// float2 through the global view (HIP's float2 is a class that cannot be
+// copied from an address-space-qualified reference; the native vector can)
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float2 ld_global_f2(const float* p) {
+  const f32x2_t v = *as_global(reinterpret_cast<const f32x2_t*>(p));
+  return make_float2(v.x, v.y);
+}
+
 template <int K>
 __device__ __forceinline__ LaneWords<K> load_lane_words(const uint32_t* p) {
   LaneWords<K> r;
   if constexpr (K == 2) {
-    uint4 v = *reinterpret_cast<const uint4*>(p);
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const u32x4_t v = *as_global(reinterpret_cast<const u32x4_t*>(p));
     r.w[0] = v.x;
     r.w[1] = v.y;
     r.w[2] = v.z;
     r.w[3] = v.w;
   } else {
-    r.w[0] = p[0];
-    r.w[1] = p[1];
-    r.w[2] = p[2];
+    const auto* g = as_global(p);
+    r.w[0] = g[0];
+    r.w[1] = g[1];
+    r.w[2] = g[2];
   }
   return r;
 }
@@ -80,15 +105,17 @@ template <int K = 2>
 __device__ __forceinline__ LaneWords<K> load_lane_words_nt(const uint32_t* p) {
   LaneWords<K> r;
   if constexpr (K == 2) {
-    const nt_u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4_t*>(p));
+    const nt_u32x4_t v =
+        __builtin_nontemporal_load(as_global(reinterpret_cast<const nt_u32x4_t*>(p)));
     r.w[0] = v.x;
     r.w[1] = v.y;
     r.w[2] = v.z;
     r.w[3] = v.w;
   } else {
-    r.w[0] = __builtin_nontemporal_load(p);
-    r.w[1] = __builtin_nontemporal_load(p + 1);
-    r.w[2] = __builtin_nontemporal_load(p + 2);
+    const auto* g = as_global(p);
+    r.w[0] = __builtin_nontemporal_load(g);
+    r.w[1] = __builtin_nontemporal_load(g + 1);
+    r.w[2] = __builtin_nontemporal_load(g + 2);
   }
   return r;
 }
@@ -177,46 +204,90 @@ __device__ __forceinline__ void x_pairs(const uint32_t* xw, uint32_t* xp) {
 }
 __device__ constexpr int xpair_index(int r) { return 2 * (r >> 2) | (r & 1); }
 
-// Packed-decode variant of fast_tile (hash only): steps u and u+8 of the lane
-// (u>>3 even) share a tile column and sit 2 rows apart, so they form one
-// dot2 pair.  K=2: their 16-bit windows are adjacent, one v_alignbit gives both.
+// Packed hash decode of the lane's steps u and u+8 (u>>3 even): they share a
+// tile column and sit 2 rows apart, so they form one dot2 pair.  K=2: their
+// 16-bit windows are adjacent, one v_alignbit gives both.
+template <int K>
+__device__ __forceinline__ uint32_t decode_pair(const LaneWords<K>& lw, uint32_t wprev, int u) {
+  using G = Geo<K>;
+  const uint32_t clo = kClo, chi = kChi;
+  if constexpr (K == 2) {
+    // 32-bit window starting at step u's first bit: [s_u | s_{u+8}]
+    const int rel = 2 * (u + 1) - 16;
+    const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
+    const uint32_t hi = a < 0 ? wprev : lw.w[a];
+    uint32_t p;
+    if (off == 0)
+      p = hi;
+    else
+      p = __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 32 - off);
+    return halves_sum2(mask_xor(hash_x<false>(p, clo, chi)), mask_xor(hash_x<true>(p, clo, chi)));
+  } else {
+    static_assert(G::WPL == 3, "");
+    uint32_t s2[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int uu = u + 8 * (1 - h);  // low half: step u+8, high half: step u
+      const int rel = 3 * (uu + 1) - 16;
+      const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
+      const uint32_t hi = a < 0 ? wprev : lw.w[a];
+      // the state in the low 16 bits (bits above are ignored by the u16 ops)
+      s2[h] = off <= 16 ? hi >> (16 - off) : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 48 - off);
+    }
+    return halves_sum2(mask_xor(hash_x<false>(s2[0], clo, chi)),
+                       mask_xor(hash_x<false>(s2[1], clo, chi)));
+  }
+}
+
+// Packed-decode variant of fast_tile (hash only), each pair multiplied as soon
+// as it is decoded (the form the streaming kernels use).
 template <int K>
 __device__ __forceinline__ void fast_tile_packed(const LaneWords<K>& lw, uint32_t wprev,
                                                  const uint32_t* xp, float* acc) {
   using G = Geo<K>;
-  const uint32_t clo = kClo, chi = kChi;
 #pragma unroll
   for (int u = 0; u < G::SPL; ++u) {
     if ((u >> 3) & 1) continue;  // u+8 handled with u
-    uint32_t w2;
-    if constexpr (K == 2) {
-      // 32-bit window starting at step u's first bit: [s_u | s_{u+8}]
-      const int rel = 2 * (u + 1) - 16;
-      const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
-      const uint32_t hi = a < 0 ? wprev : lw.w[a];
-      uint32_t p;
-      if (off == 0)
-        p = hi;
-      else
-        p = __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 32 - off);
-      w2 = halves_sum2(mask_xor(hash_x<false>(p, clo, chi)), mask_xor(hash_x<true>(p, clo, chi)));
-    } else {
-      uint32_t s2[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int uu = u + 8 * (1 - h);  // low half: step u+8, high half: step u
-        const int rel = 3 * (uu + 1) - 16;
-        const int a = (rel + 32) / 32 - 1, off = rel - 32 * a;
-        const uint32_t hi = a < 0 ? wprev : lw.w[a];
-        // the state in the low 16 bits (bits above are ignored by the u16 ops)
-        s2[h] = off <= 16 ? hi >> (16 - off)
-                          : __builtin_amdgcn_alignbit(hi, lw.w[a + 1], 48 - off);
-      }
-      w2 = halves_sum2(mask_xor(hash_x<false>(s2[0], clo, chi)),
-                       mask_xor(hash_x<false>(s2[1], clo, chi)));
-    }
     const int ci = G::col_slot(u);
-    acc[ci] = dot2(xp[xpair_index(fast_row(u))], w2, acc[ci]);
+    acc[ci] = dot2(xp[xpair_index(fast_row(u))], decode_pair<K>(lw, wprev, u), acc[ci]);
+  }
+}
+
+// The same in two phases, so that a caller can decode while its inputs are
+// still on their way: decode_pairs_packed keeps the lane's SPL/2 weight pairs
+// in registers (step order), dot_pairs_packed multiplies them into acc in the
+// same order, so the two are bit-identical to fast_tile_packed.
+template <int K>
+struct TilePairs {
+  uint32_t w[Geo<K>::SPL / 2];
+};
+
+// The pairs are pinned where the decode is written (empty volatile asm with
+// each pair as an operand): left alone, the compiler sinks each decode next to
+// its multiply, past the barrier that waits for the inputs.
+template <int K>
+__device__ __forceinline__ TilePairs<K> decode_pairs_packed(const LaneWords<K>& lw,
+                                                           uint32_t wprev) {
+  TilePairs<K> t;
+  int n = 0;
+#pragma unroll
+  for (int u = 0; u < Geo<K>::SPL; ++u)
+    if (!((u >> 3) & 1)) t.w[n++] = decode_pair<K>(lw, wprev, u);
+#pragma unroll
+  for (int i = 0; i < Geo<K>::SPL / 2; ++i) __asm__ volatile("" : "+v"(t.w[i]));
+  return t;
+}
+
+template <int K>
+__device__ __forceinline__ void dot_pairs_packed(const TilePairs<K>& t, const uint32_t* xp,
+                                                 float* acc) {
+  using G = Geo<K>;
+  int n = 0;
+#pragma unroll
+  for (int u = 0; u < G::SPL; ++u) {
+    if ((u >> 3) & 1) continue;
+    const int ci = G::col_slot(u);
+    acc[ci] = dot2(xp[xpair_index(fast_row(u))], t.w[n++], acc[ci]);
   }
 }
 

@@ -213,6 +213,50 @@ __device__ __forceinline__ void item_to_lds(const ItemCode<K, NKT, NW>& code, co
   for (int c = 0; c < G::NCOL; ++c) s_red[wave][lane][c] = acc[c];
 }
 
+// The item's weights decoded ahead of its inputs (items of one token-layer,
+// whose code arrives before the inputs are transformed): the lane's packed
+// pairs per kt-step, multiplied later by the overload below in the same
+// order, so the item's partials are bit-identical to the one-pass form.
+template <int K, int NKT, int NW>
+struct ItemPairs {
+  TilePairs<K> t[ItemGeo<K, NKT, NW>::NSTEP];
+};
+
+template <int K, int NKT, int NW>
+__device__ __forceinline__ ItemPairs<K, NKT, NW> decode_item(const ItemCode<K, NKT, NW>& code) {
+  using G = Geo<K>;
+  const int lane = threadIdx.x & 63;
+  const int q = lane % G::LPT, i = lane / G::LPT;
+  const int src = i * G::LPT + (q + G::LPT - 1) % G::LPT;
+  ItemPairs<K, NKT, NW> w;
+#pragma unroll
+  for (int k = 0; k < ItemGeo<K, NKT, NW>::NSTEP; ++k)
+    w.t[k] = decode_pairs_packed<K>(code.w[k], __shfl(code.w[k].w[G::WPL - 1], src));
+  return w;
+}
+
+template <int K, int NKT, int NW>
+__device__ __forceinline__ void item_to_lds(const ItemPairs<K, NKT, NW>& w, const uint32_t* s_x,
+                                            float (*s_red)[64][4]) {
+  using G = Geo<K>;
+  using IG = ItemGeo<K, NKT, NW>;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wi = wave % IG::WPG;
+  float acc[G::NCOL];
+#pragma unroll
+  for (int c = 0; c < G::NCOL; ++c) acc[c] = 0.f;
+#pragma unroll
+  for (int k = 0; k < IG::NSTEP; ++k) {
+    const int kl = wi * IG::NSTEP + k;
+    uint32_t xp[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xp[j] = s_x[8 * kl + j];
+    dot_pairs_packed<K>(w.t[k], xp, acc);
+  }
+#pragma unroll
+  for (int c = 0; c < G::NCOL; ++c) s_red[wave][lane][c] = acc[c];
+}
+
 // Column c (0..255) of an item after item_to_lds and a barrier: its wave
 // partials summed in wave order.
 template <int K, int NW = 4>
@@ -232,8 +276,9 @@ __device__ __forceinline__ float item_col(const float (*s_red)[64][4], int c) {
 // dst (device-coherent stores when COH, for a consumer in the same launch;
 // plain stores when the only consumer runs in a later launch).  Thread j < 256
 // returns column j.
-template <int K, int NKT, bool WAIT = true, bool COH = true, bool STORE = true, int NW = 4>
-__device__ __forceinline__ float compute_item(const ItemCode<K, NKT, NW>& code, const uint32_t* s_x,
+template <int K, int NKT, bool WAIT = true, bool COH = true, bool STORE = true, int NW = 4,
+          typename Code = ItemCode<K, NKT, NW>>
+__device__ __forceinline__ float compute_item(const Code& code, const uint32_t* s_x,
                                               float (*s_red)[64][4], float* __restrict__ dst) {
   item_to_lds<K, NKT, NW>(code, s_x, s_red);
   __syncthreads();
@@ -256,12 +301,17 @@ __device__ __forceinline__ float compute_item(const ItemCode<K, NKT, NW>& code, 
 }
 
 template <int K, int KTA, int NW = 4>
-__device__ __forceinline__ ItemCode<K, KTA, NW> load_gate_up(const FusedMoe& p, int l, int a) {
-  const MoeLayer& L = p.layer(l);
+__device__ __forceinline__ ItemCode<K, KTA, NW> load_gate_up(const FusedMoe& p, const MoeLayer& L,
+                                                             int a) {
   const int kc = a % p.NKC, rb = a / p.NKC, b = rb % p.NB, r = rb / p.NB;
   const int TK = p.H / 16, TN = 2 * p.I / 16, half_tn = p.I / 16;
-  return load_item<K, KTA, NW>(L.gu_code + (size_t)L.ids[r] * TK * TN * (8 * K), TN, KTA * kc,
+  return load_item<K, KTA, NW>(L.gu_code + (size_t)as_global(L.ids)[r] * TK * TN * (8 * K), TN, KTA * kc,
                            [&](int it) { return it < 8 ? 8 * b + it : half_tn + 8 * b + (it - 8); });
+}
+
+template <int K, int KTA, int NW = 4>
+__device__ __forceinline__ ItemCode<K, KTA, NW> load_gate_up(const FusedMoe& p, int l, int a) {
+  return load_gate_up<K, KTA, NW>(p, p.layer(l), a);
 }
 
 template <int K, int KTB>
@@ -269,7 +319,7 @@ __device__ __forceinline__ ItemCode<K, KTB> load_down(const FusedMoe& p, int l, 
   const MoeLayer& L = p.layer(l);
   const int kb = bi % p.NKB, cp = (bi / p.NKB) % p.NCP, r = bi / p.NKB / p.NCP;
   const int TK = p.I / 16, TN = p.H / 16;
-  return load_item<K, KTB>(L.dn_code + (size_t)L.ids[r] * TK * TN * (8 * K), TN, KTB * kb,
+  return load_item<K, KTB>(L.dn_code + (size_t)as_global(L.ids)[r] * TK * TN * (8 * K), TN, KTB * kb,
                            [&](int it) { return 16 * cp + it; });
 }
 
@@ -281,22 +331,48 @@ __device__ __forceinline__ void publish_gate_up(const FusedMoe& p, int l, int a)
 
 // gate_up item a of layer l with its code already in flight: transform the
 // item's 16*KTA inputs (one wave per 128-block), decode + multiply, publish.
-template <int K, int KTA, bool PUBLISH = true, bool COH = true, int NW = 4>
-__device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, KTA, NW>& code,
-                            uint32_t* s_x, float (*s_red)[64][4]) {
+// The inputs of gate_up item a that wave `wave` < KTA/8 transforms: its two
+// values of x and their two input scales.
+struct GateUpIn {
+  half_t x0, x1;
+  float r0, r1;
+};
+
+template <int KTA>
+__device__ __forceinline__ GateUpIn gate_up_in(const FusedMoe& p, const MoeLayer& L, int a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const MoeLayer& L = p.layer(l);
-  const int kc = a % p.NKC, r = a / p.NKC / p.NB;
-  const int t = r / p.top_k, e = L.ids[r];
+  GateUpIn in{};
   if (wave < KTA / 8) {
+    const int kc = a % p.NKC, r = a / p.NKC / p.NB;
+    const int t = r / p.top_k, e = as_global(L.ids)[r];
     const int c = 16 * KTA * kc + 128 * wave + 2 * lane;
-    const uint16_t* xr = L.x + (size_t)t * p.H + c;
-    const float* ri = L.gu_rin + (size_t)e * p.H + c;
-    float v0 = (float)__builtin_bit_cast(half_t, xr[0]) * ri[0];
-    float v1 = (float)__builtin_bit_cast(half_t, xr[1]) * ri[1];
+    const auto* xr = as_global(L.x + (size_t)t * p.H + c);
+    const auto* ri = as_global(L.gu_rin + (size_t)e * p.H + c);
+    in.x0 = __builtin_bit_cast(half_t, xr[0]);
+    in.x1 = __builtin_bit_cast(half_t, xr[1]);
+    in.r0 = ri[0];
+    in.r1 = ri[1];
+  }
+  return in;
+}
+
+// Input transform of the item's 16*KTA inputs (one wave per 128-block) into
+// s_x as decode input pairs.
+template <int KTA>
+__device__ __forceinline__ void gate_up_transform(const GateUpIn& in, uint32_t* s_x) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave < KTA / 8) {
+    float v0 = (float)in.x0 * in.r0;
+    float v1 = (float)in.x1 * in.r1;
     h128_wave(v0, v1);
     s_x[64 * wave + lane] = paired_word(pack2(to_f16(v0 * kRS), to_f16(v1 * kRS)));
   }
+}
+
+template <int K, int KTA, bool PUBLISH = true, bool COH = true, int NW = 4>
+__device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, KTA, NW>& code,
+                            uint32_t* s_x, float (*s_red)[64][4]) {
+  gate_up_transform<KTA>(gate_up_in<KTA>(p, p.layer(l), a), s_x);
   __syncthreads();
   compute_item<K, KTA, PUBLISH, COH, true, NW>(code, s_x, s_red,
                                               p.partA + ((size_t)l * p.nA + a) * 256);
@@ -308,47 +384,83 @@ __device__ void run_gate_up(const FusedMoe& p, int l, int a, const ItemCode<K, K
 // kc order, the gate_up output transform, SwiGLU and the down input transform.
 // COH: the partials were published in this launch (device-coherent loads);
 // otherwise by an earlier launch (plain loads, which may hit L2).
+// One batch of CH kc partials of the h-block (gate and up values of the
+// lane's two columns), loaded together.
+template <int CH>
+struct HBatch {
+  float2 g[CH], u[CH];
+};
+
+template <bool COH, int CH>
+__device__ __forceinline__ HBatch<CH> h_batch(const FusedMoe& p, const float* base, int kc0) {
+  HBatch<CH> b;
+#pragma unroll
+  for (int j = 0; j < CH; ++j)
+    if (kc0 + j < p.NKC) {
+      if constexpr (COH) {
+        b.g[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256);
+        b.u[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256 + 128);
+      } else {
+        b.g[j] = *reinterpret_cast<const float2*>(base + (size_t)(kc0 + j) * 256);
+        b.u[j] = *reinterpret_cast<const float2*>(base + (size_t)(kc0 + j) * 256 + 128);
+      }
+    }
+  return b;
+}
+
+__device__ __forceinline__ const float* h_base(const FusedMoe& p, int l, int r, int kb) {
+  return p.partA + ((size_t)l * p.nA + (size_t)(r * p.NB + kb) * p.NKC) * 256 +
+         2 * (threadIdx.x & 63);
+}
+
+// The scales h-block kb of row r needs after its sums: the gate_up output
+// scales of the lane's two gate and two up columns and the down input scales
+// of its two inputs (expert e).
+struct HScales {
+  float2 g, u, ri;
+};
+
+__device__ __forceinline__ HScales h_scales(const FusedMoe& p, const MoeLayer& L, int e, int kb) {
+  const int cg = 128 * kb + 2 * (threadIdx.x & 63);
+  const float* ro = L.gu_rout + (size_t)e * 2 * p.I;
+  return HScales{ld_global_f2(ro + cg), ld_global_f2(ro + p.I + cg),
+                 ld_global_f2(L.dn_rin + (size_t)e * p.I + cg)};
+}
+
+// h_pair with its first batch of partials and its scales already requested
+// (h_batch at kc0 = 0, h_scales), so that a caller can issue those loads
+// before other work.
 template <bool COH = true, int CH = 8>
-__device__ uint32_t h_pair(const FusedMoe& p, int l, int r, int kb) {
-  const int lane = threadIdx.x & 63;
-  const MoeLayer& L = p.layer(l);
-  const int e = L.ids[r];
-  const float* base =
-      p.partA + ((size_t)l * p.nA + (size_t)(r * p.NB + kb) * p.NKC) * 256 + 2 * lane;
+__device__ uint32_t h_pair_from(const FusedMoe& p, int l, int r, int kb, const HBatch<CH>& first,
+                                const HScales& sc) {
+  const float* base = h_base(p, l, r, kb);
   float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
   for (int kc0 = 0; kc0 < p.NKC; kc0 += CH) {
-    float2 gv[CH], uv[CH];
+    const HBatch<CH> b = kc0 == 0 ? first : h_batch<COH, CH>(p, base, kc0);
 #pragma unroll
     for (int j = 0; j < CH; ++j)
       if (kc0 + j < p.NKC) {
-        if constexpr (COH) {
-          gv[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256);
-          uv[j] = ld_coherent2(base + (size_t)(kc0 + j) * 256 + 128);
-        } else {
-          gv[j] = *reinterpret_cast<const float2*>(base + (size_t)(kc0 + j) * 256);
-          uv[j] = *reinterpret_cast<const float2*>(base + (size_t)(kc0 + j) * 256 + 128);
-        }
-      }
-#pragma unroll
-    for (int j = 0; j < CH; ++j)
-      if (kc0 + j < p.NKC) {
-        g0 = g0 + gv[j].x;
-        g1 = g1 + gv[j].y;
-        u0 = u0 + uv[j].x;
-        u1 = u1 + uv[j].y;
+        g0 = g0 + b.g[j].x;
+        g1 = g1 + b.g[j].y;
+        u0 = u0 + b.u[j].x;
+        u1 = u1 + b.u[j].y;
       }
   }
   h128_wave(g0, g1);
   h128_wave(u0, u1);
-  const int cg = 128 * kb + 2 * lane, cu = p.I + cg;
-  const float* ro = L.gu_rout + (size_t)e * 2 * p.I;
-  const half_t h0 = swiglu1(to_f16((g0 * kRS) * ro[cg]), to_f16((u0 * kRS) * ro[cu]));
-  const half_t h1 = swiglu1(to_f16((g1 * kRS) * ro[cg + 1]), to_f16((u1 * kRS) * ro[cu + 1]));
-  const float* ri = L.dn_rin + (size_t)e * p.I + cg;
-  float v0 = (float)h0 * ri[0];
-  float v1 = (float)h1 * ri[1];
+  const half_t h0 = swiglu1(to_f16((g0 * kRS) * sc.g.x), to_f16((u0 * kRS) * sc.u.x));
+  const half_t h1 = swiglu1(to_f16((g1 * kRS) * sc.g.y), to_f16((u1 * kRS) * sc.u.y));
+  float v0 = (float)h0 * sc.ri.x;
+  float v1 = (float)h1 * sc.ri.y;
   h128_wave(v0, v1);
   return paired_word(pack2(to_f16(v0 * kRS), to_f16(v1 * kRS)));
+}
+
+template <bool COH = true, int CH = 8>
+__device__ uint32_t h_pair(const FusedMoe& p, int l, int r, int kb) {
+  const MoeLayer& L = p.layer(l);
+  return h_pair_from<COH, CH>(p, l, r, kb, h_batch<COH, CH>(p, h_base(p, l, r, kb), 0),
+                              h_scales(p, L, as_global(L.ids)[r], kb));
 }
 
 // h-block kb of row r (layer l) -> its 128 down inputs (paired words) in s_x[0..63].
@@ -398,12 +510,12 @@ __device__ void combine_tile(const FusedMoe& p, int l, int t, int cp, uint16_t (
     for (int u = 0; u < 2; ++u) {
       const int s = s0 + 4 * u;
       if (s >= p.top_k) continue;
-      const int e = L.ids[t * p.top_k + s];
+      const int e = as_global(L.ids)[t * p.top_k + s];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         h128_wave(v[u][h][0], v[u][h][1]);
         const int col = 256 * cp + 128 * h + 2 * lane;
-        const float* ro = L.dn_rout + (size_t)e * p.H + col;
+        const auto* ro = as_global(L.dn_rout + (size_t)e * p.H + col);
         s_d[s][128 * h + 2 * lane] = __builtin_bit_cast(uint16_t, to_f16((v[u][h][0] * kRS) * ro[0]));
         s_d[s][128 * h + 2 * lane + 1] =
             __builtin_bit_cast(uint16_t, to_f16((v[u][h][1] * kRS) * ro[1]));
@@ -414,10 +526,10 @@ __device__ void combine_tile(const FusedMoe& p, int l, int t, int cp, uint16_t (
   const int j = threadIdx.x;
   float a = 0.f;
   for (int s = 0; s < p.top_k; ++s) {
-    const float w = (float)(half_t)L.scores[t * p.top_k + s];
+    const float w = (float)(half_t)as_global(L.scores)[t * p.top_k + s];
     a = a + (float)__builtin_bit_cast(half_t, s_d[s][j]) * w;
   }
-  L.y[(size_t)t * p.H + 256 * cp + j] = __builtin_bit_cast(uint16_t, (half_t)a);
+  as_global_w(L.y)[(size_t)t * p.H + 256 * cp + j] = __builtin_bit_cast(uint16_t, (half_t)a);
 }
 
 // Block-uniform wait for the gate_up items of (layer l, row r, h-block kb):
@@ -507,8 +619,22 @@ __global__ __launch_bounds__(64 * NW) void k_moe_gate_up_items(FusedMoe p) {
   const int tid = threadIdx.x;
   const int g = xcd_item(blockIdx.x, gridDim.x);
   const int l = g / p.nA, a = g % p.nA;
-  const auto code = load_gate_up<KG, KTA, NW>(p, l, a);
-  run_gate_up<KG, KTA, false, PREH, NW>(p, l, a, code, s_x, s_red);
+  if constexpr (NW == 16) {
+    // one token-layer (the record in the kernel arguments, read once): one
+    // kt-step per wave, whose weights are decoded as soon as the code arrives,
+    // while the inputs' loads and transform are still pending
+    static_assert(!PREH, "16-wave items run one token-layer");
+    const MoeLayer L = p.l0;
+    const auto code = load_gate_up<KG, KTA, NW>(p, L, a);
+    const GateUpIn in = gate_up_in<KTA>(p, L, a);
+    const auto w = decode_item<KG, KTA, NW>(code);
+    gate_up_transform<KTA>(in, s_x);
+    __syncthreads();
+    compute_item<KG, KTA, false, false, true, NW>(w, s_x, s_red, p.partA + (size_t)a * 256);
+  } else {
+    const auto code = load_gate_up<KG, KTA, NW>(p, l, a);
+    run_gate_up<KG, KTA, false, PREH, NW>(p, l, a, code, s_x, s_red);
+  }
   if constexpr (PREH) {
     wait_vm();  // this wave's partial stores have completed
     __syncthreads();
@@ -629,6 +755,47 @@ __device__ __forceinline__ void block_item_to_lds(const BlockCode<K, NW>& code,
   for (int c = 0; c < G::NCOL; ++c) s_red[wave][lane][c] = acc[c];
 }
 
+// A block item's weights decoded ahead of its inputs (as ItemPairs).
+template <int K, int NW>
+struct BlockPairs {
+  TilePairs<K> t[BlockItem<K, NW>::NSTEP];
+};
+
+template <int K, int NW>
+__device__ __forceinline__ BlockPairs<K, NW> decode_block_item(const BlockCode<K, NW>& code) {
+  using G = Geo<K>;
+  const int lane = threadIdx.x & 63;
+  const int q = lane % G::LPT, i = lane / G::LPT;
+  const int src = i * G::LPT + (q + G::LPT - 1) % G::LPT;
+  BlockPairs<K, NW> w;
+#pragma unroll
+  for (int k = 0; k < BlockItem<K, NW>::NSTEP; ++k)
+    w.t[k] = decode_pairs_packed<K>(code.w[k], __shfl(code.w[k].w[G::WPL - 1], src));
+  return w;
+}
+
+template <int K, int NW>
+__device__ __forceinline__ void block_item_to_lds(const BlockPairs<K, NW>& w, const uint32_t* s_x,
+                                                  float (*s_red)[64][4]) {
+  using G = Geo<K>;
+  using BI = BlockItem<K, NW>;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = (lane & 63) / G::LPT;
+  float acc[G::NCOL];
+#pragma unroll
+  for (int c = 0; c < G::NCOL; ++c) acc[c] = 0.f;
+#pragma unroll
+  for (int k = 0; k < BI::NSTEP; ++k) {
+    const int kl = BI::KPS * (wave * BI::NSTEP + k) + i / 8;
+    uint32_t xp[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xp[j] = s_x[8 * kl + j];
+    dot_pairs_packed<K>(w.t[k], xp, acc);
+  }
+#pragma unroll
+  for (int c = 0; c < G::NCOL; ++c) s_red[wave][lane][c] = acc[c];
+}
+
 // Column c (0..127) of a block item after block_item_to_lds and a barrier:
 // summed over the waves in order, each wave's kt slots in order.
 template <int K, int NW>
@@ -646,14 +813,80 @@ __device__ __forceinline__ float block_item_col(const float (*s_red)[64][4], int
   return v;
 }
 
+// What wave 0 of a block down item needs after the decode, requested when the
+// item starts so that no load waits behind its barriers: the two output
+// scales of column pair `lane` and the f16-rounded score of slot `lane`.
+struct DownTail {
+  float ro0 = 0.f, ro1 = 0.f, score = 0.f;
+};
+
+__device__ __forceinline__ DownTail down_tail(const FusedMoe& p, const MoeLayer& L, int e, int t,
+                                              int hb) {
+  const int lane = threadIdx.x & 63;
+  DownTail d;
+  if ((threadIdx.x >> 6) == 0) {
+    const auto* ro = as_global(L.dn_rout + (size_t)e * p.H + 128 * hb + 2 * lane);
+    d.ro0 = ro[0];
+    d.ro1 = ro[1];
+    if (lane < p.top_k) d.score = (float)(half_t)as_global(L.scores)[t * p.top_k + lane];
+  }
+  return d;
+}
+
+// Block down item bi of layer l after block_item_to_lds and a barrier: wave 0
+// sums the waves, applies the down output transform, rounds the 128 columns
+// to f16 and publishes them (256 bytes of partB at float offset 64 bi); the
+// last of the (token, hb)'s top_k items to publish gathers their f16 rows and
+// combines them in slot order (f16(score) weights, float32 sum, one f16
+// rounding) into y.
+template <int KD, int NW>
+__device__ __forceinline__ void down_block_finish(const FusedMoe& p, const MoeLayer& L, int l,
+                                                  int bi, const DownTail& d,
+                                                  const float (*s_red)[64][4]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave != 0) return;
+  const int hb = bi % p.NCP, t = bi / p.NCP / p.top_k;
+  uint32_t* rows = reinterpret_cast<uint32_t*>(p.partB + (size_t)l * p.nB * 256);
+  float v0 = block_item_col<KD, NW>(s_red, 2 * lane);
+  float v1 = block_item_col<KD, NW>(s_red, 2 * lane + 1);
+  h128_wave(v0, v1);
+  const uint32_t w = pack2(to_f16((v0 * kRS) * d.ro0), to_f16((v1 * kRS) * d.ro1));
+  __hip_atomic_store(rows + (size_t)bi * 64 + lane, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  wait_vm();
+  int last = 0;
+  if (lane == 0) {
+    int* c = &p.cntB[(size_t)l * p.T * p.NCP + t * p.NCP + hb];
+    last = add_publish(c, 1) == p.top_k - 1;
+    if (last) {
+      after_count();
+      __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (!__shfl(last, 0)) return;
+  float a0 = 0.f, a1 = 0.f;
+  for (int s0 = 0; s0 < p.top_k; s0 += 8) {
+    uint32_t d8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (s0 + j < p.top_k)
+        d8[j] = __hip_atomic_load(rows + (size_t)((t * p.top_k + s0 + j) * p.NCP + hb) * 64 + lane,
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (s0 + j < p.top_k) {
+        const float sw = __shfl(d.score, s0 + j);
+        a0 = a0 + (float)__builtin_bit_cast(half_t, (uint16_t)d8[j]) * sw;
+        a1 = a1 + (float)__builtin_bit_cast(half_t, (uint16_t)(d8[j] >> 16)) * sw;
+      }
+  }
+  as_global_w(reinterpret_cast<uint32_t*>(L.y + (size_t)t * p.H + 128 * hb))[lane] =
+      pack2((half_t)a0, (half_t)a1);
+}
+
 // One item per block (plan: NCP = H / 128 column blocks, NKB = 1).  The item
 // takes the row's 512 down inputs (4 waves, one h-block each: derived from the
 // gate_up partials, or read ready-made from xh2 when PREH), decodes and
-// multiplies, sums its waves, applies the down output transform and rounds
-// its 128 columns to f16 itself; the last of a (token, hb)'s top_k items to
-// finish gathers their f16 rows and combines them in slot order (f16(score)
-// weights, float32 sum, one f16 rounding).  The f16 row of item bi takes
-// 256 bytes of partB at float offset 64 bi.
+// multiplies, and finishes as down_block_finish.
 template <int KG, int KD, bool PREH, int NW>
 __global__ __launch_bounds__(64 * NW) void k_moe_down_blocks(FusedMoe p) {
   static_assert(NW >= 4, "one wave per h-block");
@@ -663,66 +896,43 @@ __global__ __launch_bounds__(64 * NW) void k_moe_down_blocks(FusedMoe p) {
   const int g = xcd_item(blockIdx.x, gridDim.x);
   const int l = g / p.nB, bi = g % p.nB;
   const int hb = bi % p.NCP, r = bi / p.NCP, t = r / p.top_k;
-  const MoeLayer& L = p.layer(l);
-  const int e = L.ids[r];
   const int TN = p.H / 16;
-  const auto code = load_block_item<KD, NW>(L.dn_code + (size_t)e * (p.I / 16) * TN * (8 * KD), TN, hb);
-  // wave 0's tail inputs, requested now so that no load waits behind the
-  // barriers: its two output scales and the f16-rounded score of slot `lane`
-  float ro0 = 0.f, ro1 = 0.f, score = 0.f;
-  if (wave == 0) {
-    const float* ro = L.dn_rout + (size_t)e * p.H + 128 * hb + 2 * lane;
-    ro0 = ro[0];
-    ro1 = ro[1];
-    if (lane < p.top_k) score = (float)(half_t)L.scores[t * p.top_k + lane];
-  }
-  if (wave < 4) {
-    if constexpr (PREH)
-      s_x[64 * wave + lane] = reinterpret_cast<const uint32_t*>(
-          p.xh2 + ((size_t)l * p.T * p.top_k + r) * p.I + 128 * wave)[lane];
-    else
-      s_x[64 * wave + lane] = h_pair<false>(p, l, r, wave);
-  }
-  __syncthreads();
-  block_item_to_lds<KD, NW>(code, s_x, s_red);
-  __syncthreads();
-  uint32_t* rows = reinterpret_cast<uint32_t*>(p.partB + (size_t)l * p.nB * 256);
-  if (wave == 0) {
-    float v0 = block_item_col<KD, NW>(s_red, 2 * lane);
-    float v1 = block_item_col<KD, NW>(s_red, 2 * lane + 1);
-    h128_wave(v0, v1);
-    const uint32_t d = pack2(to_f16((v0 * kRS) * ro0), to_f16((v1 * kRS) * ro1));
-    __hip_atomic_store(rows + (size_t)bi * 64 + lane, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    wait_vm();
-    int last = 0;
-    if (lane == 0) {
-      int* c = &p.cntB[(size_t)l * p.T * p.NCP + t * p.NCP + hb];
-      last = add_publish(c, 1) == p.top_k - 1;
-      if (last) {
-        after_count();
-        __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+  if constexpr (NW == 16) {
+    // one token-layer (the record in the kernel arguments, read once): the
+    // gate_up partials are requested first (their address needs no expert
+    // id), then the expert's code and every scale the item needs, and the
+    // weights are decoded while the partials are still on their way
+    static_assert(!PREH, "16-wave block items run one token-layer");
+    const MoeLayer L = p.l0;
+    const HBatch<8> first = wave < 4 ? h_batch<false, 8>(p, h_base(p, 0, r, wave), 0) : HBatch<8>{};
+    const int e = as_global(L.ids)[r];
+    const auto code =
+        load_block_item<KD, NW>(L.dn_code + (size_t)e * (p.I / 16) * TN * (8 * KD), TN, hb);
+    const DownTail d = down_tail(p, L, e, t, hb);
+    const HScales sc = wave < 4 ? h_scales(p, L, e, wave) : HScales{};
+    const auto w = decode_block_item<KD, NW>(code);
+    if (wave < 4) s_x[64 * wave + lane] = h_pair_from<false, 8>(p, 0, r, wave, first, sc);
+    __syncthreads();
+    block_item_to_lds<KD, NW>(w, s_x, s_red);
+    __syncthreads();
+    down_block_finish<KD, NW>(p, L, 0, bi, d, s_red);
+  } else {
+    const MoeLayer& L = p.layer(l);
+    const int e = as_global(L.ids)[r];
+    const auto code =
+        load_block_item<KD, NW>(L.dn_code + (size_t)e * (p.I / 16) * TN * (8 * KD), TN, hb);
+    const DownTail d = down_tail(p, L, e, t, hb);
+    if (wave < 4) {
+      if constexpr (PREH)
+        s_x[64 * wave + lane] = reinterpret_cast<const uint32_t*>(
+            p.xh2 + ((size_t)l * p.T * p.top_k + r) * p.I + 128 * wave)[lane];
+      else
+        s_x[64 * wave + lane] = h_pair<false>(p, l, r, wave);
     }
-    if (__shfl(last, 0)) {
-      float a0 = 0.f, a1 = 0.f;
-      for (int s0 = 0; s0 < p.top_k; s0 += 8) {
-        uint32_t d8[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (s0 + j < p.top_k)
-            d8[j] = __hip_atomic_load(rows + (size_t)((t * p.top_k + s0 + j) * p.NCP + hb) * 64 + lane,
-                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (s0 + j < p.top_k) {
-            const float w = __shfl(score, s0 + j);
-            a0 = a0 + (float)__builtin_bit_cast(half_t, (uint16_t)d8[j]) * w;
-            a1 = a1 + (float)__builtin_bit_cast(half_t, (uint16_t)(d8[j] >> 16)) * w;
-          }
-      }
-      reinterpret_cast<uint32_t*>(L.y + (size_t)t * p.H + 128 * hb)[lane] =
-          pack2((half_t)a0, (half_t)a1);
-    }
+    __syncthreads();
+    block_item_to_lds<KD, NW>(code, s_x, s_red);
+    __syncthreads();
+    down_block_finish<KD, NW>(p, L, l, bi, d, s_red);
   }
 }
 

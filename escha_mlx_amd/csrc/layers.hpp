@@ -225,7 +225,7 @@ struct GuMeta {
 };
 
 __device__ __forceinline__ GuMeta gu_meta(const LayersMoe& p, const MoeLayer& L, const GuItem& it) {
-  const int e = L.ids[it.r];
+  const int e = as_global(L.ids)[it.r];
   const size_t tn = 2 * p.I / 16;
   GuMeta m;
   m.code = L.gu_code + (size_t)e * (p.H / 16) * tn * 16 + (size_t)(8 * it.kc) * tn * 16 +
@@ -265,9 +265,9 @@ struct GuScales {
 };
 __device__ __forceinline__ GuScales gu_scales(const LayersMoe& p, const GuMeta& m) {
   const int lane = threadIdx.x & 63;
-  return GuScales{*reinterpret_cast<const float2*>(m.rout + 2 * lane),
-                  *reinterpret_cast<const float2*>(m.rout + p.I + 2 * lane),
-                  *reinterpret_cast<const float2*>(m.drin + 2 * lane)};
+  return GuScales{ld_global_f2(m.rout + 2 * lane),
+                  ld_global_f2(m.rout + p.I + 2 * lane),
+                  ld_global_f2(m.drin + 2 * lane)};
 }
 
 __device__ __forceinline__ void gu_epilogue(const LayersMoe& p, int l, int r, int b,
@@ -319,8 +319,8 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_gu(LayersMoe p
   const GuMeta* meta = s_meta + wave * p.P - i0;  // meta[i]: item i of this wave
   GuMeta m = gu_meta_uniform(meta[i0]);
   LaneWords<2> w = load_lane_words_nt(m.code + off);
-  uint32_t xw = *reinterpret_cast<const uint32_t*>(m.x + 2 * lane);
-  float2 ri = *reinterpret_cast<const float2*>(m.rin + 2 * lane);
+  uint32_t xw = *as_global(reinterpret_cast<const uint32_t*>(m.x + 2 * lane));
+  float2 ri = ld_global_f2(m.rin + 2 * lane);
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (int i = i0; i < iend; ++i) {
     prio_left(iend - i);
@@ -330,8 +330,8 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_gu(LayersMoe p
     walk_head(m.code, off, 8, stride, xv, tb, w, acc);
     // the next item's inputs and first step (the current item's again when
     // there is none: in bounds, unused)
-    xw = *reinterpret_cast<const uint32_t*>(m1.x + 2 * lane);
-    ri = *reinterpret_cast<const float2*>(m1.rin + 2 * lane);
+    xw = *as_global(reinterpret_cast<const uint32_t*>(m1.x + 2 * lane));
+    ri = ld_global_f2(m1.rin + 2 * lane);
     {
       const LaneWords<2> wn = load_lane_words_nt(m1.code + off);
       mix_step(w, xv, 56, tb, acc);
@@ -372,7 +372,7 @@ __device__ __forceinline__ void combine_pair(const LayersMoe& p, int l, int t, i
       if (k0 + j < p.top_k) {
         d8[0][j] = ld_coherent_u32(rws + (size_t)(k0 + j) * (p.H / 2));
         d8[1][j] = ld_coherent_u32(rws + (size_t)(k0 + j) * (p.H / 2) + 64);
-        w8[j] = (float)(half_t)L.scores[t * p.top_k + k0 + j];
+        w8[j] = (float)(half_t)as_global(L.scores)[t * p.top_k + k0 + j];
       }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
@@ -386,7 +386,7 @@ __device__ __forceinline__ void combine_pair(const LayersMoe& p, int l, int t, i
   }
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk)
-    reinterpret_cast<uint32_t*>(L.y + (size_t)t * p.H + 256 * cp + 128 * blk)[lane] =
+    as_global_w(reinterpret_cast<uint32_t*>(L.y + (size_t)t * p.H + 256 * cp + 128 * blk))[lane] =
         pack2((half_t)s[blk][0], (half_t)s[blk][1]);
 }
 
@@ -412,7 +412,7 @@ struct DnMeta {
 };
 
 __device__ __forceinline__ DnMeta dn_meta(const LayersMoe& p, const MoeLayer& L, const DnItem& it) {
-  const int e = L.ids[it.r];
+  const int e = as_global(L.ids)[it.r];
   const size_t tn = p.H / 16;
   DnMeta m;
   m.code = L.dn_code + (size_t)e * (p.I / 16) * tn * 16 + (size_t)(it.e8 * (p.I / 128)) * tn * 16 +
@@ -494,8 +494,8 @@ __global__ __launch_bounds__(64 * kLayersWaves) void k_moe_layers_dn(LayersMoe p
     const int g = i / kDownEighths;  // group (l, r, cp)
     if (!more || (i + 1) / kDownEighths != g) {
       // the output scales, requested before the hand-off
-      const float2 ra = *reinterpret_cast<const float2*>(m.rout + 2 * lane);
-      const float2 rb = *reinterpret_cast<const float2*>(m.rout + 128 + 2 * lane);
+      const float2 ra = ld_global_f2(m.rout + 2 * lane);
+      const float2 rb = ld_global_f2(m.rout + 128 + 2 * lane);
       if (publish(p, g, kDownEighths, acc)) {
         // columns 2 lane, +1 of block 2 cp (tiles 0-7, a) and 2 cp + 1 (b)
         float a0, a1, b0, b1;

@@ -728,6 +728,39 @@ def test_moe_block_down_items_vs_oracle(K_gu, K_dn, T, k, monkeypatch):
         assert np.array_equal(bits16(blk(x, ids, sc)), first)
 
 
+@pytest.mark.parametrize("K_gu,K_dn,k", [(2, 2, 8), (2, 3, 8), (3, 2, 4), (3, 3, 16)])
+def test_moe_token_alone_equals_token_in_a_larger_call(K_gu, K_dn, k):
+    """I == 512, one token-layer kernels (16-wave gate_up items that decode
+    before their inputs arrive, 16-wave down blocks that decode while the
+    gate_up partials load): a token routed alone and the same token as token 0
+    of a call with more tokens give bit-identical outputs (each row's sums do
+    not depend on the other rows), 40 calls in a row on one workspace stay
+    bit-identical (the combine counters return to zero), and the output is
+    held to the oracle."""
+    E, H, I = 64, 2048, 512
+    T2 = 16 // k + 1
+    c = _moe_case(E, H, I, K_gu, K_dn, T2, k, 500 + 10 * K_gu + K_dn + k)
+    o = ops()
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    ids2, sc2 = o.route_topk(dv(c["logits"]), k)
+    x2 = dv(c["x"])
+    args = (dcode(c["gu_code"]), dv(c["gu_rin"]), dv(c["gu_rout"]), K_gu, dcode(c["dn_code"]),
+            dv(c["dn_rin"]), dv(c["dn_rout"]), K_dn)
+    y2 = o.moe_expert_path(x2, ids2, sc2, *args)
+    x1, ids1, sc1 = x2[:1].contiguous(), ids2[:1].contiguous(), sc2[:1].contiguous()
+    ws = torch.zeros(o.moe_expert_path_workspace(1, k, E, H, I), dtype=torch.uint8, device=DEV)
+    y1 = o.moe_expert_path(x1, ids1, sc1, *args, ws=ws)
+    assert np.array_equal(bits16(y1), bits16(y2[:1]))
+    first = bits16(y1)
+    for _ in range(40):
+        assert np.array_equal(bits16(o.moe_expert_path(x1, ids1, sc1, *args, ws=ws)), first)
+    ids_np, sc_np = ids1.cpu().numpy(), sc1.cpu().numpy()
+    c1 = dict(c, x=c["x"][:1])
+    want = _oracle_moe(c1, ids_np, sc_np, E, H, I, K_gu, K_dn, np.unique(ids_np)).astype(np.float32)
+    got = y1.cpu().numpy().astype(np.float32)
+    assert np.abs(got - want).max() / np.abs(want).max() < 5e-3
+
+
 # ---------------------------------------------------------------- dense module
 
 def test_dense_linear_module_vs_deploy_and_oracle(dense_linear_golden, monkeypatch):
