@@ -132,5 +132,24 @@ __device__ __forceinline__ void table_put(const TablePieces& t, uint16_t* s_dst)
 #pragma unroll
   for (int k = 0; k < 8; ++k) dst[threadIdx.x + 1024 * k] = t.v[k];
 }
+// The same copy for a workgroup of 16 waves through the LDS DMA path
+// (global_load_lds_dwordx4): each wave's eight loads write their 1 KiB pieces
+// straight into LDS (lane i's 16 bytes at the wave's base + 16 i), so no
+// register holds the table and the wave can decode meanwhile.  The loads
+// count against vmcnt: the caller waits for them (s_waitcnt vmcnt(0)) before
+// the barrier after which the table is read.
+__device__ __forceinline__ void table_dma(uint16_t* s_dst) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const char* src = reinterpret_cast<const char*>(g_lut);
+  char* dst = reinterpret_cast<char*>(s_dst);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int piece = (16 * k + wave) * 1024;  // bytes
+    __builtin_amdgcn_global_load_lds(
+        (const __attribute__((address_space(1))) void*)(src + piece + 16 * lane),
+        (__attribute__((address_space(3))) void*)(dst + piece), 16, 0, 0);
+  }
+}
 
 }  // namespace esc

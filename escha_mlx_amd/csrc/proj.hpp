@@ -167,10 +167,8 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_proj_rows1(ProjArgs p) {
   const uint32_t off = (uint32_t)(lane * Geo<K>::WPL);
   const size_t half_off = (size_t)8 * 8 * K;  // K=3: the next 8 tiles
 
-  // the table's pieces, then this wave's first unit and its inputs, are
-  // requested before anything waits
-  TablePieces tp;
-  if constexpr (NT > 0) table_fetch(tp);
+  // this wave's first unit and its inputs, then the table's pieces (LDS DMA),
+  // are requested before anything waits
   ProjUnit c = proj_unit(q, busy ? a : 0);
   const ProjUnit cl = proj_unit(q, busy ? b - 1 : 0);
   LaneWords<K> w[K == 3 ? 2 : 1];
@@ -180,44 +178,68 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_proj_rows1(ProjArgs p) {
   // units [a, ub) use block A, [ub, b) block B; [a, ug) group c.g, [ug, b) cl.g
   const int ub = two_blocks ? b - 1 - (cl.kt & 7) : b;
   const int ug = cl.g != c.g ? b - 1 - cl.kt : b;
-
-  uint32_t tb = 0;
-  if constexpr (NT > 0) {
-    table_put(tp, s_dyn);
-    tb = (uint32_t)(size_t)s_dyn;
-  }
   if (lane == 0) {
     s_grp[wave][0] = busy ? c.g : -1;
     s_grp[wave][1] = busy && ug < b ? cl.g : -1;
   }
+
   const uint32_t xa = proj_inputs(ina, p.rs);
   const uint32_t xb = two_blocks ? proj_inputs(inb, p.rs) : xa;
-  __syncthreads();
+  if constexpr (NT > 0) {
+    // The table's pieces are requested once the first unit's code and the
+    // inputs are in registers (the compiler waits for every outstanding load
+    // after a DMA into LDS, so a wait placed later would also wait for the
+    // table), and land while the first unit decodes.
+#pragma unroll
+    for (int h = 0; h < (K == 3 ? 2 : 1); ++h)
+#pragma unroll
+      for (int j = 0; j < Geo<K>::WPL; ++j) __asm__ volatile("" : : "v"(w[h].w[j]));
+    table_dma(s_dyn);
+  }
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f}, accA[4] = {0.f, 0.f, 0.f, 0.f};
+  // unit u: the next unit's code requested (this one again at the end: in
+  // bounds, unused), decode + multiply (table pairs from LDS when TAB), and
+  // the partial of group c.g set aside when that group ends inside the range
+  auto unit = [&](int u, auto tab, uint32_t tbu) {
+    ProjUnit cn = c;
+    if (u + 1 < b && ++cn.kt == q.TK) {
+      cn.kt = 0;
+      ++cn.g;
+    }
+    LaneWords<K> wn[K == 3 ? 2 : 1];
+    proj_load<K>(proj_code<K>(q, cn), half_off, off, wn);
+    proj_step<K, decltype(tab)::value>(w, u < ub ? xa : xb, 8 * (c.kt & 7), tbu, s_dyn, acc);
+    if (u + 1 == ug && ug < b) {  // group c.g ends inside the range
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        accA[i] = acc[i];
+        acc[i] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < (K == 3 ? 2 : 1); ++h) w[h] = wn[h];
+    c = cn;
+  };
+  // the first unit is decoded by hash before the table is in LDS, so its
+  // decode runs while the table's pieces are still arriving (the table is
+  // the hash's image and the step order is the same: bit-identical)
+  if (busy) {
+    prio_left(b - a);
+    unit(a, std::integral_constant<int, 0>{}, 0u);
+  }
+  uint32_t tb = 0;
+  if constexpr (NT > 0) {
+    wait_vm();  // this wave's table pieces are in LDS
+    tb = (uint32_t)(size_t)s_dyn;
+  }
+  __syncthreads();
+
   if (busy) {
 #pragma unroll 1
-    for (int u = a; u < b; ++u) {
+    for (int u = a + 1; u < b; ++u) {
       prio_left(b - u);
-      // the next unit (this one again at the end: in bounds, unused)
-      ProjUnit cn = c;
-      if (u + 1 < b && ++cn.kt == q.TK) {
-        cn.kt = 0;
-        ++cn.g;
-      }
-      LaneWords<K> wn[K == 3 ? 2 : 1];
-      proj_load<K>(proj_code<K>(q, cn), half_off, off, wn);
-      proj_step<K, NT>(w, u < ub ? xa : xb, 8 * (c.kt & 7), tb, s_dyn, acc);
-      if (u + 1 == ug && ug < b) {  // group c.g ends inside the range
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          accA[i] = acc[i];
-          acc[i] = 0.f;
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < (K == 3 ? 2 : 1); ++h) w[h] = wn[h];
-      c = cn;
+      unit(u, std::integral_constant<int, NT>{}, tb);
     }
   }
   // every wave has finished decoding: the table's space holds the partials
@@ -247,15 +269,30 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_proj_rows1(ProjArgs p) {
       ro[blk] = *reinterpret_cast<const float2*>(q.rout + col0 + 128 * blk + 2 * lane);
       if (q.bias) bw[blk] = *reinterpret_cast<const uint32_t*>(q.bias + col0 + 128 * blk + 2 * lane);
     }
+    // which waves' partials hold group g (lane v reads wave v's slots), then
+    // every wave's partial requested at once and summed in wave order,
+    // skipping the waves without the group (one LDS round trip, not two per
+    // wave)
+    int slot_l = -1;
+    if (lane < kProjWaves) slot_l = s_grp[lane][0] == g ? 0 : (s_grp[lane][1] == g ? 1 : -1);
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int v = 0; v < kProjWaves; ++v) {
-      const int slot = s_grp[v][0] == g ? 0 : (s_grp[v][1] == g ? 1 : -1);
-      if (slot < 0) continue;
-      const float4 t = *reinterpret_cast<const float4*>(s_wp + (v * 2 + slot) * 256 + 4 * lane);
-      s.x = s.x + t.x;
-      s.y = s.y + t.y;
-      s.z = s.z + t.z;
-      s.w = s.w + t.w;
+#pragma unroll
+    for (int v0 = 0; v0 < kProjWaves; v0 += 8) {
+      float4 tv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int slot = __builtin_amdgcn_readlane(slot_l, v0 + j);
+        tv[j] = *reinterpret_cast<const float4*>(s_wp + ((v0 + j) * 2 + (slot > 0 ? 1 : 0)) * 256 +
+                                                 4 * lane);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (__builtin_amdgcn_readlane(slot_l, v0 + j) < 0) continue;
+        s.x = s.x + tv[j].x;
+        s.y = s.y + tv[j].y;
+        s.z = s.z + tv[j].z;
+        s.w = s.w + tv[j].w;
+      }
     }
     // the workgroups that publish for group g (its units [g TK, (g+1) TK));
     // a group inside one workgroup needs no hand-off
