@@ -37,6 +37,9 @@ constexpr int kProjWaves = 16;  // waves per workgroup
 constexpr int kProjMaxP = 8;    // units per wave
 constexpr int kProjMax = 4;     // projections per launch
 constexpr int kProjGroupCols = 256;
+// units each wave decodes by hash before the table barrier (measured on
+// MI355X, config 2 at batch 1: 1 beats 2 and 3)
+constexpr int kProjHashUnits = 1;
 
 // One projection of the launch.
 struct ProjOne {
@@ -221,12 +224,14 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_proj_rows1(ProjArgs p) {
     for (int h = 0; h < (K == 3 ? 2 : 1); ++h) w[h] = wn[h];
     c = cn;
   };
-  // the first unit is decoded by hash before the table is in LDS, so its
+  // the first units are decoded by hash before the table is in LDS, so their
   // decode runs while the table's pieces are still arriving (the table is
   // the hash's image and the step order is the same: bit-identical)
-  if (busy) {
-    prio_left(b - a);
-    unit(a, std::integral_constant<int, 0>{}, 0u);
+  const int uh = NT > 0 ? min(b, a + kProjHashUnits) : a;
+#pragma unroll 1
+  for (int u = a; u < uh; ++u) {
+    prio_left(b - u);
+    unit(u, std::integral_constant<int, 0>{}, 0u);
   }
   uint32_t tb = 0;
   if constexpr (NT > 0) {
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_proj_rows1(ProjArgs p) {
 
   if (busy) {
 #pragma unroll 1
-    for (int u = a + 1; u < b; ++u) {
+    for (int u = uh; u < b; ++u) {
       prio_left(b - u);
       unit(u, std::integral_constant<int, NT>{}, tb);
     }
