@@ -1580,8 +1580,16 @@ int moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, 
                                       p.S1, p1, s)) {
     return rc;
   }
-  hipLaunchKernelGGL(esc::k_moe_mid, dim3(I / 128, p.M), dim3(64), 0, s, p1, p.S1, p.M, I, ids,
-                     gu_rout, dn_rin, rs, xh2);
+  auto mid = [&](auto sc) {
+    hipLaunchKernelGGL((esc::k_moe_mid<decltype(sc)::value>), dim3(I / 128, p.M), dim3(64), 0, s,
+                       p1, p.S1, p.M, I, ids, gu_rout, dn_rin, rs, xh2);
+  };
+  switch (esc::splits_class(p.S1)) {
+    case 1: mid(std::integral_constant<int, 1>{}); break;
+    case 2: mid(std::integral_constant<int, 2>{}); break;
+    case 4: mid(std::integral_constant<int, 4>{}); break;
+    default: mid(std::integral_constant<int, 0>{});
+  }
   if (int rc = launched("k_moe_mid")) return rc;
   if (p.R) {
     if (int rc = group_rows(K_dn, use_lut, p.R, xh2, dn_code, rows, gexp, p.n_groups, p.M, I / 16,
@@ -1591,8 +1599,16 @@ int moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, 
                                       p2, s)) {
     return rc;
   }
-  hipLaunchKernelGGL(esc::k_moe_combine, dim3(H / 128, T), dim3(64), 0, s, p2, p.S2, p.M, H, ids,
-                     scores, top_k, dn_rout, rs, y);
+  auto combine = [&](auto sc) {
+    hipLaunchKernelGGL((esc::k_moe_combine<decltype(sc)::value>), dim3(H / 128, T), dim3(64), 0, s,
+                       p2, p.S2, p.M, H, ids, scores, top_k, dn_rout, rs, y);
+  };
+  switch (esc::splits_class(p.S2)) {
+    case 1: combine(std::integral_constant<int, 1>{}); break;
+    case 2: combine(std::integral_constant<int, 2>{}); break;
+    case 4: combine(std::integral_constant<int, 4>{}); break;
+    default: combine(std::integral_constant<int, 0>{});
+  }
   return launched("k_moe_combine");
 }
 

@@ -62,35 +62,61 @@ __device__ __forceinline__ half_t swiglu1(half_t g, half_t u) {
 }
 
 // Split-K sums, in z order, of the partials of several (row, column pair)
-// points at once: every point's loads of a 4-split chunk are issued before
-// any add, so the points' memory latencies overlap.
-template <int NP>
+// points at once.  SC > 0: S == SC splits, every load in one straight run
+// (no branch between them, so they issue back to back and their latencies
+// overlap); SC == 0: any S, in chunks of 4 whose loads are unconditional (the
+// split index clamped to S - 1) and whose adds take the splits below S.  v
+// starts at +0 and a sum of floats from +0 is never -0, so adding +0 for a
+// clamped split is exact.  (Loads under a condition each got a full wait for
+// the loads before them: one memory latency per load.)  rows[j] must be rows
+// of part (0 <= rows[j] < M).
+template <int NP, int SC>
 __device__ __forceinline__ void sum_splits(const float* __restrict__ part, int S, int M, int OC,
                                            const int* rows, const int* cols, float2* v) {
+  auto ld = [&](int z, int j) {
+    return *reinterpret_cast<const float2*>(part + ((size_t)z * M + rows[j]) * OC + cols[j]);
+  };
 #pragma unroll
   for (int j = 0; j < NP; ++j) v[j] = make_float2(0.f, 0.f);
-  for (int z0 = 0; z0 < S; z0 += 4) {
-    float2 pv[NP][4];
+  if constexpr (SC > 0) {
+    float2 pv[NP][SC];
 #pragma unroll
     for (int j = 0; j < NP; ++j)
 #pragma unroll
-      for (int zz = 0; zz < 4; ++zz)
-        if (rows[j] >= 0 && z0 + zz < S)
-          pv[j][zz] = *reinterpret_cast<const float2*>(
-              part + ((size_t)(z0 + zz) * M + rows[j]) * OC + cols[j]);
+      for (int z = 0; z < SC; ++z) pv[j][z] = ld(z, j);
 #pragma unroll
     for (int j = 0; j < NP; ++j)
 #pragma unroll
-      for (int zz = 0; zz < 4; ++zz)
-        if (rows[j] >= 0 && z0 + zz < S) {
-          v[j].x = v[j].x + pv[j][zz].x;
-          v[j].y = v[j].y + pv[j][zz].y;
+      for (int z = 0; z < SC; ++z) {
+        v[j].x = v[j].x + pv[j][z].x;
+        v[j].y = v[j].y + pv[j][z].y;
+      }
+  } else {
+    for (int z0 = 0; z0 < S; z0 += 4) {
+      float2 pv[NP][4];
+#pragma unroll
+      for (int j = 0; j < NP; ++j)
+#pragma unroll
+        for (int zz = 0; zz < 4; ++zz) pv[j][zz] = ld(min(z0 + zz, S - 1), j);
+#pragma unroll
+      for (int j = 0; j < NP; ++j)
+#pragma unroll
+        for (int zz = 0; zz < 4; ++zz) {
+          const bool in = z0 + zz < S;
+          v[j].x = v[j].x + (in ? pv[j][zz].x : 0.f);
+          v[j].y = v[j].y + (in ? pv[j][zz].y : 0.f);
         }
+    }
   }
 }
 
+// the split counts with a straight-line sum_splits; others take SC = 0
+__host__ __device__ constexpr int splits_class(int S) { return S == 1 || S == 2 || S == 4 ? S : 0; }
+
 // gate_up epilogue -> swiglu -> down input transform, one wave per
-// (row, 128-block of the intermediate): grid (I/128, M), block 64.
+// (row, 128-block of the intermediate): grid (I/128, M), block 64;
+// SC = splits_class(S).
+template <int SC>
 __global__ __launch_bounds__(64) void k_moe_mid(const float* __restrict__ part, int S, int M,
                                                 int I, const int* __restrict__ ids,
                                                 const float* __restrict__ gu_rout,
@@ -99,20 +125,23 @@ __global__ __launch_bounds__(64) void k_moe_mid(const float* __restrict__ part, 
   const int b = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
   const int e = ids[row];
   const int OC = 2 * I;
-  const float* ro = gu_rout + (size_t)e * OC;
   const int c = b * 128 + 2 * lane;
+  // the expert's scales of the lane's columns, requested before the partial
+  // sums so that their latency overlaps the partials'
+  const float2 rg = *reinterpret_cast<const float2*>(gu_rout + (size_t)e * OC + c);
+  const float2 ru = *reinterpret_cast<const float2*>(gu_rout + (size_t)e * OC + I + c);
+  const float2 ri = *reinterpret_cast<const float2*>(dn_rin + (size_t)e * I + c);
   // the gate and up partials of the lane's two columns, summed in z order
   const int rows2[2] = {row, row}, cols2[2] = {c, I + c};
   float2 gu[2];
-  sum_splits<2>(part, S, M, OC, rows2, cols2, gu);
+  sum_splits<2, SC>(part, S, M, OC, rows2, cols2, gu);
   h128_wave(gu[0].x, gu[0].y);
   h128_wave(gu[1].x, gu[1].y);
-  const half_t g0 = to_f16((gu[0].x * rs) * ro[c]), g1 = to_f16((gu[0].y * rs) * ro[c + 1]);
-  const half_t u0 = to_f16((gu[1].x * rs) * ro[I + c]), u1 = to_f16((gu[1].y * rs) * ro[I + c + 1]);
+  const half_t g0 = to_f16((gu[0].x * rs) * rg.x), g1 = to_f16((gu[0].y * rs) * rg.y);
+  const half_t u0 = to_f16((gu[1].x * rs) * ru.x), u1 = to_f16((gu[1].y * rs) * ru.y);
   const half_t h0 = swiglu1(g0, u0), h1 = swiglu1(g1, u1);
-  const float* ri = dn_rin + (size_t)e * I + c;
-  float v0 = (float)h0 * ri[0];
-  float v1 = (float)h1 * ri[1];
+  float v0 = (float)h0 * ri.x;
+  float v1 = (float)h1 * ri.y;
   h128_wave(v0, v1);
   uint16_t* o = xh2 + (size_t)row * I + c;
   o[0] = __builtin_bit_cast(uint16_t, to_f16(v0 * rs));
@@ -122,7 +151,8 @@ __global__ __launch_bounds__(64) void k_moe_mid(const float* __restrict__ part, 
 // down epilogue + weighted combine: y[t] = f16(sum_s f32(d16[t*k+s]) * f32(f16(score)))
 // summed in slot order in float32 (models/qwen3_5_moe.py:227-253).  The
 // partials of 8 slots are requested together, then transformed and summed
-// in slot order.  grid (H/128, T), block 64.
+// in slot order.  grid (H/128, T), block 64; SC = splits_class(S).
+template <int SC>
 __global__ __launch_bounds__(64) void k_moe_combine(const float* __restrict__ part, int S,
                                                     int M, int H, const int* __restrict__ ids,
                                                     const float* __restrict__ scores, int top_k,
@@ -132,32 +162,41 @@ __global__ __launch_bounds__(64) void k_moe_combine(const float* __restrict__ pa
   const int c = blk * 128 + 2 * lane;
   float a0 = 0.f, a1 = 0.f;
   for (int s0 = 0; s0 < top_k; s0 += 8) {
+    // slots past the token's last one re-read its last slot (every load
+    // unconditional) and are not summed
+    const int n = min(8, top_k - s0);
     int rows[8], cols[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      rows[j] = s0 + j < top_k ? tok * top_k + s0 + j : -1;
+      rows[j] = tok * top_k + s0 + min(j, n - 1);
       cols[j] = c;
     }
-    // every slot's output scales and weight are requested before the
-    // partial sums, so the slots' expert-dependent loads overlap
+    // slot j's expert and weight by lane j (one vector load for the 8
+    // slots, not a scalar round trip per slot), then every slot's output
+    // scales, requested before the partial sums so that the loads overlap
+    const int rl = tok * top_k + s0 + min(lane & 7, n - 1);
+    const int e_l = ids[rl];
+    const float w_l = (float)(half_t)scores[rl];
     float2 ro[8];
     float w[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (rows[j] >= 0) {
-        ro[j] = *reinterpret_cast<const float2*>(dn_rout + (size_t)ids[rows[j]] * H + c);
-        w[j] = (float)(half_t)scores[rows[j]];
-      }
-    float2 d[8];
-    sum_splits<8>(part, S, M, H, rows, cols, d);
+    for (int j = 0; j < 8; ++j) {
+      const int e = __builtin_amdgcn_readlane(e_l, j);
+      ro[j] = *reinterpret_cast<const float2*>(dn_rout + (size_t)e * H + c);
+      w[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_l), j));
+    }
+      float2 d[8];
+    sum_splits<8, SC>(part, S, M, H, rows, cols, d);
+    // no branch between the loads and their use (the compiler would sink
+    // each slot's loads into its branch, one latency per slot): the slots
+    // past n add +0 (a0, a1 start at +0 and are never -0, so this is exact)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      if (rows[j] < 0) break;  // uniform
       h128_wave(d[j].x, d[j].y);
       const half_t d0 = to_f16((d[j].x * rs) * ro[j].x);
       const half_t d1 = to_f16((d[j].y * rs) * ro[j].y);
-      a0 = a0 + (float)d0 * w[j];
-      a1 = a1 + (float)d1 * w[j];
+      a0 = a0 + (j < n ? (float)d0 * w[j] : 0.f);
+      a1 = a1 + (j < n ? (float)d1 * w[j] : 0.f);
     }
   }
   y[(size_t)tok * H + c] = __builtin_bit_cast(uint16_t, (half_t)a0);
