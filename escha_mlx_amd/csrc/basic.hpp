@@ -153,6 +153,8 @@ __global__ __launch_bounds__(256) void k_input_transform(const void* __restrict_
 
 // y = f16((H128(mid) * RS) * rout) [+ bias, added in f32 after the f16 round]
 // (escha_mlx/msl.py:919-949, 1050-1067; bias per dense.py:358-361).
+// EXP: row_expert is given (rout per row's expert).
+template <bool EXP>
 __global__ __launch_bounds__(256) void k_output_transform(const float* __restrict__ mid,
                                                           const float* __restrict__ rout,
                                                           const int* __restrict__ row_expert,
@@ -163,25 +165,31 @@ __global__ __launch_bounds__(256) void k_output_transform(const float* __restric
   const int blk = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = blk * 128 + 2 * lane;
   const int row0 = blockIdx.y * kTransformRows + RPW * wave;
-  float2 v[RPW];
+  // every load unconditional (rows past m re-read row m - 1 and are not
+  // stored), the bias (under its branch) first: a load under a branch waits
+  // for all the loads before it
+  const uint32_t bw = bias ? *reinterpret_cast<const uint32_t*>(bias + c) : 0u;
+  float2 v[RPW], r[RPW];
 #pragma unroll
-  for (int j = 0; j < RPW; ++j)
-    v[j] = *reinterpret_cast<const float2*>(mid + (size_t)min(row0 + j, m - 1) * OC + c);
+  for (int j = 0; j < RPW; ++j) {
+    const int row = min(row0 + j, m - 1);
+    v[j] = *reinterpret_cast<const float2*>(mid + (size_t)row * OC + c);
+    r[j] = *reinterpret_cast<const float2*>(rout + (EXP ? (size_t)row_expert[row] * OC : 0) + c);
+  }
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {
     const int row = row0 + j;
-    if (row >= m) continue;  // wave-uniform
     float v0 = v[j].x, v1 = v[j].y;
     h128_wave(v0, v1);
-    const float* r = rout + (row_expert ? (size_t)row_expert[row] * OC : 0) + c;
-    half_t y0 = to_f16((v0 * rs) * r[0]);
-    half_t y1 = to_f16((v1 * rs) * r[1]);
+    half_t y0 = to_f16((v0 * rs) * r[j].x);
+    half_t y1 = to_f16((v1 * rs) * r[j].y);
     if (bias) {
-      y0 = to_f16((float)y0 + (float)__builtin_bit_cast(half_t, bias[c]));
-      y1 = to_f16((float)y1 + (float)__builtin_bit_cast(half_t, bias[c + 1]));
+      y0 = to_f16((float)y0 + (float)__builtin_bit_cast(half_t, (uint16_t)(bw & 0xFFFFu)));
+      y1 = to_f16((float)y1 + (float)__builtin_bit_cast(half_t, (uint16_t)(bw >> 16)));
     }
-    *reinterpret_cast<uint32_t*>(out + (size_t)row * OC + c) =
-        (uint32_t)__builtin_bit_cast(uint16_t, y0) | ((uint32_t)__builtin_bit_cast(uint16_t, y1) << 16);
+    if (row < m)
+      *reinterpret_cast<uint32_t*>(out + (size_t)row * OC + c) =
+          (uint32_t)__builtin_bit_cast(uint16_t, y0) | ((uint32_t)__builtin_bit_cast(uint16_t, y1) << 16);
   }
 }
 

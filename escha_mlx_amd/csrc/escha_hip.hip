@@ -570,8 +570,12 @@ int esc_output_transform(const float* mid, const float* rout, const int32_t* row
   ESC_REQUIRE(m >= 0, "negative row count");
   if (m == 0) return ESC_OK;
   const int ry = (m + esc::kTransformRows - 1) / esc::kTransformRows;
-  hipLaunchKernelGGL(esc::k_output_transform, dim3(OC / 128, ry), dim3(256), 0, S(stream), mid,
-                     rout, row_expert, bias, m, OC, rs, out);
+  if (row_expert)
+    hipLaunchKernelGGL(esc::k_output_transform<true>, dim3(OC / 128, ry), dim3(256), 0, S(stream),
+                       mid, rout, row_expert, bias, m, OC, rs, out);
+  else
+    hipLaunchKernelGGL(esc::k_output_transform<false>, dim3(OC / 128, ry), dim3(256), 0, S(stream),
+                       mid, rout, row_expert, bias, m, OC, rs, out);
   return launched("k_output_transform");
 }
 

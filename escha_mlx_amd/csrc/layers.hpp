@@ -365,24 +365,29 @@ __device__ __forceinline__ void combine_pair(const LayersMoe& p, int l, int t, i
                         ((size_t)l * p.M + t * p.top_k) * (p.H / 2) + 128 * cp + lane;
   float s[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
   for (int k0 = 0; k0 < p.top_k; k0 += 8) {
+    // slots past top_k re-read the last slot and add +0 (s starts at +0 and
+    // is never -0, so this is exact): every load unconditional and issued
+    // together (a load under a branch waits for all the loads before it)
+    const int n = min(8, p.top_k - k0);
     uint32_t d8[2][8];
     float w8[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (k0 + j < p.top_k) {
-        d8[0][j] = ld_coherent_u32(rws + (size_t)(k0 + j) * (p.H / 2));
-        d8[1][j] = ld_coherent_u32(rws + (size_t)(k0 + j) * (p.H / 2) + 64);
-        w8[j] = (float)(half_t)as_global(L.scores)[t * p.top_k + k0 + j];
-      }
+    for (int j = 0; j < 8; ++j) {
+      const int k = k0 + min(j, n - 1);
+      d8[0][j] = ld_coherent_u32(rws + (size_t)k * (p.H / 2));
+      d8[1][j] = ld_coherent_u32(rws + (size_t)k * (p.H / 2) + 64);
+      w8[j] = (float)(half_t)as_global(L.scores)[t * p.top_k + k];
+    }
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (k0 + j < p.top_k) {
+    for (int j = 0; j < 8; ++j) {
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-          s[blk][0] = s[blk][0] + (float)__builtin_bit_cast(half_t, (uint16_t)d8[blk][j]) * w8[j];
-          s[blk][1] = s[blk][1] + (float)__builtin_bit_cast(half_t, (uint16_t)(d8[blk][j] >> 16)) * w8[j];
-        }
+      for (int blk = 0; blk < 2; ++blk) {
+        const float v0 = (float)__builtin_bit_cast(half_t, (uint16_t)d8[blk][j]) * w8[j];
+        const float v1 = (float)__builtin_bit_cast(half_t, (uint16_t)(d8[blk][j] >> 16)) * w8[j];
+        s[blk][0] = s[blk][0] + (j < n ? v0 : 0.f);
+        s[blk][1] = s[blk][1] + (j < n ? v1 : 0.f);
       }
+    }
   }
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk)
