@@ -260,11 +260,93 @@ __global__ __launch_bounds__(64) void k_route_topk(const float* __restrict__ log
 // Shared memory holds per-expert counts; E <= 4096.
 // The body runs in one block of 1024 threads (k_build_groups, or block 0 of
 // k_moe_prep).
+// Fast form when E * ceil(m / 64) <= kGroupMaskWords: a bit per (expert,
+// row) in LDS.  A row's rank within its expert is the popcount of its
+// expert's bits below it, an expert's count the popcount of all of them, so
+// every slot is written once (no clearing pass, no ordering between writers)
+// and the only serial step is the prefix over the experts' padded counts.
+constexpr int kGroupMaskWords = 4096;
+
+// exclusive prefix over the block (1024 threads) of one int per thread; the
+// block's total in *total
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s_wsum, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(inc, o);
+    if (lane >= o) inc += t;
+  }
+  if (lane == 63) s_wsum[wave] = inc;
+  __syncthreads();
+  int before = 0, all = 0;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+    before += w < wave ? s_wsum[w] : 0;
+    all += s_wsum[w];
+  }
+  *total = all;
+  return before + inc - v;
+}
+
+__device__ void build_groups_mask(const int* __restrict__ row_expert, int m, int E, int R,
+                                  int n_groups, int* __restrict__ rows_idx,
+                                  int* __restrict__ group_expert, int* s_start) {
+  __shared__ unsigned long long s_mask[kGroupMaskWords];  // [E][nw]
+  __shared__ int s_wsum[16];
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int nw = (m + 63) >> 6;
+  for (int i = tid; i < E * nw; i += nt) s_mask[i] = 0ull;
+  __syncthreads();
+  for (int r = tid; r < m; r += nt)
+    atomicOr(&s_mask[row_expert[r] * nw + (r >> 6)], 1ull << (r & 63));
+  __syncthreads();
+  // experts 4 tid .. 4 tid + 3: counts, padded counts, first slots
+  int cnt[4], pad[4], sum = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 4 * tid + j;
+    cnt[j] = 0;
+    if (e < E)
+      for (int w = 0; w < nw; ++w) cnt[j] += __popcll(s_mask[e * nw + w]);
+    pad[j] = (cnt[j] + R - 1) / R * R;
+    sum += pad[j];
+  }
+  int total;
+  int start = block_exclusive_scan(sum, s_wsum, &total);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 4 * tid + j;
+    if (e < E) {
+      s_start[e] = start;
+      // the expert's groups and its padding slots (= m)
+      for (int g = start / R; g < (start + pad[j]) / R; ++g) group_expert[g] = e;
+      for (int i = cnt[j]; i < pad[j]; ++i) rows_idx[start + i] = m;
+    }
+    start += pad[j];
+  }
+  // past the last expert: padding slots and groups of expert -1
+  for (int i = total + tid; i < n_groups * R; i += nt) rows_idx[i] = m;
+  for (int g = total / R + tid; g < n_groups; g += nt) group_expert[g] = -1;
+  __syncthreads();
+  // each row at its expert's first slot + the rows of its expert before it
+  for (int r = tid; r < m; r += nt) {
+    const int e = row_expert[r], w0 = r >> 6;
+    const unsigned long long* me = s_mask + e * nw;
+    int rank = __popcll(me[w0] & ((1ull << (r & 63)) - 1ull));
+    for (int w = 0; w < w0; ++w) rank += __popcll(me[w]);
+    rows_idx[s_start[e] + rank] = r;
+  }
+}
+
 __device__ void build_groups_block(const int* __restrict__ row_expert, int m, int E, int R,
                                    int n_groups, int* __restrict__ rows_idx,
                                    int* __restrict__ group_expert) {
-  __shared__ int s_cnt[4096];    // rows per expert, then rows placed so far
   __shared__ int s_start[4096];  // first padded slot of each expert
+  if ((long)E * ((m + 63) >> 6) <= kGroupMaskWords) {
+    build_groups_mask(row_expert, m, E, R, n_groups, rows_idx, group_expert, s_start);
+    return;
+  }
+  __shared__ int s_cnt[4096];    // rows per expert, then rows placed so far
   __shared__ int s_e[1024];      // one chunk of row_expert
   const int tid = threadIdx.x, nt = blockDim.x;
   for (int e = tid; e < E; e += nt) s_cnt[e] = 0;
