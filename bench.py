@@ -467,7 +467,7 @@ C2_PROJS = [("q", 5120, 5120, 2, True), ("k", 5120, 5120, 2, True), ("v", 5120, 
             ("down", 17408, 5120, 3, False)]
 C2_BYTES = sum(ic * oc * K_ // 8 for _, ic, oc, K_, _ in C2_PROJS)
 TRAFFIC_KERNELS = {1: ("k_linear_small",), 2: ("k_proj_rows1", "k_linear_small"),
-                   4: ("k_gemv_fast_rows", "k_moe_prep", "k_moe_mid", "k_moe_combine"),
+                   4: ("k_gemv_rows_table", "k_moe_prep", "k_moe_mid", "k_moe_combine"),
                    5: ("k_gemm_mma2", "k_input_transform")}
 
 
@@ -543,9 +543,11 @@ def c4_setup(torch, ops, n_layers):
 
     def step(i):
         R_ = recs[i % len(recs)]
+        # the table decode asked for: the grouped GEMMs run the persistent
+        # k_gemv_rows_table (outputs bit-identical to the hash kernels')
         ops.moe_expert_path(R_["x"], R_["ids"], R_["scores"], R_["gu_code"], R_["gu_rin"],
                             R_["gu_rout"], K, R_["dn_code"], R_["dn_rin"], R_["dn_rout"], K,
-                            ws=ws, out=R_["y"])
+                            ws=ws, out=R_["y"], lut=True)
     return recs, step
 
 
@@ -691,7 +693,7 @@ def c4_parity(recs, want, n_tokens: int = 4):
     a = float(np.abs(got.astype(np.float64) - want.astype(np.float64)).max())
     r = a / float(np.abs(want.astype(np.float64)).max())
     return {"checked": f"y rows 0-{n_tokens - 1} written by the timed esc_moe_expert_path call "
-                       "of layer-step 0 (k_moe_prep, k_gemv_fast_rows, k_moe_mid, "
+                       "of layer-step 0 (k_moe_prep, k_gemv_rows_table, k_moe_mid, "
                        "k_moe_combine; every token of the step routed together) against "
                        "oracle/ref_np.py moe_routed for those tokens",
             "max_abs_err": a, "max_rel_err": round(r, 6),
@@ -958,13 +960,14 @@ def bench_c4(args, torch, ops, traffic=(None, "not measured (--no-traffic)")):
            "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-           "dtype": "u32 codes -> f16 weights (hash), f32 accumulate",
+           "dtype": "u32 codes -> f16 weights (half the step pairs from the table in LDS, "
+                    "half by hash), f32 accumulate",
            "data": "synthetic, seeded logits [32,256] per layer, 8 layer stacks rotated",
            "config": {"workload": "config 4: E=256, H=2048, I=512, top-8, T=32 (m=256 rows)"},
            "distinct_experts_per_layer": distinct, "tok_s_per_layer": round(C4_T / (ms * 1e-3), 1),
            "roofline": roofline_block(
                "hbm", gbs, HBM_PEAK_GBS, "GB/s", traffic[0], traffic[1],
-               "k_moe_prep + k_gemv_fast_rows<2,false,8> (gate_up, down) + k_moe_mid + "
+               "k_moe_prep + k_gemv_rows_table<2,8> (gate_up, down) + k_moe_mid + "
                "k_moe_combine, one esc_moe_expert_path call per layer-step",
                bytes_per_step=int(b), avg_step_us=round(ms * 1e3, 2))}
     if not args.no_cpu:

@@ -290,7 +290,8 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_wsum, int* tot
 
 __device__ void build_groups_mask(const int* __restrict__ row_expert, int m, int E, int R,
                                   int n_groups, int* __restrict__ rows_idx,
-                                  int* __restrict__ group_expert, int* s_start) {
+                                  int* __restrict__ group_expert, int* s_start,
+                                  int* __restrict__ n_active) {
   __shared__ unsigned long long s_mask[kGroupMaskWords];  // [E][nw]
   __shared__ int s_wsum[16];
   const int tid = threadIdx.x, nt = blockDim.x;
@@ -325,6 +326,7 @@ __device__ void build_groups_mask(const int* __restrict__ row_expert, int m, int
     start += pad[j];
   }
   // past the last expert: padding slots and groups of expert -1
+  if (n_active && tid == 0) *n_active = total / R;
   for (int i = total + tid; i < n_groups * R; i += nt) rows_idx[i] = m;
   for (int g = total / R + tid; g < n_groups; g += nt) group_expert[g] = -1;
   __syncthreads();
@@ -338,12 +340,14 @@ __device__ void build_groups_mask(const int* __restrict__ row_expert, int m, int
   }
 }
 
+// n_active (when not null): the number of groups that hold rows.
 __device__ void build_groups_block(const int* __restrict__ row_expert, int m, int E, int R,
                                    int n_groups, int* __restrict__ rows_idx,
-                                   int* __restrict__ group_expert) {
+                                   int* __restrict__ group_expert,
+                                   int* __restrict__ n_active = nullptr) {
   __shared__ int s_start[4096];  // first padded slot of each expert
   if ((long)E * ((m + 63) >> 6) <= kGroupMaskWords) {
-    build_groups_mask(row_expert, m, E, R, n_groups, rows_idx, group_expert, s_start);
+    build_groups_mask(row_expert, m, E, R, n_groups, rows_idx, group_expert, s_start, n_active);
     return;
   }
   __shared__ int s_cnt[4096];    // rows per expert, then rows placed so far
@@ -386,6 +390,7 @@ __device__ void build_groups_block(const int* __restrict__ row_expert, int m, in
   for (int e = tid; e < E; e += nt) {
     const int ng = (s_cnt[e] + R - 1) / R;
     for (int g = 0; g < ng; ++g) group_expert[s_start[e] / R + g] = e;
+    if (n_active && e == E - 1) *n_active = s_start[e] / R + ng;
     s_cnt[e] = 0;
   }
   __syncthreads();

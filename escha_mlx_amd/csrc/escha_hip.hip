@@ -1175,7 +1175,7 @@ int moe_input(const uint16_t* x, const int32_t* ids, int top_k, const float* rin
 
 struct MoePlan {
   int M, S1, S2, R, n_groups;
-  size_t off_xh, off_p1, off_xh2, off_p2, off_rows, off_gexp, total;
+  size_t off_xh, off_p1, off_xh2, off_p2, off_rows, off_gexp, off_nact, total;
 };
 // base: bytes at the start of the workspace left to the caller (the
 // no-allocation variant keeps its counters there).
@@ -1200,7 +1200,8 @@ MoePlan moe_plan(int T, int top_k, int E, int H, int I, int K_gu, int K_dn, size
   p.off_p2 = al(p.off_xh2 + (size_t)p.M * I * 2);
   p.off_rows = al(p.off_p2 + (size_t)p.S2 * p.M * H * 4);
   p.off_gexp = al(p.off_rows + (size_t)p.n_groups * p.R * 4);
-  p.total = al(p.off_gexp + (size_t)p.n_groups * 4);
+  p.off_nact = al(p.off_gexp + (size_t)p.n_groups * 4);
+  p.total = al(p.off_nact + 4);
   return p;
 }
 
@@ -1221,14 +1222,34 @@ struct GroupRowsF {
   }
 };
 
+// The grouped GEMM with the table decode: the persistent k_gemv_rows_table
+// (one workgroup per CU, the table staged once), its item count from the
+// groups build_groups filled (nact, on the device).
+template <int K>
+int launch_rows_table(const uint16_t* xh, const uint32_t* code, const int* rows, const int* gexp,
+                      const int* nact, int M, int TK, int TN, int S, float* part, hipStream_t s) {
+  static std::once_flag once;
+  static hipError_t err = hipSuccess;
+  std::call_once(once, [] {
+    err = hipFuncSetAttribute((const void*)esc::k_gemv_rows_table<K, kMoeGroupRows>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 65536 * 2);
+  });
+  if (int rc = hip_check(err, "hipFuncSetAttribute")) return rc;
+  hipLaunchKernelGGL((esc::k_gemv_rows_table<K, kMoeGroupRows>), dim3(device_cus()), dim3(1024),
+                     65536 * 2, s, xh, code, rows, gexp, nact, M, TK, TN, TK / S, S, part);
+  return launched("k_gemv_rows_table");
+}
+
 int group_rows(int K, int lut, int R, const uint16_t* xh, const uint32_t* code, const int* rows,
-               const int* gexp, int n_groups, int M, int TK, int TN, int S, float* part,
-               hipStream_t s) {
-  if (K == 2)
-    return lut ? GroupRowsF<2, true>::run(R, xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s)
-               : GroupRowsF<2, false>::run(R, xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s);
-  return lut ? GroupRowsF<3, true>::run(R, xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s)
-             : GroupRowsF<3, false>::run(R, xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s);
+               const int* gexp, const int* nact, int n_groups, int M, int TK, int TN, int S,
+               float* part, hipStream_t s) {
+  if (lut) {
+    if (R != kMoeGroupRows) return fail(ESC_EINVAL, "rows per expert group %d", R);
+    return K == 2 ? launch_rows_table<2>(xh, code, rows, gexp, nact, M, TK, TN, S, part, s)
+                  : launch_rows_table<3>(xh, code, rows, gexp, nact, M, TK, TN, S, part, s);
+  }
+  return K == 2 ? GroupRowsF<2, false>::run(R, xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s)
+                : GroupRowsF<3, false>::run(R, xh, code, rows, gexp, n_groups, M, TK, TN, S, part, s);
 }
 
 // One-launch path (fused.hpp).  Latency mode: small items over the whole GPU
@@ -1569,14 +1590,15 @@ int moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, 
   const float rs = esc::kRS;
   int* rows = reinterpret_cast<int*>(w + p.off_rows);
   int* gexp = reinterpret_cast<int*>(w + p.off_gexp);
+  int* nact = reinterpret_cast<int*>(w + p.off_nact);
   if (p.R) {
     // input transform and expert grouping in one launch
     const int waves = H / 128 * p.M;
     hipLaunchKernelGGL(esc::k_moe_prep, dim3(1 + (waves + 15) / 16), dim3(1024), 0, s, x, ids,
-                       top_k, gu_rin, H, rs, xh, p.M, E, p.R, p.n_groups, rows, gexp);
+                       top_k, gu_rin, H, rs, xh, p.M, E, p.R, p.n_groups, rows, gexp, nact);
     if (int rc = launched("k_moe_prep")) return rc;
-    if (int rc = group_rows(K_gu, use_lut, p.R, xh, gu_code, rows, gexp, p.n_groups, p.M, H / 16,
-                            2 * I / 16, p.S1, p1, s))
+    if (int rc = group_rows(K_gu, use_lut, p.R, xh, gu_code, rows, gexp, nact, p.n_groups, p.M,
+                            H / 16, 2 * I / 16, p.S1, p1, s))
       return rc;
   } else if (int rc = moe_input(x, ids, top_k, gu_rin, H, rs, xh, p.M, s)) {
     return rc;
@@ -1596,8 +1618,8 @@ int moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, 
   }
   if (int rc = launched("k_moe_mid")) return rc;
   if (p.R) {
-    if (int rc = group_rows(K_dn, use_lut, p.R, xh2, dn_code, rows, gexp, p.n_groups, p.M, I / 16,
-                            H / 16, p.S2, p2, s))
+    if (int rc = group_rows(K_dn, use_lut, p.R, xh2, dn_code, rows, gexp, nact, p.n_groups, p.M,
+                            I / 16, H / 16, p.S2, p2, s))
       return rc;
   } else if (int rc = by_k_lut<FastF>(K_dn, use_lut, xh2, dn_code, ids, p.M, I / 16, H / 16, p.S2,
                                       p2, s)) {

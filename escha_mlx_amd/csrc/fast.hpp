@@ -624,6 +624,85 @@ __device__ __forceinline__ void fast_tile_mix3(const LaneWords<3>& lw, uint32_t 
   }
 }
 
+// mma_tile with the table decode from the 65,536-entry table in LDS (at byte
+// address tb): the first register pair of every A operand (m = 0, as in
+// mma_a_operand<K, true>) from the table, the second by hash.  In chunks of
+// CH operands: every table read of the chunk is issued first (byte
+// addresses by v_mad_u32_u16: the state's half selected by op_sel, times 2,
+// plus the base), then the chunk's hash work, so the reads' latency is spent
+// on the hash; then the operands are packed and multiplied in mma_tile's
+// order.  The table is the hash's image: bit-identical to mma_tile.
+template <int K, int CH = 4>
+__device__ __forceinline__ void mma_tile_mix(const LaneWords<K>& lw, uint32_t wprev, u32x4_t b0,
+                                             u32x4_t b1, f32x4_t* acc, uint32_t tb) {
+  using G = Geo<K>;
+  const uint32_t clo = kClo, chi = kChi;
+  constexpr int NO = 2 * G::NCOL;  // operands (ci, P), ci major
+  static_assert(NO % CH == 0, "");
+#pragma unroll
+  for (int o0 = 0; o0 < NO; o0 += CH) {
+    uint32_t t[CH][4];  // [a[0] lo, a[0] hi, a[1] lo, a[1] hi] f16 values
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int o = o0 + j, ci = o >> 1, P = o & 1;
+      const int ua = mma_step<K>(0, 2 * P, ci), ub = mma_step<K>(0, 2 * P + 1, ci);
+      uint32_t ad[4];
+      if constexpr (K == 2) {
+        // a[0] = [w of ua | w of ub] from the windows' high halves, a[1] from the low
+        const uint32_t pa = window2(lw, wprev, ua), pb = window2(lw, wprev, ub);
+        __asm__("v_mad_u32_u16 %0, %1, 2, %2 op_sel:[1,0,0,0]" : "=v"(ad[0]) : "v"(pa), "v"(tb));
+        __asm__("v_mad_u32_u16 %0, %1, 2, %2 op_sel:[1,0,0,0]" : "=v"(ad[1]) : "v"(pb), "v"(tb));
+        __asm__("v_mad_u32_u16 %0, %1, 2, %2" : "=v"(ad[2]) : "v"(pa), "v"(tb));
+        __asm__("v_mad_u32_u16 %0, %1, 2, %2" : "=v"(ad[3]) : "v"(pb), "v"(tb));
+      } else {
+        const uint32_t sa0 = state3(lw, wprev, ua), sb0 = state3(lw, wprev, ub);
+        const uint32_t sa1 = state3(lw, wprev, ua + 8), sb1 = state3(lw, wprev, ub + 8);
+        __asm__("v_mad_u32_u16 %0, %1, 2, %2" : "=v"(ad[0]) : "v"(sa0), "v"(tb));
+        __asm__("v_mad_u32_u16 %0, %1, 2, %2" : "=v"(ad[1]) : "v"(sb0), "v"(tb));
+        __asm__("v_mad_u32_u16 %0, %1, 2, %2" : "=v"(ad[2]) : "v"(sa1), "v"(tb));
+        __asm__("v_mad_u32_u16 %0, %1, 2, %2" : "=v"(ad[3]) : "v"(sb1), "v"(tb));
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) t[j][r] = lds_u16(ad[r]);
+    }
+    // the hash reads its code words through this barrier (left alone, the
+    // compiler hoists the hash above the reads and waits on each read at once)
+    LaneWords<K> lh = lw;
+    uint32_t wph = wprev;
+#pragma unroll
+    for (int r = 0; r < G::WPL; ++r) __asm__ volatile("" : "+v"(lh.w[r]) : : "memory");
+    __asm__ volatile("" : "+v"(wph) : : "memory");
+    uint32_t h[CH][2];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int o = o0 + j, ci = o >> 1, P = o & 1;
+      const int ua = mma_step<K>(2, 2 * P, ci), ub = mma_step<K>(2, 2 * P + 1, ci);
+      if constexpr (K == 2) {
+        const uint32_t pa = window2(lh, wph, ua), pb = window2(lh, wph, ub);
+        h[j][0] = halves_sum2(mask_xor(hash_x<true>(pa, clo, chi)), mask_xor(hash_x<true>(pb, clo, chi)));
+        h[j][1] = halves_sum2(mask_xor(hash_x<false>(pa, clo, chi)), mask_xor(hash_x<false>(pb, clo, chi)));
+      } else {
+        const uint32_t sa0 = state3(lh, wph, ua), sb0 = state3(lh, wph, ub);
+        const uint32_t sa1 = state3(lh, wph, ua + 8), sb1 = state3(lh, wph, ub + 8);
+        h[j][0] = halves_sum2(mask_xor(hash_x<false>(sa0, clo, chi)), mask_xor(hash_x<false>(sb0, clo, chi)));
+        h[j][1] = halves_sum2(mask_xor(hash_x<false>(sa1, clo, chi)), mask_xor(hash_x<false>(sb1, clo, chi)));
+      }
+      __asm__ volatile("" : "+v"(h[j][0]), "+v"(h[j][1]));
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int o = o0 + j, ci = o >> 1, P = o & 1;
+      __asm__ volatile("" : "+v"(t[j][0]), "+v"(t[j][1]), "+v"(t[j][2]), "+v"(t[j][3]));
+      u32x4_t a;
+      a[0] = t[j][0] | (t[j][1] << 16);
+      a[1] = t[j][2] | (t[j][3] << 16);
+      a[2] = h[j][0];
+      a[3] = h[j][1];
+      acc[ci] = mma16(a, P ? b1 : b0, acc[ci]);
+    }
+  }
+}
+
 // One wave's share of the split-K row-group GEMM on the matrix core: tiles
 // [tile0, tile0 + 16/LPT) of the stream at code_e over kt [z*KS, (z+1)*KS),
 // B column c = input row xr_c (the lane's row, xr), accumulated into acc.

@@ -44,13 +44,143 @@ __global__ __launch_bounds__(1024) void k_moe_prep(const uint16_t* __restrict__ 
                                                    const float* __restrict__ rin, int H, float rs,
                                                    uint16_t* __restrict__ xh, int m, int E, int R,
                                                    int n_groups, int* __restrict__ rows_idx,
-                                                   int* __restrict__ group_expert) {
+                                                   int* __restrict__ group_expert,
+                                                   int* __restrict__ n_active) {
   if (blockIdx.x == 0) {
-    build_groups_block(ids, m, E, R, n_groups, rows_idx, group_expert);
+    build_groups_block(ids, m, E, R, n_groups, rows_idx, group_expert, n_active);
     return;
   }
   const int nhb = H / 128, w = (blockIdx.x - 1) * 16 + (threadIdx.x >> 6);
   if (w < nhb * m) moe_input_wave(x, ids, top_k, rin, H, rs, xh, w % nhb, w / nhb);
+}
+
+// The grouped split-K GEMM of k_gemv_fast_rows with the table decode, as a
+// persistent launch: one workgroup of 16 waves per CU requests the
+// 65,536-entry table into LDS once (LDS DMA; a short-lived workgroup that
+// stages 128 KiB for one wave-step range of a few rows costs more than the
+// table saves), then each wave walks a contiguous range of wave-items.  A
+// wave-item is one wave's share of k_gemv_fast_rows -- TPS tiles (tw) of
+// group g over the KS kt of split z -- and writes the same partial slice
+// part[z][row][16 TPS tw ..], so the consumers are unchanged.  Items run
+// (g, z, tw) with tw fastest, over the n_active groups build_groups filled
+// (groups past them belong to no expert).  The wave walks its items' steps
+// as one sequence: each step requests the next step's code and inputs, the
+// next item's first step included, and each item's group and rows are
+// loaded one item ahead.  Table pairs are the table's image of the hash and
+// the MFMAs run in mma_tile's order: the partials are bit-identical to
+// k_gemv_fast_rows'.  grid: one workgroup per CU, block 1024, dynamic LDS
+// 128 KiB.
+// One wave-item's loaded values (both per lane: the expert is read with a
+// vector load so that nothing waits for it until the item's first code is
+// requested, one item later) and its place.
+struct RowsItem {
+  int e, row;  // the group's expert, the lane's row (M: padding)
+  int z, tw;   // split, wave tile
+};
+
+template <int K, int R>
+__global__ __launch_bounds__(1024) void k_gemv_rows_table(const uint16_t* __restrict__ xh,
+                                                          const uint32_t* __restrict__ code,
+                                                          const int* __restrict__ rows_idx,
+                                                          const int* __restrict__ group_expert,
+                                                          const int* __restrict__ n_active, int M,
+                                                          int TK, int TN, int KS, int S,
+                                                          float* __restrict__ part) {
+  static_assert(R >= 1 && R <= 16, "");
+  using G = Geo<K>;
+  constexpr int TPS = 16 / G::LPT;
+  extern __shared__ uint16_t s_tab[];
+  table_dma(s_tab);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int NTW = TN / TPS;  // wave tiles per group row
+  const long n = (long)*n_active * S * NTW;
+  const long W = (long)gridDim.x * 16, gw = (long)blockIdx.x * 16 + wave;
+  const int i0 = (int)(n * gw / W), i1 = (int)(n * (gw + 1) / W);
+  const int gk = lane >> 4, c = lane & 15, tc = c / G::LPT, q = lane % G::LPT;
+  const int src = (lane & ~(G::LPT - 1)) | ((lane + G::LPT - 1) & (G::LPT - 1));
+  const int rc = c < R ? c : R - 1;  // the lane's B column: row min(c, R-1) of the group
+  const size_t kstride = (size_t)TN * (8 * K);
+  const size_t estride = (size_t)TK * TN * (8 * K);
+  const int last_i = (int)max(n - 1, 0L);
+  auto item = [&](int i) {
+    RowsItem it;
+    it.tw = i % NTW;
+    const int gz = i / NTW, g = gz / S;
+    it.z = gz % S;
+    // g as a per-lane value (an identity DPP move): the expert is loaded
+    // with a vector load, not a scalar one that the next LDS wait would
+    // also wait for
+    const int gv = __builtin_amdgcn_update_dpp(0, g, 0xE4, 0xF, 0xF, false);
+    it.e = group_expert[gv];
+    it.row = rows_idx[g * R + rc];
+    return it;
+  };
+  // the lane's code words at kt 0 and its input row
+  auto code_of = [&](const RowsItem& it) {
+    return code + (size_t)it.e * estride + (size_t)(TPS * it.tw + tc) * (8 * K) + q * G::WPL;
+  };
+  auto x_of = [&](const RowsItem& it) {
+    return reinterpret_cast<const uint4*>(xh + (size_t)(it.row < M ? it.row : 0) * TK * 16);
+  };
+  // this wave's first item, the next and the one after (each item's values
+  // are loaded three items ahead: the compiler computes an item's pointers
+  // where the item before it starts)
+  RowsItem cur = item(min(i0, last_i)), nxt = item(min(i0 + 1, last_i));
+  RowsItem pend = item(min(i0 + 2, last_i));
+  const int nsteps = KS / 4;
+  const uint32_t* lp = code_of(cur);
+  const uint4* xq = x_of(cur);
+  int kt = cur.z * KS + gk;
+  LaneWords<K> w = load_lane_words_nt<K>(lp + (size_t)kt * kstride);
+  uint4 xa = xq[2 * kt], xb = xq[2 * kt + 1];
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's table pieces
+  __syncthreads();
+  const uint32_t tb = (uint32_t)(size_t)s_tab;
+  if (i0 >= i1) return;
+  f32x4_t acc[G::NCOL];
+#pragma unroll
+  for (int j = 0; j < G::NCOL; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int i = i0; i < i1; ++i) {
+    const uint32_t* lp_next = code_of(nxt);
+    const uint4* xq_next = x_of(nxt);
+    const int kt_next = nxt.z * KS + gk;
+    RowsItem p3;
+    // one wave-step: the next step's code and inputs requested (this item's
+    // k + 1, or the next item's first; the last item's re-reads its own: in
+    // bounds, unused), then the decode and the MFMAs.  The first step also
+    // requests item i + 3's values, just before its own loads: the wait for
+    // those covers them, where a load of their own at the item's start would
+    // be waited for at the first step
+    auto step = [&](int k, bool first) {
+      if (first) p3 = item(min(i + 3, i1 - 1));
+      const bool last = k + 1 == nsteps;
+      const uint32_t* lpn = last ? lp_next : lp;
+      const uint4* xqn = last ? xq_next : xq;
+      const int ktn = last ? kt_next : kt + 4;
+      const LaneWords<K> wn = load_lane_words_nt<K>(lpn + (size_t)ktn * kstride);
+      const uint4 na = xqn[2 * ktn], nb = xqn[2 * ktn + 1];
+      const uint32_t wprev = __shfl(w.w[G::WPL - 1], src);
+      mma_tile_mix<K>(w, wprev, __builtin_bit_cast(u32x4_t, xa), __builtin_bit_cast(u32x4_t, xb),
+                      acc, tb);
+      w = wn;
+      xa = na;
+      xb = nb;
+      lp = lpn;
+      xq = xqn;
+      kt = ktn;
+    };
+    step(0, true);
+#pragma unroll 1
+    for (int k = 1; k < nsteps; ++k) step(k, false);
+    if (c < R && cur.row < M)
+      mma_store<K>(acc, gk, part + ((size_t)cur.z * M + cur.row) * TN * 16 + 16 * TPS * cur.tw);
+#pragma unroll
+    for (int j = 0; j < G::NCOL; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    cur = nxt;
+    nxt = pend;
+    pend = p3;
+  }
 }
 
 // h = f16(f16(silu(g)) * u) with silu(g) = g / (1 + exp(-g)) in float32

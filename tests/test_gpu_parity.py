@@ -451,6 +451,33 @@ def test_moe_multi_launch_path_vs_oracle(E, T, K_gu, K_dn, H, monkeypatch):
     assert torch.equal(blk(x, ids, sc), y)
 
 
+@pytest.mark.parametrize("E,T,K_gu,K_dn,H,I", [(64, 9, 2, 2, 256, 128), (64, 12, 3, 2, 512, 256),
+                                                 (32, 16, 2, 3, 384, 128), (256, 32, 2, 2, 2048, 512)],
+                         ids=["k2", "gate_up_k3", "down_k3", "config4_shape"])
+def test_moe_grouped_table_path_bit_identical_to_hash(E, T, K_gu, K_dn, H, I, monkeypatch):
+    """The grouped chain with the table asked for runs the persistent
+    k_gemv_rows_table (one workgroup per CU, the table staged once, waves over
+    contiguous wave-item ranges): its partials are the hash kernel's bit for
+    bit, so the whole path's output is; and both are within tolerance of the
+    oracle.  Repeat calls on one workspace agree."""
+    k = 8
+    c = _moe_case(E, H, I, K_gu, K_dn, T, k, 40 + E + T)
+    ids, sc = ops().route_topk(torch.from_numpy(c["logits"]).to(DEV), k)
+    x = torch.from_numpy(c["x"]).to(DEV)
+    args = [dcode(c["gu_code"]), torch.from_numpy(c["gu_rin"]).to(DEV),
+            torch.from_numpy(c["gu_rout"]).to(DEV), K_gu, dcode(c["dn_code"]),
+            torch.from_numpy(c["dn_rin"]).to(DEV), torch.from_numpy(c["dn_rout"]).to(DEV), K_dn]
+    ws = torch.zeros(ops().moe_expert_path_workspace(T, k, E, H, I), dtype=torch.uint8, device=DEV)
+    y_hash = ops().moe_expert_path(x, ids, sc, *args, lut=False, ws=ws)
+    y_tab = ops().moe_expert_path(x, ids, sc, *args, lut=True, ws=ws)
+    assert torch.equal(y_tab, y_hash)
+    assert torch.equal(ops().moe_expert_path(x, ids, sc, *args, lut=True, ws=ws), y_tab)
+    ids_np, sc_np = ids.cpu().numpy(), sc.cpu().numpy()
+    want = _oracle_moe(c, ids_np, sc_np, E, H, I, K_gu, K_dn, np.unique(ids_np)).astype(np.float32)
+    got = y_tab.cpu().numpy().astype(np.float32)
+    assert np.abs(got - want).max() / np.abs(want).max() < 5e-3
+
+
 def test_moe_one_launch_status_and_reuse(monkeypatch):
     """The one persistent launch (k_moe_fused: H or I not a multiple of 512)
     never hits its bounded wait and leaves its counters zero: repeated calls on
