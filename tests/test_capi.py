@@ -323,6 +323,7 @@ def test_no_float_atomics_in_kernels():
     allowed = {
         ("basic.hpp", "atomicAdd(&s_cnt[row_expert[r]], 1)"),   # int LDS expert counts
         ("basic.hpp", "atomicAdd(&s_cnt[e], 1)"),
+        ("basic.hpp", "atomicOr(&s_mask[row_expert[r] * nw + (r >> 6)], 1ull << (r & 63))"),  # u64 bits
         ("fused.hpp", "__hip_atomic_fetch_add(p, v,"),          # add_publish(int* p, int v)
         ("fused.hpp", "__hip_atomic_compare_exchange_strong(p, &expected, 1,"),  # claim(int* p)
         ("fused.hpp", "atomicOr(p.err, 1)"),                      # int flags
