@@ -55,14 +55,14 @@ def _device(c, k):
     return d
 
 
-def _both(d, K=2):
+def _both(d, K=2, lut=None):
     """(static entry point's output, regular entry point's output)."""
     from escha_mlx_amd import ops
     args = (d["x"], d["ids"], d["scores"], d["gu_code"], d["gu_rin"], d["gu_rout"], K,
             d["dn_code"], d["dn_rin"], d["dn_rout"], K)
     y_s = torch.full(tuple(d["x"].shape), float("nan"), dtype=torch.float16, device=DEV)
-    ops.moe_expert_path_static(*args, out=y_s)
-    y_r = ops.moe_expert_path(*args)
+    ops.moe_expert_path_static(*args, out=y_s, lut=lut)
+    y_r = ops.moe_expert_path(*args, lut=lut)
     return y_s, y_r
 
 
@@ -137,6 +137,24 @@ def test_static_grouped_shape_between_fused_shapes():
     for name, d in (("two-launch T=1", fused), ("grouped T=16", grouped), ("persistent T=2", pers),
                     ("grouped again", grouped), ("two-launch again", fused)):
         y_s, y_r = _both(d)
+        torch.cuda.synchronize()
+        assert not torch.isnan(y_s.float()).any(), name
+        assert torch.equal(y_s.view(torch.int16), y_r.view(torch.int16)), name
+
+
+def test_static_grouped_table_shape_equals_workspace_path():
+    """The grouped chain with the table asked for (the persistent
+    k_gemv_rows_table, whose item count it reads from the scratch) through
+    the static array, bit-identical to the workspace entry point, between two
+    calls of the grouped chain by hash."""
+    from escha_mlx_amd import ops
+    ops.init()
+    k = 8
+    grouped = _device(_case(8, 512, 256, 16, k, 913), k)
+    other = _device(_case(16, 512, 256, 16, k, 914), k)  # within the 4 MiB scratch
+    for name, d, lut in (("hash E=8", grouped, False), ("table E=16", other, True),
+                         ("table E=8", grouped, True), ("hash E=16", other, False)):
+        y_s, y_r = _both(d, lut=lut)
         torch.cuda.synchronize()
         assert not torch.isnan(y_s.float()).any(), name
         assert torch.equal(y_s.view(torch.int16), y_r.view(torch.int16)), name
