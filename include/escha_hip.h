@@ -287,7 +287,10 @@ int esc_q8_embed(const int32_t* ids, int T, const int8_t* w8, const float* scale
  * workgroup that gives up writes NaN outputs and raises a device-wide flag,
  * and the next call on the device that would take that launch returns
  * ESC_ETIMEOUT without running (the flag is read without a synchronisation;
- * esc_moe_status reads it at once).
+ * esc_moe_status reads it at once).  use_lut: the decode table (the hash's
+ * image, same outputs) where a kernel uses it; above 64 routed rows with at
+ * least one row per expert the grouped GEMMs then run as one persistent
+ * launch that stages the table once per CU.
  * Replaces EschaSparseMoeBlock._expert_path (escha_mlx/models/qwen3_5_moe.py:207-253). */
 size_t esc_moe_expert_path_workspace(int T, int top_k, int E, int H, int I);
 int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, int T,
