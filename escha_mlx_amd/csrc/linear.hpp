@@ -94,9 +94,12 @@ __device__ __forceinline__ void linear_small_body(const LinearSmallArgs& a, int 
   const int kt0 = kMma ? z * KS + gk : z * KS + kl0;
   const int nsteps = KS / 4, kstep = kMma ? 4 : 1;
   // the first step's code is requested before anything else, so its latency
-  // overlaps the input transform
-  LaneWords<K> cur{};
-  if (valid) cur = load_lane_words_nt<K>(lp + (size_t)kt0 * kstride);
+  // overlaps the input transform; lanes past the last tile read the code's
+  // first words instead (in bounds, never stored) -- a load under a branch
+  // would be waited for where the branch ends, before the inputs are
+  // requested
+  const uint32_t* lp0 = valid ? lp + (size_t)kt0 * kstride : code;
+  LaneWords<K> cur = load_lane_words_nt<K>(lp0);
   // 1. input transform: xh = f16(H128(f32(x) * rin) * RS) per (row, block);
   // wave w takes items w, w + 4, ...; with several rows it requests up to 8
   // items' inputs before transforming them, so one memory round trip serves
