@@ -95,6 +95,11 @@ __global__ __launch_bounds__(1024) void k_gemv_rows_table(const uint16_t* __rest
   const int lane = threadIdx.x & 63;
   const int NTW = TN / TPS;  // wave tiles per group row
   const long n = (long)*n_active * S * NTW;
+  if (n <= 0) {
+    // no filled group (the items below would read group 0, an expert of -1)
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
   const long W = (long)gridDim.x * 16, gw = (long)blockIdx.x * 16 + wave;
   const int i0 = (int)(n * gw / W), i1 = (int)(n * (gw + 1) / W);
   const int gk = lane >> 4, c = lane & 15, tc = c / G::LPT, q = lane % G::LPT;
@@ -102,7 +107,7 @@ __global__ __launch_bounds__(1024) void k_gemv_rows_table(const uint16_t* __rest
   const int rc = c < R ? c : R - 1;  // the lane's B column: row min(c, R-1) of the group
   const size_t kstride = (size_t)TN * (8 * K);
   const size_t estride = (size_t)TK * TN * (8 * K);
-  const int last_i = (int)max(n - 1, 0L);
+  const int last_i = (int)(n - 1);
   auto item = [&](int i) {
     RowsItem it;
     it.tw = i % NTW;
