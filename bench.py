@@ -1223,6 +1223,22 @@ def main():
         ms_c = timed(torch, chained, args.steps, args.warmup, stream)
         gbs_c = BYTES_TOKEN_LAYER * nl / (ms_c * 1e-3) / 1e9
 
+        # the same step with each token-layer as one launch
+        # (esc_moe_expert_path_one_launch; a workspace of its own: the two
+        # forms lay out their counters differently)
+        ws1 = torch.zeros_like(ws)
+
+        def chained_one(i):
+            x = layers[0]["x"]
+            for L in routes[i % ROUTE_SETS]:
+                ops.moe_expert_path(x, L["ids"], L["scores"], L["gu_code"], L["gu_rin"],
+                                    L["gu_rout"], K, L["dn_code"], L["dn_rin"], L["dn_rout"], K,
+                                    ws=ws1, out=L["y"], one_launch=True)
+                x = L["y"]
+
+        ms_c1 = timed(torch, chained_one, args.steps, args.warmup, stream)
+        gave_up = ops.moe_status(ws1, 1, TOP_K, H, I)
+
         # the same decode step replayed as one HIP graph per route set (the
         # host's launch issue taken out of the chain)
         def chained_fresh(i):
@@ -1240,6 +1256,8 @@ def main():
             "chained_ms_per_token": round(ms_c, 4),
             "chained_us_per_token_layer": round(ms_c * 1e3 / nl, 3),
             "chained_graph_us_per_token_layer": round(ms_g * 1e3 / nl, 3),
+            "chained_one_launch_us_per_token_layer": round(ms_c1 * 1e3 / nl, 3),
+            "chained_one_launch_wait_gave_up": bool(gave_up),
             "chained_gbs": round(gbs_c, 2),
         })
         if "value" not in result:

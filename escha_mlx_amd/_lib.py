@@ -73,6 +73,8 @@ SIGNATURES = {
     "esc_moe_expert_path_layers": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
     "esc_moe_expert_path": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _P,
                                  _I, _I, _P, _P, _Z, _P]),
+    "esc_moe_expert_path_one_launch": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P,
+                                            _P, _P, _I, _I, _P, _P, _Z, _P]),
 }
 
 _lib = None

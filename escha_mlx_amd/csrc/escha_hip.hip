@@ -1276,6 +1276,13 @@ constexpr int kKtaLayers = 16, kKtbLayers = 16;
 // items are 128-column blocks over all 32 kt (k_moe_down_blocks)
 constexpr int kKtaSingle = 16, kKtbSingle = 16;
 constexpr int kKtbBlocks = 32;
+// kt per gate_up / down item of the single persistent launch: small items
+// where it is esc_moe_expert_path's own choice (H or I not a multiple of 512);
+// at the shapes that call runs as two launches, esc_moe_expert_path_one_launch
+// takes larger ones (config 3: 22.9 us per token-layer against 32.9 us with
+// the small items; KTB stays a divisor of I / 16 for every I it accepts)
+constexpr int kKtaOne = 8, kKtbOne = 4;
+constexpr int kKtaOneLarge = 16, kKtbOneLarge = 8;
 // waves per gate_up / block down item of one token-layer, and per block
 // down item of many token-layers
 constexpr int kGateUpWavesSingle = 16, kDownBlockWavesSingle = 16;
@@ -1285,15 +1292,22 @@ constexpr int kDownBlockWavesLayers = 4;
 // many bytes and the float data after it, so calls of different shapes on one
 // workspace never find another call's floats where their counters are (the
 // no-allocation variant; the caller checks n_int * 4 <= int_region).
+bool throughput_ok(int H, int I);
+
 FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput,
                      size_t int_region = 0) {
   // the two-launch path (throughput) uses the large items; the one-launch
-  // path the small ones (KTA = 8, KTB = 4), which spread one token-layer wide
+  // path the small ones (KTA = 8, KTB = 4), which spread one token-layer wide,
+  // or at two-launch shapes the middle ones (KTA = 16, KTB = 8)
   const bool large = throughput;
   const bool layers = large && L > 1;
-  const int kta = layers ? kKtaLayers : large ? kKtaSingle : 8;
+  const bool one_large = !large && throughput_ok(H, I);
+  const int kta = layers ? kKtaLayers : large ? kKtaSingle : one_large ? kKtaOneLarge : kKtaOne;
   const bool blocks = large && I == 16 * kKtbBlocks;
-  const int ktb = blocks ? kKtbBlocks : layers ? kKtbLayers : large ? kKtbSingle : 4;
+  const int ktb = blocks ? kKtbBlocks
+                  : layers ? kKtbLayers
+                  : large  ? kKtbSingle
+                  : one_large ? kKtbOneLarge : kKtbOne;
   FusedPlan f;
   f.L = L;
   f.M = T * top_k;
@@ -1382,8 +1396,13 @@ int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
     hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, kKtbSingle, false>), gb, blk, 0, s, p);
     return launched("k_moe_down_items");
   } else {
-    hipLaunchKernelGGL((esc::k_moe_fused<KG, KD, 8, 4, true>), dim3(grid),
-                       dim3(esc::kFusedThreads), 0, s, p);
+    // the plan's item size (fused_plan: large items at two-launch shapes)
+    if (p.H == 16 * kKtaOneLarge * p.NKC)
+      hipLaunchKernelGGL((esc::k_moe_fused<KG, KD, kKtaOneLarge, kKtbOneLarge, true>), dim3(grid),
+                         dim3(esc::kFusedThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((esc::k_moe_fused<KG, KD, kKtaOne, kKtbOne, true>), dim3(grid),
+                         dim3(esc::kFusedThreads), 0, s, p);
     return launched("k_moe_fused");
   }
 }
@@ -1510,7 +1529,16 @@ int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int
   ESC_REQUIRE(ws && host_flag, "null pointer");
   *host_flag = 0;
   // only the single persistent launch has a bounded wait
-  if (!fused_eligible(T, top_k, H, I) || throughput_ok(H, I)) return ESC_OK;
+  if (!fused_eligible(T, top_k, H, I)) return ESC_OK;
+  if (throughput_ok(H, I)) {
+    // esc_moe_expert_path runs two launches at this shape; a call through
+    // esc_moe_expert_path_one_launch reports a give-up through the
+    // device-wide flag (its workspace slot is not read: the same workspace
+    // may have served the two-launch plan, whose layout differs)
+    int* unused = nullptr;
+    if (take_wait_error(&unused) == ESC_ETIMEOUT) *host_flag = 1;
+    return ESC_OK;
+  }
   const FusedPlan f = fused_plan(1, T, top_k, H, I, false);
   ESC_REQUIRE(ws_bytes >= f.total, "workspace smaller than the plan");
   // the status slot (the last integer): read, then cleared for the next read
@@ -1542,7 +1570,7 @@ int moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, 
                     int E, int H, int I, const uint32_t* gu_code, const float* gu_rin,
                     const float* gu_rout, int K_gu, const uint32_t* dn_code, const float* dn_rin,
                     const float* dn_rout, int K_dn, int use_lut, uint16_t* y, void* ws,
-                    size_t ws_bytes, size_t int_region, void* stream) {
+                    size_t ws_bytes, size_t int_region, void* stream, bool one_launch = false) {
   ESC_REQUIRE(x && ids && scores && gu_code && gu_rin && gu_rout && dn_code && dn_rin && dn_rout &&
                   y,
               "null pointer");
@@ -1554,8 +1582,9 @@ int moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scores, 
   if (fused_eligible(T, top_k, H, I)) {
     // throughput_ok: two launches (gate_up items, down items + combine),
     // measured faster than the single persistent launch for one token-layer
-    // on gfx950; otherwise the single persistent launch
-    const bool two = throughput_ok(H, I);
+    // on gfx950; otherwise (or when the caller asks for it) the single
+    // persistent launch
+    const bool two = throughput_ok(H, I) && !one_launch;
     const FusedPlan f = fused_plan(1, T, top_k, H, I, two, int_region);
     // a fixed counter region keeps its last word for the status flag
     if (int_region && (size_t)f.n_int * 4 > int_region - 4)
@@ -1697,6 +1726,25 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
   if (int rc = ensure_wait_flag()) return rc;
   return moe_expert_path(x, ids, scores, T, top_k, E, H, I, gu_code, gu_rin, gu_rout, K_gu,
                          dn_code, dn_rin, dn_rout, K_dn, use_lut, y, ws, ws_bytes, 0, stream);
+}
+
+int esc_moe_expert_path_one_launch(const uint16_t* x, const int32_t* ids, const float* scores,
+                                   int T, int top_k, int E, int H, int I,
+                                   const uint32_t* gu_code, const float* gu_rin,
+                                   const float* gu_rout, int K_gu, const uint32_t* dn_code,
+                                   const float* dn_rin, const float* dn_rout, int K_dn,
+                                   int use_lut, uint16_t* y, void* ws, size_t ws_bytes,
+                                   void* stream) {
+  ESC_REQUIRE(T >= 0 && top_k >= 1 && H > 0 && I > 0, "bad sizes T=%d top_k=%d H=%d I=%d", T,
+              top_k, H, I);
+  ESC_REQUIRE(fused_eligible(T, top_k, H, I),
+              "one-launch expert path needs T*top_k <= %d, top_k <= 32, H a multiple of 256 "
+              "up to 7936 and I a multiple of 128 (got T=%d top_k=%d H=%d I=%d)",
+              kFusedMaxRows, T, top_k, H, I);
+  if (int rc = ensure_wait_flag()) return rc;
+  return moe_expert_path(x, ids, scores, T, top_k, E, H, I, gu_code, gu_rin, gu_rout, K_gu,
+                         dn_code, dn_rin, dn_rout, K_dn, use_lut, y, ws, ws_bytes, 0, stream,
+                         true);
 }
 
 size_t esc_moe_expert_path_static_max(void) { return kStaticScratchBytes; }

@@ -407,8 +407,10 @@ def moe_expert_path_workspace(T: int, top_k: int, E: int, H: int, I: int) -> int
 
 
 def moe_expert_path(x, ids, scores, gu_code, gu_rin, gu_rout, K_gu, dn_code, dn_rin, dn_rout,
-                    K_dn, lut=None, ws=None, out=None):
-    """Routed experts for T tokens -> f16 [T, H] (models/qwen3_5_moe.py:207-253)."""
+                    K_dn, lut=None, ws=None, out=None, one_launch=False):
+    """Routed experts for T tokens -> f16 [T, H] (models/qwen3_5_moe.py:207-253).
+    one_launch: the whole path as one persistent launch (esc_moe_expert_path_one_launch)
+    where the default takes two."""
     _dev(x, ids, scores, gu_code, gu_rin, gu_rout, dn_code, dn_rin, dn_rout)
     t, h = x.shape
     k = ids.shape[1]
@@ -422,7 +424,8 @@ def moe_expert_path(x, ids, scores, gu_code, gu_rin, gu_rout, K_gu, dn_code, dn_
         # them zero, so a workspace is reusable for calls of the same shape
         ws = torch.zeros(max(nbytes, 4), dtype=torch.uint8, device=x.device)
     y = out if out is not None else torch.empty((t, h), dtype=torch.float16, device=x.device)
-    _lib.call("esc_moe_expert_path", _ptr(x), _ptr(ids), _ptr(scores), t, k, E, h, I,
+    _lib.call("esc_moe_expert_path_one_launch" if one_launch else "esc_moe_expert_path",
+              _ptr(x), _ptr(ids), _ptr(scores), t, k, E, h, I,
               _ptr(_as_u32(gu_code)), _ptr(gu_rin), _ptr(gu_rout), K_gu,
               _ptr(_as_u32(dn_code)), _ptr(dn_rin), _ptr(dn_rout), K_dn, _lut_flag(lut),
               _ptr(y), _ptr(ws), ws.numel(), _stream())

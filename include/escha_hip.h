@@ -155,7 +155,8 @@ int esc_gemm_mfma_out(const uint16_t* xh, const uint32_t* code, const float* rou
  * sums the partials in fixed order and output-transforms.
  * M >= 16: input transform, then esc_gemm_mfma_out.  ws: esc_linear_workspace bytes, zero-filled before its
  * first use (its counters are left zero after every call); calls sharing one
- * ws must not overlap.  Tolerance contract (reassociated float32 sum);
+ * ws must not overlap, and a ws moved to another shape is zero-filled again
+ * (each shape's plan puts its counters where another's partials may lie).  Tolerance contract (reassociated float32 sum);
  * decoded weights bit-exact.
  * Replaces EschaLinear.__call__ (escha_mlx/dense.py:337-362). */
 size_t esc_linear_workspace(int M, int K, int IC, int OC);
@@ -282,7 +283,9 @@ int esc_q8_embed(const int32_t* ids, int T, const int8_t* w8, const float* scale
  * Tolerance contract (reassociated GEMV sums; decode bit-exact).  ws:
  * esc_moe_expert_path_workspace bytes, zero-filled before its first use (the
  * counters it holds are left zero by every call); calls sharing one ws must
- * not overlap.  Shapes that run as one persistent launch (H or I not a
+ * not overlap, and a ws moved to another shape, or between this entry point
+ * and esc_moe_expert_path_one_launch, is zero-filled again (each plan puts its
+ * counters where another's partials may lie).  Shapes that run as one persistent launch (H or I not a
  * multiple of 512) hand work between workgroups with bounded waits: a
  * workgroup that gives up writes NaN outputs and raises a device-wide flag,
  * and the next call on the device that would take that launch returns
@@ -299,6 +302,25 @@ int esc_moe_expert_path(const uint16_t* x, const int32_t* ids, const float* scor
                         const uint32_t* dn_code, const float* dn_rin, const float* dn_rout,
                         int K_dn, int use_lut, uint16_t* y, void* ws, size_t ws_bytes,
                         void* stream);
+
+/* esc_moe_expert_path as one persistent launch at every shape it takes
+ * (T*top_k <= 64, top_k <= 32, H a multiple of 256 up to 7936, I a multiple
+ * of 128; others return ESC_EINVAL): gate_up items, the SwiGLU hand-off,
+ * down items and the slot combine in one dispatch, handing work between
+ * workgroups with the bounded waits described above.  Same arguments,
+ * workspace, outputs and tolerance contract as esc_moe_expert_path, which
+ * takes this launch by itself only where H or I is not a multiple of 512 (at
+ * the others two launches measured faster on MI355X).  No counterpart in the
+ * reference as a separate call: it is the one-launch walk of the selected
+ * experts' gate/up/down stacks, for callers that want one dispatch per
+ * token-layer. */
+int esc_moe_expert_path_one_launch(const uint16_t* x, const int32_t* ids, const float* scores,
+                                   int T, int top_k, int E, int H, int I,
+                                   const uint32_t* gu_code, const float* gu_rin,
+                                   const float* gu_rout, int K_gu, const uint32_t* dn_code,
+                                   const float* dn_rin, const float* dn_rout, int K_dn,
+                                   int use_lut, uint16_t* y, void* ws, size_t ws_bytes,
+                                   void* stream);
 
 /* esc_moe_expert_path without allocation: the same computation and outputs
  * (the same kernels), with its scratch (partials, counters, down inputs) in a
@@ -358,7 +380,10 @@ int esc_moe_expert_path_layers(const esc_moe_layer* layers, int L, int T, int to
  * since the flags were last read (never expected: the kernel's work claiming
  * guarantees progress; the outputs of an item that gave up are NaN, never
  * stale values).  Reading clears both flags, so the next esc_moe_expert_path
- * call does not also return ESC_ETIMEOUT for it.  Synchronises the stream.
+ * call does not also return ESC_ETIMEOUT for it.  At shapes that
+ * esc_moe_expert_path runs as two launches (H and I multiples of 512), only
+ * the device-wide flag is read (a run of esc_moe_expert_path_one_launch sets
+ * it).  Synchronises the stream.
  * No counterpart in the reference (its expert path has no cross-workgroup
  * hand-off). */
 int esc_moe_status(const void* ws, size_t ws_bytes, int T, int top_k, int H, int I,

@@ -87,6 +87,18 @@ def test_rejects_groups_below_bound():
     assert rc == _lib.ESC_EINVAL and "bound" in msg
 
 
+def test_one_launch_expert_path_rejects_shapes_it_does_not_take():
+    # 16 tokens x top-8 = 128 routed rows: above the one-launch path's 64
+    args = (DUMMY, DUMMY, DUMMY, 16, 8, 256, 2048, 512, DUMMY, DUMMY, DUMMY, 2, DUMMY, DUMMY, DUMMY,
+            2, 0, DUMMY, DUMMY, 1 << 30, None)
+    rc, msg = _rc_msg("esc_moe_expert_path_one_launch", *args)
+    assert rc == _lib.ESC_EINVAL and "T*top_k <= 64" in msg and "T=16" in msg
+    # H = 2176 is not a multiple of 256
+    args = (DUMMY, DUMMY, DUMMY, 1, 8, 256, 2176, 512) + args[8:]
+    rc, msg = _rc_msg("esc_moe_expert_path_one_launch", *args)
+    assert rc == _lib.ESC_EINVAL and "H=2176" in msg
+
+
 def test_workspace_sizes_are_positive():
     lib = _lib.load()
     assert lib.esc_gemv_fast_workspace(8, 2, 2048, 1024) > 0

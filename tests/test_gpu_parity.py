@@ -494,6 +494,38 @@ def test_moe_one_launch_status_and_reuse(monkeypatch):
     assert ops().moe_status(ws, 1, k, H, I) == 0
 
 
+@pytest.mark.parametrize("E,H,I,K_gu,K_dn,T,k", [(256, 2048, 512, 2, 2, 1, 8),
+                                                  (256, 2048, 512, 2, 2, 4, 8),
+                                                  (64, 1024, 512, 2, 3, 8, 8)])
+def test_moe_one_launch_entry_vs_oracle(E, H, I, K_gu, K_dn, T, k):
+    """esc_moe_expert_path_one_launch at shapes the default runs as two
+    launches (config 3's among them, and 64 routed rows, the most it takes):
+    against the oracle, beside the two-launch default, bit-identical on repeat
+    on one workspace (its counters left zero), and no bounded wait given up."""
+    c = _moe_case(E, H, I, K_gu, K_dn, T, k, 5 * T + K_dn)
+    o = ops()
+    ids, sc = o.route_topk(torch.from_numpy(c["logits"]).to(DEV), k)
+    x = torch.from_numpy(c["x"]).to(DEV)
+    args = (x, ids, sc, dcode(c["gu_code"]), torch.from_numpy(c["gu_rin"]).to(DEV),
+            torch.from_numpy(c["gu_rout"]).to(DEV), K_gu, dcode(c["dn_code"]),
+            torch.from_numpy(c["dn_rin"]).to(DEV), torch.from_numpy(c["dn_rout"]).to(DEV), K_dn)
+    ws = torch.zeros(o.moe_expert_path_workspace(T, k, E, H, I), dtype=torch.uint8, device=DEV)
+    one = o.moe_expert_path(*args, ws=ws, one_launch=True)
+    first = bits16(one)
+    for _ in range(3):
+        assert np.array_equal(bits16(o.moe_expert_path(*args, ws=ws, one_launch=True)), first)
+    assert o.moe_status(ws, T, k, H, I) == 0
+    # the two-launch default on a workspace of its own (the plans differ)
+    two = o.moe_expert_path(*args).cpu().numpy().astype(np.float32)
+    ids_np, sc_np = ids.cpu().numpy(), sc.cpu().numpy()
+    want = _oracle_moe(c, ids_np, sc_np, E, H, I, K_gu, K_dn, np.unique(ids_np)).astype(np.float32)
+    scale = np.abs(want).max()
+    got = one.cpu().numpy().astype(np.float32)
+    assert np.isfinite(got).all()
+    assert np.abs(got - want).max() / scale < 5e-3
+    assert np.abs(two - want).max() / scale < 5e-3
+
+
 def test_moe_one_launch_gave_up_wait_is_reported(monkeypatch):
     """Failure reporting of the one persistent launch, forced from the host:
     with a spin limit of 0 every down item's wait gives up at once (no wait
