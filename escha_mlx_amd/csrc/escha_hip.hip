@@ -1314,7 +1314,10 @@ FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput,
   f.NB = I / 128;
   f.NKC = std::max(1, H / (16 * kta));
   f.NKB = std::max(1, I / (16 * ktb));
-  f.NCP = ktb == kKtbBlocks ? H / 128 : H / 256;
+  // 128-column blocks for the block kernels, 256-column pairs for every
+  // other down item (k_moe_down_items, k_moe_fused): keyed on the kernel the
+  // plan is for, not on the item's kt count
+  f.NCP = blocks ? H / 128 : H / 256;
   f.nA = f.M * f.NB * f.NKC;
   f.nB = f.M * f.NCP * f.NKB;
   f.grid = throughput ? std::min(L * std::max(f.nA, f.nB), 1024)
@@ -1396,6 +1399,8 @@ int launch_fused_k(const esc::FusedMoe& p, int grid, hipStream_t s) {
     hipLaunchKernelGGL((esc::k_moe_down_items<KG, KD, kKtbSingle, false>), gb, blk, 0, s, p);
     return launched("k_moe_down_items");
   } else {
+    // k_moe_fused's down items are 256-column pairs (16 tiles each)
+    ESC_REQUIRE(p.NCP * 256 == p.H, "one-launch plan with %d column groups for H=%d", p.NCP, p.H);
     // the plan's item size (fused_plan: large items at two-launch shapes)
     if (p.H == 16 * kKtaOneLarge * p.NKC)
       hipLaunchKernelGGL((esc::k_moe_fused<KG, KD, kKtaOneLarge, kKtbOneLarge, true>), dim3(grid),
