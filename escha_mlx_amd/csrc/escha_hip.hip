@@ -1278,11 +1278,12 @@ constexpr int kKtaSingle = 16, kKtbSingle = 16;
 constexpr int kKtbBlocks = 32;
 // kt per gate_up / down item of the single persistent launch: small items
 // where it is esc_moe_expert_path's own choice (H or I not a multiple of 512);
-// at the shapes that call runs as two launches, esc_moe_expert_path_one_launch
-// takes larger ones (config 3: 22.9 us per token-layer against 32.9 us with
-// the small items; KTB stays a divisor of I / 16 for every I it accepts)
+// at the shapes that call runs as two launches (H and I multiples of 512),
+// esc_moe_expert_path_one_launch takes larger ones (config 3: 22.3 us per
+// token-layer against 32.9 us with the small items, 22.7-22.9 us with 16 and
+// 8 kt, 24.5-28.0 us with 32 kt gate_up items)
 constexpr int kKtaOne = 8, kKtbOne = 4;
-constexpr int kKtaOneLarge = 16, kKtbOneLarge = 8;
+constexpr int kKtaOneLarge = 16, kKtbOneLarge = 16;
 // waves per gate_up / block down item of one token-layer, and per block
 // down item of many token-layers
 constexpr int kGateUpWavesSingle = 16, kDownBlockWavesSingle = 16;
@@ -1298,7 +1299,7 @@ FusedPlan fused_plan(int L, int T, int top_k, int H, int I, bool throughput,
                      size_t int_region = 0) {
   // the two-launch path (throughput) uses the large items; the one-launch
   // path the small ones (KTA = 8, KTB = 4), which spread one token-layer wide,
-  // or at two-launch shapes the middle ones (KTA = 16, KTB = 8)
+  // or at two-launch shapes the middle ones (KTA = KTB = 16)
   const bool large = throughput;
   const bool layers = large && L > 1;
   const bool one_large = !large && throughput_ok(H, I);
