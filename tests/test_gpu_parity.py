@@ -562,6 +562,40 @@ def test_moe_one_launch_gave_up_wait_is_reported(monkeypatch):
         assert ops().moe_status(ws, 1, k, H, I) == 0
 
 
+def test_moe_one_launch_entry_gave_up_wait_is_reported():
+    """The same failure reporting for esc_moe_expert_path_one_launch at a shape
+    the default runs as two launches, forced from the host (spin limit 0: the
+    kernel still reaches its end): NaN outputs, then either the next one-launch
+    call raises EschaWaitTimeout without running or esc_moe_status reports the
+    device-wide flag once; the call after that matches the good output."""
+    from escha_mlx_amd import _lib
+    E, H, I, k = 64, 1024, 512, 8
+    c = _moe_case(E, H, I, 2, 2, 1, k, 17)
+    o = ops()
+    ids, sc = o.route_topk(torch.from_numpy(c["logits"]).to(DEV), k)
+    x = torch.from_numpy(c["x"]).to(DEV)
+    args = (x, ids, sc, dcode(c["gu_code"]), torch.from_numpy(c["gu_rin"]).to(DEV),
+            torch.from_numpy(c["gu_rout"]).to(DEV), 2, dcode(c["dn_code"]),
+            torch.from_numpy(c["dn_rin"]).to(DEV), torch.from_numpy(c["dn_rout"]).to(DEV), 2)
+    ws = torch.zeros(o.moe_expert_path_workspace(1, k, E, H, I), dtype=torch.uint8, device=DEV)
+    good = bits16(o.moe_expert_path(*args, ws=ws, one_launch=True))
+    assert not np.isnan(good.view(np.float16)).any()
+    for via_status in (False, True):
+        o.set_moe_spin_limit(0)
+        try:
+            bad = o.moe_expert_path(*args, ws=ws, one_launch=True).float().cpu()
+        finally:
+            o.set_moe_spin_limit(-1)
+        assert torch.isnan(bad).any()
+        if via_status:
+            assert o.moe_status(ws, 1, k, H, I) == 1
+        else:
+            with pytest.raises(_lib.EschaWaitTimeout, match="bounded wait"):
+                o.moe_expert_path(*args, ws=ws, one_launch=True)
+        assert np.array_equal(bits16(o.moe_expert_path(*args, ws=ws, one_launch=True)), good)
+        assert o.moe_status(ws, 1, k, H, I) == 0
+
+
 @pytest.mark.parametrize("K_gu,K_dn,I", [(2, 2, 512), (2, 3, 512), (3, 3, 512), (3, 2, 1024)])
 def test_moe_layers_one_launch_vs_oracle(K_gu, K_dn, I):
     """Independent token-layers in one launch (throughput mode): every layer's
