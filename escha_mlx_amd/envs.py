@@ -82,6 +82,12 @@ def use_exact() -> bool:
     return parse_bool("ESCHA_HIP_EXACT", False)
 
 
+def moe_one_launch() -> bool:
+    """ESCHA_HIP_MOE_ONE_LAUNCH: the routed-expert path as one launch
+    (esc_moe_expert_path_one_launch) wherever that launch takes the shape."""
+    return parse_bool("ESCHA_HIP_MOE_ONE_LAUNCH", False)
+
+
 def dense_mat() -> bool:
     return parse_bool("ESCHA_MLX_DENSE_MAT", True)
 

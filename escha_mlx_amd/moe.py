@@ -105,6 +105,7 @@ class EschaMoEExperts(torch.nn.Module):
         self._inter = dn.IC
         self._lut = envs.use_lut()
         self._exact = envs.use_exact()
+        self._one_launch = envs.moe_one_launch()
         self._fused_had = envs.fused_had()
         self._block_r = envs.block_r_pin()
         envs.kt_block()  # validated like the reference's; no code tiles are staged here
@@ -168,16 +169,19 @@ class EschaMoEExperts(torch.nn.Module):
             # the GEMVs (models/qwen3_5_moe.py:103-122), the staged chain
             return self._forward_staged(x, ids, scores)
         t, h = x.shape
-        # one zero-initialised workspace per token count: the one-launch path
-        # keeps its counters there and leaves them zero after every call
-        key = (t, x.device)
+        # ESCHA_HIP_MOE_ONE_LAUNCH: one launch wherever that launch takes the shape
+        one = self._one_launch and ops.moe_one_launch_takes(t, self.top_k, h, self._inter)
+        # one zero-initialised workspace per token count and form: the one-launch
+        # path keeps its counters there and leaves them zero after every call,
+        # and the two forms lay their counters out differently
+        key = (t, x.device, one)
         ws = self._ws.get(key)
         if ws is None:
             need = ops.moe_expert_path_workspace(t, self.top_k, self.num_experts, h, self._inter)
             ws = self._ws[key] = torch.zeros(max(need, 4), dtype=torch.uint8, device=x.device)
         gu, dn = self._gu, self._dn
         return ops.moe_expert_path(x, ids, scores, gu.code, gu.rin, gu.rout, gu.K, dn.code,
-                                   dn.rin, dn.rout, dn.K, lut=self._lut, ws=ws)
+                                   dn.rin, dn.rout, dn.K, lut=self._lut, ws=ws, one_launch=one)
 
 
 class EschaSparseMoeBlock(torch.nn.Module):

@@ -406,6 +406,12 @@ def moe_expert_path_workspace(T: int, top_k: int, E: int, H: int, I: int) -> int
     return int(_lib.load().esc_moe_expert_path_workspace(T, top_k, E, H, I))
 
 
+def moe_one_launch_takes(T: int, top_k: int, H: int, I: int) -> bool:
+    """Whether esc_moe_expert_path_one_launch takes this shape (up to 64 routed
+    rows, top_k <= 32, H a multiple of 256 up to 7936, I a multiple of 128)."""
+    return T * top_k <= 64 and top_k <= 32 and H % 256 == 0 and H <= 7936 and I % 128 == 0
+
+
 def moe_expert_path(x, ids, scores, gu_code, gu_rin, gu_rout, K_gu, dn_code, dn_rin, dn_rout,
                     K_dn, lut=None, ws=None, out=None, one_launch=False):
     """Routed experts for T tokens -> f16 [T, H] (models/qwen3_5_moe.py:207-253).

@@ -99,6 +99,20 @@ def test_one_launch_expert_path_rejects_shapes_it_does_not_take():
     assert rc == _lib.ESC_EINVAL and "H=2176" in msg
 
 
+def test_one_launch_shape_rule_matches_the_library():
+    # the Python rule the module uses to pick the one-launch form, against the
+    # library's own rejection on every side of each bound
+    from escha_mlx_amd import ops as o
+    for T, k, H, I in [(8, 8, 2048, 512), (9, 8, 2048, 512), (1, 8, 7936 + 256, 512),
+                       (1, 8, 2176, 512), (1, 8, 2048, 640), (1, 8, 2048, 576), (1, 33, 2048, 512),
+                       (2, 32, 1024, 128)]:
+        args = (DUMMY, DUMMY, DUMMY, T, k, 256, H, I, DUMMY, DUMMY, DUMMY, 2, DUMMY, DUMMY,
+                DUMMY, 2, 0, DUMMY, DUMMY, 0, None)
+        rc, msg = _rc_msg("esc_moe_expert_path_one_launch", *args)
+        rejected = rc == _lib.ESC_EINVAL and "one-launch" in msg
+        assert rejected == (not o.moe_one_launch_takes(T, k, H, I)), (T, k, H, I, rc, msg)
+
+
 def test_workspace_sizes_are_positive():
     lib = _lib.load()
     assert lib.esc_gemv_fast_workspace(8, 2, 2048, 1024) > 0
@@ -265,7 +279,8 @@ def test_env_validation(monkeypatch):
 @pytest.mark.parametrize("name,fn,default", [
     ("ESCHA_MLX_LUT", envs.use_lut, False), ("ESCHA_MLX_FUSED_HAD", envs.fused_had, True),
     ("ESCHA_HIP_EXACT", envs.use_exact, False), ("ESCHA_MLX_DENSE_MAT", envs.dense_mat, True),
-    ("ESCHA_MLX_BIAS", dense.apply_bias, False)])
+    ("ESCHA_MLX_BIAS", dense.apply_bias, False),
+    ("ESCHA_HIP_MOE_ONE_LAUNCH", envs.moe_one_launch, False)])
 def test_bool_knobs_take_reference_spellings(monkeypatch, name, fn, default, raw, want):
     """Every boolean knob accepts the reference's spellings, blanks and case
     ignored (escha_mlx/envs.py:89-95); empty means the default."""

@@ -490,7 +490,7 @@ def test_moe_one_launch_status_and_reuse(monkeypatch):
     first = bits16(blk(x, ids, sc))
     for _ in range(4):
         assert np.array_equal(bits16(blk(x, ids, sc)), first)
-    ws = blk._ws[(1, x.device)]
+    ws = blk._ws[(1, x.device, False)]
     assert ops().moe_status(ws, 1, k, H, I) == 0
 
 
@@ -542,7 +542,7 @@ def test_moe_one_launch_gave_up_wait_is_reported(monkeypatch):
     x = torch.from_numpy(c["x"]).to(DEV)
     good = bits16(blk(x, ids, sc))
     assert not np.isnan(good.view(np.float16)).any()
-    ws = blk._ws[(1, x.device)]
+    ws = blk._ws[(1, x.device, False)]
     for via_status in (False, True):
         ops().set_moe_spin_limit(0)
         try:
@@ -560,6 +560,28 @@ def test_moe_one_launch_gave_up_wait_is_reported(monkeypatch):
         if not via_status:
             assert ops().moe_status(ws, 1, k, H, I) == 1
         assert ops().moe_status(ws, 1, k, H, I) == 0
+
+
+def test_moe_module_one_launch_knob(monkeypatch):
+    """ESCHA_HIP_MOE_ONE_LAUNCH=1: EschaMoEExperts takes the one-launch entry
+    where it takes the shape (bit-identical to calling it directly) and the
+    default elsewhere (above 64 routed rows)."""
+    E, H, I, k = 64, 1024, 512, 8
+    monkeypatch.setenv("ESCHA_HIP_MOE_ONE_LAUNCH", "1")
+    for T in (2, 12):
+        c = _moe_case(E, H, I, 2, 2, T, k, 31 + T)
+        blk = _block(c, E, k, 2, 2, monkeypatch, exact=False)
+        assert blk._one_launch
+        ids, sc = ops().route_topk(torch.from_numpy(c["logits"]).to(DEV), k)
+        x = torch.from_numpy(c["x"]).to(DEV)
+        got = bits16(blk(x, ids, sc))
+        one = T * k <= 64
+        assert ops().moe_one_launch_takes(T, k, H, I) == one
+        args = (x, ids, sc, dcode(c["gu_code"]), torch.from_numpy(c["gu_rin"]).to(DEV),
+                torch.from_numpy(c["gu_rout"]).to(DEV), 2, dcode(c["dn_code"]),
+                torch.from_numpy(c["dn_rin"]).to(DEV), torch.from_numpy(c["dn_rout"]).to(DEV), 2)
+        want = bits16(ops().moe_expert_path(*args, one_launch=one))
+        assert np.array_equal(got, want), T
 
 
 def test_moe_one_launch_entry_gave_up_wait_is_reported():
